@@ -1,0 +1,425 @@
+// FP32 column-major NN SGEMM for CDNA4 (gfx950): D = alpha * A * B + beta * C.
+//
+// One translation unit per tuned configuration.  The generator compiles this
+// file with `hipcc --cuda-device-only -c --offload-arch=gfx950 -DSG_...=<value>` and the
+// resulting code object exports one kernel, `generated_gemm`, whose explicit
+// kernel arguments are laid out byte-for-byte like the reference emitter's
+// (generator.py:2604-2620, packed by generator_runner.cpp:132-148):
+//
+//   offset  0 a   8 b   16 c   24 d          (global float pointers)
+//   offset 32 m  36 n   40 k   44 lda  48 ldb  52 ldc  56 ldd   (uint32)
+//   offset 60 alpha     64 beta                 (float)
+//   offset 68 numWorkgroupX  72 numWorkgroupY   (int32)      -> 76 B, padded to 80
+//
+// Launch: grid = (numWorkgroupX, numWorkgroupY) workgroups of
+// SG_WG0 * SG_WG1 * 64 work-items; all LDS is static (the runner passes 0 B of
+// dynamic LDS, generator_runner.cpp:189).  numWorkgroupX = ceil(m / MT0),
+// numWorkgroupY = ceil(n / MT1) with MT0 = atom_m * WG0 * WT0 and
+// MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  The kernel needs
+// m % MT0 == 0, n % MT1 == 0, k % DK == 0 and lda/ldb/ldc/ldd % 4 == 0; the
+// host side (shim, runner) checks this before every launch.
+//
+// Data path per K tile of depth DK:
+//   HBM --global_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
+//   LDS --ds_read_b{32,64,128}--> VGPR --v_mfma_f32_{32x32x2,16x16x4}_f32--> accumulators
+// and after the K loop accumulators --(alpha, beta)--> global_store_dwordx{1,2,4}.
+//
+// LDS layouts (floats):
+//   A tile: [DK][MT0 + PAD_A]  -- one k per row, m contiguous; written straight
+//           from the column-major global rows (coalesced, conflict-free).
+//   B tile: [MT1][DK + PAD_B]  -- one n per row, k contiguous; written straight
+//           from the column-major global columns.
+//
+// K permutation.  An MFMA atom with atom_k = 2 (32x32x2) or 4 (16x16x4) feeds
+// lane group g = lane / atom_m one k value.  Any bijection between the k values
+// of a block and (MFMA step j, lane group g) gives the same sum as long as A and
+// B use the same one, so within a block of KB = atom_k * KPL values lane group g
+// takes k = block + g * KPL + j at step j (j < KPL).  A lane then reads KPL
+// consecutive k of one B column with a single ds_read_b128 (KPL = 4).
+//
+// M interleave.  Atom i of a wave's WT0 atoms along M owns the rows
+// wave_row + r * WT0 + i (r < atom_m), so one lane's A operands for the WT0
+// atoms at one k are WT0 consecutive floats in an LDS row: one ds_read_b128
+// for WT0 = 4.  The same interleave makes the epilogue's WT0 values per
+// accumulator slot consecutive rows of D, stored with one dwordx4 per slot.
+//
+// Work-group order.  Tiles are first spread so that each of the 8 XCDs (which
+// receive work-groups round-robin by linear id) owns a contiguous range of
+// logical tiles (SG_XCD), then grouped SG_WGM tiles wide along M
+// (generator.py:1437-1464 semantics, extended to a partial last group), and
+// the starting K tile can be rotated by (tile_x & (SG_MAPK - 1))
+// (generator.py:1506-1514, :1724-1744).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifndef SG_ATOM_M
+#define SG_ATOM_M 32
+#endif
+#ifndef SG_WG0
+#define SG_WG0 2
+#endif
+#ifndef SG_WG1
+#define SG_WG1 2
+#endif
+#ifndef SG_WT0
+#define SG_WT0 4
+#endif
+#ifndef SG_WT1
+#define SG_WT1 4
+#endif
+#ifndef SG_DK
+#define SG_DK 16
+#endif
+#ifndef SG_NBUF
+#define SG_NBUF 2
+#endif
+#ifndef SG_WGM
+#define SG_WGM 1
+#endif
+#ifndef SG_XCD
+#define SG_XCD 0
+#endif
+#ifndef SG_MAPK
+#define SG_MAPK 0
+#endif
+#ifndef SG_PLR
+#define SG_PLR 1
+#endif
+#ifndef SG_GW
+#define SG_GW 0
+#endif
+#ifndef SG_PAD_A
+#define SG_PAD_A 0
+#endif
+#ifndef SG_PAD_B
+#define SG_PAD_B 4
+#endif
+#ifndef SG_KERNEL_NAME
+#define SG_KERNEL_NAME generated_gemm
+#endif
+
+namespace sg {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int N> struct Vec;
+template <> struct Vec<1> { typedef float type; };
+template <> struct Vec<2> { typedef f32x2 type; };
+template <> struct Vec<4> { typedef f32x4 type; };
+
+template <int AM> struct Atom;
+
+// v_mfma_f32_32x32x2_f32: lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32];
+// accumulator slot q of lane l holds D[(q % 4) + 8 * (q / 4) + 4 * (l / 32)][l % 32].
+template <> struct Atom<32> {
+    static constexpr int M = 32, N = 32, K = 2, ACC = 16;
+    typedef f32x16 acc_t;
+    __device__ static __forceinline__ acc_t mfma(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ int row(int q, int lane) {
+        return (q & 3) + 8 * (q >> 2) + 4 * (lane >> 5);
+    }
+};
+
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// accumulator slot q of lane l holds D[q + 4 * (l / 16)][l % 16].
+template <> struct Atom<16> {
+    static constexpr int M = 16, N = 16, K = 4, ACC = 4;
+    typedef f32x4 acc_t;
+    __device__ static __forceinline__ acc_t mfma(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    __device__ static __forceinline__ int row(int q, int lane) { return q + 4 * (lane >> 4); }
+};
+
+template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B>
+struct Geometry {
+    typedef Atom<AM> atom;
+    static constexpr int NT = WG0 * WG1 * 64;
+    static constexpr int MT0 = atom::M * WG0 * WT0;
+    static constexpr int MT1 = atom::N * WG1 * WT1;
+    // k values a lane reads per LDS read of B (and MFMA steps per k block)
+    static constexpr int KPL = (DK / atom::K >= 4) ? 4 : ((DK / atom::K >= 2) ? 2 : 1);
+    static constexpr int KB = atom::K * KPL;
+    static constexpr int A_LD = MT0 + PAD_A;  // LDS row stride of the A tile (floats)
+    static constexpr int B_LD = DK + PAD_B;   // LDS row stride of the B tile (floats)
+    static constexpr int A_STAGE = DK * A_LD;
+    static constexpr int B_STAGE = MT1 * B_LD;
+    static constexpr int STAGE = A_STAGE + B_STAGE;
+    static constexpr int LDS_FLOATS = NBUF * STAGE;
+    // float4 chunks each thread moves per K tile
+    static constexpr int A_CHUNKS = MT0 * DK / 4;
+    static constexpr int B_CHUNKS = MT1 * DK / 4;
+    static constexpr int LA = (A_CHUNKS + NT - 1) / NT;
+    static constexpr int LB = (B_CHUNKS + NT - 1) / NT;
+
+    static_assert(DK % 4 == 0, "DK must be a multiple of 4");
+    static_assert(DK % KB == 0, "DK must be a multiple of the k block");
+    static_assert(MT0 % 4 == 0, "MT0 must be a multiple of 4");
+    static_assert(WT0 == 1 || WT0 == 2 || WT0 == 4 || WT0 == 8, "WT0 must be 1, 2, 4 or 8");
+    static_assert(WT1 >= 1 && WT1 <= 8, "WT1 must be in [1, 8]");
+    static_assert(PAD_A % 4 == 0 && PAD_B % 4 == 0, "LDS pads keep 16-byte rows");
+    static_assert(NBUF >= 2, "at least two LDS buffers");
+    static_assert(LDS_FLOATS * 4 <= 163840, "LDS tile exceeds the 160 KiB of a gfx950 CU");
+};
+
+typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B> G;
+
+// Reads WT0 consecutive floats (the A operands of the WT0 interleaved atoms).
+template <int W> __device__ __forceinline__ void lds_read_row(const float* p, float (&out)[W]) {
+    if constexpr (W == 1) {
+        out[0] = p[0];
+    } else if constexpr (W == 2) {
+        f32x2 v = *reinterpret_cast<const f32x2*>(p);
+        out[0] = v.x; out[1] = v.y;
+    } else {
+#pragma unroll
+        for (int h = 0; h < W / 4; ++h) {
+            f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * h);
+            out[4 * h + 0] = v.x; out[4 * h + 1] = v.y; out[4 * h + 2] = v.z; out[4 * h + 3] = v.w;
+        }
+    }
+}
+
+template <int W> __device__ __forceinline__ void global_store_row(float* p, const float (&v)[W]) {
+    if constexpr (W == 1) {
+        p[0] = v[0];
+    } else if constexpr (W == 2) {
+        f32x2 t; t.x = v[0]; t.y = v[1];
+        *reinterpret_cast<f32x2*>(p) = t;
+    } else {
+#pragma unroll
+        for (int h = 0; h < W / 4; ++h) {
+            f32x4 t; t.x = v[4 * h]; t.y = v[4 * h + 1]; t.z = v[4 * h + 2]; t.w = v[4 * h + 3];
+            *reinterpret_cast<f32x4*>(p + 4 * h) = t;
+        }
+    }
+}
+
+template <int W> __device__ __forceinline__ void global_load_row(const float* p, float (&v)[W]) {
+    if constexpr (W == 1) {
+        v[0] = p[0];
+    } else if constexpr (W == 2) {
+        f32x2 t = *reinterpret_cast<const f32x2*>(p);
+        v[0] = t.x; v[1] = t.y;
+    } else {
+#pragma unroll
+        for (int h = 0; h < W / 4; ++h) {
+            f32x4 t = *reinterpret_cast<const f32x4*>(p + 4 * h);
+            v[4 * h] = t.x; v[4 * h + 1] = t.y; v[4 * h + 2] = t.z; v[4 * h + 3] = t.w;
+        }
+    }
+}
+
+// Maps the hardware work-group id to the logical (tile_x, tile_y).
+__device__ __forceinline__ void tile_coords(int bx, int by, int nwgx, int nwgy, int& tx, int& ty) {
+    int z = bx + by * nwgx;
+    const int total = nwgx * nwgy;
+    if constexpr (SG_XCD > 1) {
+        // Work-group z runs on XCD z % SG_XCD; give each XCD a contiguous range.
+        if (total % SG_XCD == 0) z = (z % SG_XCD) * (total / SG_XCD) + z / SG_XCD;
+    }
+    if constexpr (SG_WGM > 1) {
+        const int span = SG_WGM * nwgy;
+        const int group = z / span;
+        const int first_x = group * SG_WGM;
+        const int rem = nwgx - first_x;
+        const int width = rem < SG_WGM ? rem : SG_WGM;
+        const int in_group = z - group * span;
+        tx = first_x + in_group % width;
+        ty = in_group / width;
+    } else {
+        tx = z % nwgx;
+        ty = z / nwgx;
+    }
+}
+
+}  // namespace sg
+
+extern "C" __global__ void __launch_bounds__(sg::G::NT)
+SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
+               const float* __restrict__ c, float* __restrict__ d,
+               uint32_t m, uint32_t n, uint32_t k,
+               uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+               float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY) {
+    using namespace sg;
+    typedef G::atom AT;
+    typedef AT::acc_t acc_t;
+    constexpr int NT = G::NT, MT0 = G::MT0, MT1 = G::MT1, DK = SG_DK, NBUF = SG_NBUF;
+    constexpr int WT0 = SG_WT0, WT1 = SG_WT1, KPL = G::KPL, KB = G::KB;
+
+    __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % SG_WG0;
+    const int wn = wave / SG_WG0;
+
+    int tx, ty;
+    tile_coords(blockIdx.x, blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
+    const uint32_t row0 = (uint32_t)tx * MT0;
+    const uint32_t col0 = (uint32_t)ty * MT1;
+    const int ktiles = (int)(k / DK);
+
+    // ---- global -> VGPR staging addresses (element offsets, 64-bit bases) ----
+    const float* a_tile = a + row0;                      // + kt * DK * lda
+    const float* b_tile = b + (size_t)col0 * ldb;        // + kt * DK
+    uint32_t a_off[G::LA], b_off[G::LB];
+    int a_lds[G::LA], b_lds[G::LB];
+#pragma unroll
+    for (int i = 0; i < G::LA; ++i) {
+        const int ch = tid + i * NT;
+        const int mc = ch % (MT0 / 4), kc = ch / (MT0 / 4);
+        a_off[i] = (uint32_t)(mc * 4) + (uint32_t)kc * lda;
+        a_lds[i] = kc * G::A_LD + mc * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < G::LB; ++i) {
+        const int ch = tid + i * NT;
+        const int kc = ch % (DK / 4), nc = ch / (DK / 4);
+        b_off[i] = (uint32_t)(kc * 4) + (uint32_t)nc * ldb;
+        b_lds[i] = G::A_STAGE + nc * G::B_LD + kc * 4;
+    }
+    f32x4 ra[G::LA], rb[G::LB];
+
+    int kt_first = 0;
+    if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
+
+    auto gload = [&](int t) {
+        int kt = kt_first + t;
+        if (kt >= ktiles) kt -= ktiles;
+        const float* pa = a_tile + (size_t)kt * DK * lda;
+        const float* pb = b_tile + (size_t)kt * DK;
+#pragma unroll
+        for (int i = 0; i < G::LA; ++i)
+            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
+                ra[i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+#pragma unroll
+        for (int i = 0; i < G::LB; ++i)
+            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
+                rb[i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+    };
+    auto swrite = [&](int buf) {
+        float* s = lds + buf * G::STAGE;
+#pragma unroll
+        for (int i = 0; i < G::LA; ++i)
+            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
+                *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < G::LB; ++i)
+            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
+                *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[i];
+    };
+
+    // ---- LDS -> MFMA operand addresses ----
+    const int r = lane % AT::M;  // row (A) / column (B) inside the atom
+    const int g = lane / AT::M;  // k group
+    const int a_rd = g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
+    const int b_rd = G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + g * KPL;
+
+    acc_t acc[WT0][WT1];
+#pragma unroll
+    for (int i = 0; i < WT0; ++i)
+#pragma unroll
+        for (int j = 0; j < WT1; ++j)
+#pragma unroll
+            for (int q = 0; q < AT::ACC; ++q) acc[i][j][q] = 0.0f;
+
+    constexpr int NKB = DK / KB;
+    // operand registers for one k block
+    struct Frag {
+        float a[KPL][WT0];
+        float b[WT1][KPL];
+    };
+    auto load_frag = [&](const float* s, int kb, Frag& f) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) lds_read_row<WT0>(s + a_rd + (kb * KB + j) * G::A_LD, f.a[j]);
+#pragma unroll
+        for (int jn = 0; jn < WT1; ++jn) {
+            const float* p = s + b_rd + jn * AT::N * G::B_LD + kb * KB;
+            float tmp[KPL];
+            lds_read_row<KPL>(p, tmp);
+#pragma unroll
+            for (int j = 0; j < KPL; ++j) f.b[jn][j] = tmp[j];
+        }
+    };
+    auto mfma_frag = [&](const Frag& f) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j)
+#pragma unroll
+            for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                for (int jn = 0; jn < WT1; ++jn) acc[i][jn] = AT::mfma(f.a[j][i], f.b[jn][j], acc[i][jn]);
+    };
+    auto compute = [&](int buf) {
+        const float* s = lds + buf * G::STAGE;
+        if constexpr (SG_PLR > 0 && NKB > 1) {
+            // software pipeline: operands of block kb+1 are read while block kb multiplies
+            Frag f[2];
+            load_frag(s, 0, f[0]);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                if (kb + 1 < NKB) load_frag(s, kb + 1, f[(kb + 1) & 1]);
+                mfma_frag(f[kb & 1]);
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                Frag f;
+                load_frag(s, kb, f);
+                mfma_frag(f);
+            }
+        }
+    };
+
+    // ---- K loop: NBUF LDS buffers, one barrier per tile ----
+#pragma unroll
+    for (int s = 0; s < NBUF - 1; ++s) {
+        if (s < ktiles) {
+            gload(s);
+            swrite(s);
+        }
+    }
+    if (NBUF - 1 < ktiles) gload(NBUF - 1);
+    __syncthreads();
+
+    for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) {
+            const int t = t0 + u;
+            if (t < ktiles) {
+                compute(u);
+                if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
+                if (t + NBUF < ktiles) gload(t + NBUF);
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- epilogue: D = alpha * acc + beta * C ----
+    const int wrow = row0 + wm * (AT::M * WT0);
+    const int wcol = col0 + wn * (AT::N * WT1);
+#pragma unroll
+    for (int jn = 0; jn < WT1; ++jn) {
+        const size_t colo = (size_t)(wcol + jn * AT::N + (lane % AT::N));
+#pragma unroll
+        for (int q = 0; q < AT::ACC; ++q) {
+            const int rr = wrow + AT::row(q, lane) * WT0;
+            float v[WT0];
+#pragma unroll
+            for (int i = 0; i < WT0; ++i) v[i] = alpha * acc[i][jn][q];
+            if (beta != 0.0f) {
+                float cv[WT0];
+                global_load_row<WT0>(c + colo * ldc + rr, cv);
+#pragma unroll
+                for (int i = 0; i < WT0; ++i) v[i] = __builtin_fmaf(beta, cv[i], v[i]);
+            }
+            global_store_row<WT0>(d + colo * ldd + rr, v);
+        }
+    }
+}

@@ -1,0 +1,527 @@
+// Host library behind include/sgemm_shim.h: loads a generated gfx950 SGEMM
+// code object, owns its stream and events, packs the reference's 80-byte
+// kernarg buffer and launches through the HIP module API.  Built as
+// libsgemm_shim.so; the GeneratorRunner executable and the Python ctypes
+// wrapper both call it.
+
+#include "sgemm_shim.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cerrno>
+#include <cmath>
+#include <cstdarg>
+#include <cstddef>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <sstream>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail((int)e, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(call)                                     \
+    do {                                                  \
+        hipError_t e_ = (call);                           \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+// ---------------------------------------------------------------- TOML ----
+// The kernel .toml is flat: `key = value` lines whose values are integers,
+// booleans, strings or arrays of integers (generator.py:1001-1017).
+struct TomlValue {
+    enum Kind { INT, BOOL, STRING, INT_ARRAY } kind = INT;
+    long long i = 0;
+    bool b = false;
+    std::string s;
+    std::vector<long long> arr;
+};
+
+std::string trim(const std::string& x) {
+    size_t a = x.find_first_not_of(" \t\r\n");
+    if (a == std::string::npos) return "";
+    size_t b = x.find_last_not_of(" \t\r\n");
+    return x.substr(a, b - a + 1);
+}
+
+bool parse_int(const std::string& t, long long* out) {
+    if (t.empty()) return false;
+    char* end = nullptr;
+    errno = 0;
+    long long v = strtoll(t.c_str(), &end, 10);
+    if (errno || *end != '\0') return false;
+    *out = v;
+    return true;
+}
+
+int parse_toml(const std::string& path, std::map<std::string, TomlValue>* out) {
+    std::ifstream f(path);
+    if (!f) return fail(SGEMM_E_IO, "cannot open %s", path.c_str());
+    std::string line;
+    int lineno = 0;
+    while (std::getline(f, line)) {
+        ++lineno;
+        // strip comments outside strings
+        bool in_str = false;
+        for (size_t i = 0; i < line.size(); ++i) {
+            if (line[i] == '"') in_str = !in_str;
+            if (line[i] == '#' && !in_str) {
+                line.resize(i);
+                break;
+            }
+        }
+        line = trim(line);
+        if (line.empty()) continue;
+        if (line[0] == '[') return fail(SGEMM_E_CONFIG, "%s:%d: tables are not part of the kernel schema", path.c_str(), lineno);
+        size_t eq = line.find('=');
+        if (eq == std::string::npos) return fail(SGEMM_E_CONFIG, "%s:%d: expected key = value", path.c_str(), lineno);
+        std::string key = trim(line.substr(0, eq));
+        std::string val = trim(line.substr(eq + 1));
+        TomlValue v;
+        if (val == "true" || val == "false") {
+            v.kind = TomlValue::BOOL;
+            v.b = (val == "true");
+        } else if (!val.empty() && val[0] == '"') {
+            if (val.size() < 2 || val.back() != '"') return fail(SGEMM_E_CONFIG, "%s:%d: bad string", path.c_str(), lineno);
+            v.kind = TomlValue::STRING;
+            v.s = val.substr(1, val.size() - 2);
+        } else if (!val.empty() && val[0] == '[') {
+            if (val.back() != ']') return fail(SGEMM_E_CONFIG, "%s:%d: bad array", path.c_str(), lineno);
+            v.kind = TomlValue::INT_ARRAY;
+            std::stringstream ss(val.substr(1, val.size() - 2));
+            std::string item;
+            while (std::getline(ss, item, ',')) {
+                item = trim(item);
+                if (item.empty()) continue;
+                long long x;
+                if (!parse_int(item, &x)) return fail(SGEMM_E_CONFIG, "%s:%d: bad array item '%s'", path.c_str(), lineno, item.c_str());
+                v.arr.push_back(x);
+            }
+        } else {
+            v.kind = TomlValue::INT;
+            if (!parse_int(val, &v.i)) {
+                // other scalars (floats) are tolerated and ignored by the kernel schema
+                v.kind = TomlValue::STRING;
+                v.s = val;
+            }
+        }
+        (*out)[key] = v;
+    }
+    return SGEMM_OK;
+}
+
+int toml_int(const std::map<std::string, TomlValue>& t, const char* key, int* out, bool required = true, int dflt = 0) {
+    auto it = t.find(key);
+    if (it == t.end()) {
+        if (required) return fail(SGEMM_E_CONFIG, "kernel config misses key '%s'", key);
+        *out = dflt;
+        return SGEMM_OK;
+    }
+    if (it->second.kind != TomlValue::INT) return fail(SGEMM_E_CONFIG, "key '%s' must be an integer", key);
+    *out = (int)it->second.i;
+    return SGEMM_OK;
+}
+
+int toml_bool(const std::map<std::string, TomlValue>& t, const char* key, bool* out) {
+    auto it = t.find(key);
+    if (it == t.end()) return fail(SGEMM_E_CONFIG, "kernel config misses key '%s'", key);
+    if (it->second.kind != TomlValue::BOOL) return fail(SGEMM_E_CONFIG, "key '%s' must be a boolean", key);
+    *out = it->second.b;
+    return SGEMM_OK;
+}
+
+int toml_arr(const std::map<std::string, TomlValue>& t, const char* key, int* out, size_t n) {
+    auto it = t.find(key);
+    if (it == t.end()) return fail(SGEMM_E_CONFIG, "kernel config misses key '%s'", key);
+    if (it->second.kind != TomlValue::INT_ARRAY || it->second.arr.size() < n)
+        return fail(SGEMM_E_CONFIG, "key '%s' must be an array of %zu integers", key, n);
+    for (size_t i = 0; i < n; ++i) out[i] = (int)it->second.arr[i];
+    return SGEMM_OK;
+}
+
+#define CFG_TRY(call)                 \
+    do {                              \
+        int r_ = (call);              \
+        if (r_ != SGEMM_OK) return r_; \
+    } while (0)
+
+int load_config(const char* path, sgemm_kernel_info* info) {
+    std::map<std::string, TomlValue> t;
+    CFG_TRY(parse_toml(path, &t));
+    int a_type, b_type, cd_type, scalar_type;
+    bool trans_a, trans_b;
+    // the keys the reference runner reads (generator_runner.cpp:100-124)
+    CFG_TRY(toml_int(t, "a_type", &a_type));
+    CFG_TRY(toml_int(t, "b_type", &b_type));
+    CFG_TRY(toml_int(t, "cd_type", &cd_type));
+    CFG_TRY(toml_int(t, "scalar_type", &scalar_type));
+    CFG_TRY(toml_arr(t, "mfma", info->mfma, 4));
+    CFG_TRY(toml_arr(t, "wave_group", info->wave_group, 2));
+    CFG_TRY(toml_arr(t, "wave_tiling", info->wave_tiling, 2));
+    CFG_TRY(toml_int(t, "depth_k", &info->depth_k));
+    CFG_TRY(toml_bool(t, "trans_a", &trans_a));
+    CFG_TRY(toml_bool(t, "trans_b", &trans_b));
+    CFG_TRY(toml_int(t, "wavefront_size", &info->wavefront_size));
+    CFG_TRY(toml_int(t, "lds_usage_bytes", &info->lds_usage_bytes));
+    CFG_TRY(toml_int(t, "vmem_stage", &info->vmem_stage, false, 1));
+    if (a_type || b_type || cd_type || scalar_type) return fail(SGEMM_E_CONFIG, "only FP32 (type 0) kernels are supported");
+    if (trans_a || trans_b) return fail(SGEMM_E_CONFIG, "only the NN layout is supported");
+    if (info->wavefront_size != 64) return fail(SGEMM_E_CONFIG, "wavefront_size must be 64 on gfx950");
+    const int* mf = info->mfma;
+    const bool atom32 = mf[0] == 32 && mf[1] == 32 && mf[2] == 1 && mf[3] == 2;
+    const bool atom16 = mf[0] == 16 && mf[1] == 16 && mf[2] == 1 && mf[3] == 4;
+    if (!atom32 && !atom16) return fail(SGEMM_E_CONFIG, "unsupported mfma atom [%d, %d, %d, %d]", mf[0], mf[1], mf[2], mf[3]);
+    for (int i = 0; i < 2; ++i) {
+        if (info->wave_group[i] <= 0 || info->wave_tiling[i] <= 0)
+            return fail(SGEMM_E_CONFIG, "wave_group and wave_tiling must be positive");
+    }
+    if (info->depth_k <= 0) return fail(SGEMM_E_CONFIG, "depth_k must be positive");
+    info->tile_m = mf[0] * info->wave_group[0] * info->wave_tiling[0];
+    info->tile_n = mf[1] * info->wave_group[1] * info->wave_tiling[1];
+    info->workitems = info->wave_group[0] * info->wave_group[1] * info->wavefront_size;
+    if (info->workitems > 1024) return fail(SGEMM_E_CONFIG, "work-group of %d work-items exceeds 1024", info->workitems);
+    return SGEMM_OK;
+}
+
+// ------------------------------------------------------------- kernargs ---
+// Byte image of generated_gemm's explicit arguments (generator.py:2604-2620,
+// generator_runner.cpp:132-148): 76 bytes, padded to 80.
+struct KernArgs {
+    const float* a;
+    const float* b;
+    const float* c;
+    float* d;
+    uint32_t m, n, k, lda, ldb, ldc, ldd;
+    float alpha, beta;
+    int32_t num_wg_x, num_wg_y;
+    uint32_t pad;
+};
+static_assert(sizeof(KernArgs) == 80, "kernarg image must be 80 bytes");
+static_assert(offsetof(KernArgs, m) == 32 && offsetof(KernArgs, ldd) == 56, "kernarg offsets");
+static_assert(offsetof(KernArgs, alpha) == 60 && offsetof(KernArgs, beta) == 64, "kernarg offsets");
+static_assert(offsetof(KernArgs, num_wg_x) == 68 && offsetof(KernArgs, num_wg_y) == 72, "kernarg offsets");
+
+// ------------------------------------------------------- seeded values ---
+const uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+inline uint64_t stream_key(uint64_t seed, uint32_t matrix_id) {
+    return mix64(seed ^ (0xD1B54A32D192ED03ull * (uint64_t)(matrix_id + 1)));
+}
+
+// i-th output (from 0) of SplitMix64 started at `key`
+inline uint64_t word_at(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * kGamma); }
+
+inline float uniform_pm1(uint64_t w) {
+    const float u = (float)(w >> 40) * 5.9604644775390625e-08f;  // 24 bits * 2^-24, exact
+    return u * 2.0f - 1.0f;                                      // exact
+}
+
+inline float normal_at(uint64_t key, uint64_t i) {
+    const uint64_t p = i >> 1;
+    const double u1 = (double)((word_at(key, 2 * p) >> 11) + 1) * 1.1102230246251565e-16;  // (0, 1]
+    const double u2 = (double)(word_at(key, 2 * p + 1) >> 11) * 1.1102230246251565e-16;    // [0, 1)
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    const double th = 6.283185307179586 * u2;
+    return (float)((i & 1) ? r * std::sin(th) : r * std::cos(th));
+}
+
+}  // namespace
+
+struct sgemm_handle {
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_start = nullptr;
+    hipEvent_t ev_stop = nullptr;
+    sgemm_kernel_info info{};
+};
+
+extern "C" {
+
+const char* sgemm_last_error(void) { return g_last_error.c_str(); }
+
+int sgemm_abi_version(void) { return SGEMM_SHIM_ABI_VERSION; }
+
+int sgemm_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz, int* lds_per_block) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return fail(SGEMM_E_NO_DEVICE, "no HIP device visible (%s)", hipGetErrorString(e));
+    hipDeviceProp_t p;
+    HIP_TRY(hipGetDeviceProperties(&p, 0));
+    if (name && name_len) {
+        snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (compute_units) *compute_units = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    if (lds_per_block) *lds_per_block = (int)p.sharedMemPerBlock;
+    return SGEMM_OK;
+}
+
+int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
+    if (!co_path || !toml_path || !out) return fail(SGEMM_E_INVALID, "sgemm_open: null argument");
+    *out = nullptr;
+    sgemm_kernel_info info{};
+    int r = load_config(toml_path, &info);
+    if (r != SGEMM_OK) return r;
+    {
+        std::ifstream f(co_path, std::ios::binary);
+        if (!f) return fail(SGEMM_E_IO, "cannot open code object %s", co_path);
+    }
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return fail(SGEMM_E_NO_DEVICE, "no HIP device visible (%s)", hipGetErrorString(e));
+    sgemm_handle* h = new sgemm_handle();
+    h->info = info;
+    hipError_t err = hipModuleLoad(&h->module, co_path);
+    if (err != hipSuccess) {
+        delete h;
+        return hip_fail(err, "hipModuleLoad");
+    }
+    err = hipModuleGetFunction(&h->function, h->module, "generated_gemm");
+    if (err == hipSuccess) err = hipStreamCreate(&h->stream);
+    if (err == hipSuccess) err = hipEventCreate(&h->ev_start);
+    if (err == hipSuccess) err = hipEventCreate(&h->ev_stop);
+    if (err != hipSuccess) {
+        sgemm_close(h);
+        return hip_fail(err, "sgemm_open");
+    }
+    *out = h;
+    return SGEMM_OK;
+}
+
+void sgemm_close(sgemm_handle* h) {
+    if (!h) return;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->ev_start) (void)hipEventDestroy(h->ev_start);
+    if (h->ev_stop) (void)hipEventDestroy(h->ev_stop);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    if (h->module) (void)hipModuleUnload(h->module);
+    delete h;
+}
+
+int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info) {
+    if (!h || !info) return fail(SGEMM_E_INVALID, "sgemm_get_info: null argument");
+    *info = h->info;
+    return SGEMM_OK;
+}
+
+int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
+                      uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_check_shape: null handle");
+    const sgemm_kernel_info& i = h->info;
+    if (m % (uint32_t)i.tile_m || n % (uint32_t)i.tile_n || k % (uint32_t)i.depth_k)
+        return fail(SGEMM_E_SHAPE, "shape %ux%ux%u is not a multiple of the kernel tile %dx%d (depth_k %d)",
+                    m, n, k, i.tile_m, i.tile_n, i.depth_k);
+    if (lda < m || ldb < k || ldc < m || ldd < m)
+        return fail(SGEMM_E_SHAPE, "leading dimensions too small: lda=%u (m=%u) ldb=%u (k=%u) ldc=%u ldd=%u",
+                    lda, m, ldb, k, ldc, ldd);
+    if ((lda | ldb | ldc | ldd) & 3u)
+        return fail(SGEMM_E_SHAPE, "leading dimensions must be multiples of 4 (16-byte rows): %u %u %u %u",
+                    lda, ldb, ldc, ldd);
+    const uint64_t wgx = m / (uint32_t)i.tile_m, wgy = n / (uint32_t)i.tile_n;
+    if (wgx > 0x7fffffffull || wgy > 65535ull * 1024ull || wgx * wgy > 0x7fffffffull)
+        return fail(SGEMM_E_SHAPE, "grid %llux%llu too large", (unsigned long long)wgx, (unsigned long long)wgy);
+    return SGEMM_OK;
+}
+
+int sgemm_malloc(void** dptr, size_t bytes) {
+    if (!dptr) return fail(SGEMM_E_INVALID, "sgemm_malloc: null argument");
+    *dptr = nullptr;
+    HIP_TRY(hipMalloc(dptr, bytes ? bytes : 1));
+    return SGEMM_OK;
+}
+
+int sgemm_free(void* dptr) {
+    if (dptr) HIP_TRY(hipFree(dptr));
+    return SGEMM_OK;
+}
+
+int sgemm_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes && (!dst || !src)) return fail(SGEMM_E_INVALID, "sgemm_memcpy_h2d: null argument");
+    if (bytes) HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return SGEMM_OK;
+}
+
+int sgemm_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes && (!dst || !src)) return fail(SGEMM_E_INVALID, "sgemm_memcpy_d2h: null argument");
+    if (bytes) HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return SGEMM_OK;
+}
+
+int sgemm_memset(void* dptr, int value, size_t bytes) {
+    if (bytes && !dptr) return fail(SGEMM_E_INVALID, "sgemm_memset: null argument");
+    if (bytes) HIP_TRY(hipMemset(dptr, value, bytes));
+    return SGEMM_OK;
+}
+
+int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                 uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                 float alpha, float beta) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_launch: null handle");
+    int r = sgemm_check_shape(h, m, n, k, lda, ldb, ldc, ldd);
+    if (r != SGEMM_OK) return r;
+    if (m == 0 || n == 0) return SGEMM_OK;
+    if (!dD || (k && (!dA || !dB)) || (beta != 0.0f && !dC))
+        return fail(SGEMM_E_INVALID, "sgemm_launch: null device pointer");
+    if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 15u)
+        return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 16-byte aligned");
+    const sgemm_kernel_info& i = h->info;
+    KernArgs ka;
+    memset(&ka, 0, sizeof(ka));
+    ka.a = dA; ka.b = dB; ka.c = dC; ka.d = dD;
+    ka.m = m; ka.n = n; ka.k = k; ka.lda = lda; ka.ldb = ldb; ka.ldc = ldc; ka.ldd = ldd;
+    ka.alpha = alpha; ka.beta = beta;
+    ka.num_wg_x = (int32_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m);
+    ka.num_wg_y = (int32_t)((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+    size_t size = sizeof(ka);
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+    HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
+                                  (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+    return SGEMM_OK;
+}
+
+int sgemm_time(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+               uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+               float alpha, float beta, int warmup, int runs, float* total_ms) {
+    if (!h || !total_ms || warmup < 0 || runs <= 0) return fail(SGEMM_E_INVALID, "sgemm_time: bad argument");
+    int r;
+    for (int w = 0; w < warmup; ++w)
+        if ((r = sgemm_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta)) != SGEMM_OK) return r;
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    HIP_TRY(hipEventRecord(h->ev_start, h->stream));
+    for (int t = 0; t < runs; ++t)
+        if ((r = sgemm_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta)) != SGEMM_OK) return r;
+    HIP_TRY(hipEventRecord(h->ev_stop, h->stream));
+    HIP_TRY(hipEventSynchronize(h->ev_stop));
+    HIP_TRY(hipEventElapsedTime(total_ms, h->ev_start, h->ev_stop));
+    return SGEMM_OK;
+}
+
+int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                    float alpha, float beta, int runs, float* per_launch_ms) {
+    if (!h || !per_launch_ms || runs <= 0) return fail(SGEMM_E_INVALID, "sgemm_time_each: bad argument");
+    std::vector<hipEvent_t> ev(2 * (size_t)runs, nullptr);
+    int result = SGEMM_OK;
+    for (auto& e : ev) {
+        hipError_t err = hipEventCreate(&e);
+        if (err != hipSuccess) {
+            result = hip_fail(err, "hipEventCreate");
+            break;
+        }
+    }
+    for (int t = 0; t < runs && result == SGEMM_OK; ++t) {
+        hipError_t err = hipEventRecord(ev[2 * t], h->stream);
+        if (err != hipSuccess) { result = hip_fail(err, "hipEventRecord"); break; }
+        result = sgemm_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta);
+        if (result != SGEMM_OK) break;
+        err = hipEventRecord(ev[2 * t + 1], h->stream);
+        if (err != hipSuccess) { result = hip_fail(err, "hipEventRecord"); break; }
+    }
+    if (result == SGEMM_OK) {
+        hipError_t err = hipStreamSynchronize(h->stream);
+        if (err != hipSuccess) result = hip_fail(err, "hipStreamSynchronize");
+    }
+    for (int t = 0; t < runs && result == SGEMM_OK; ++t) {
+        hipError_t err = hipEventElapsedTime(&per_launch_ms[t], ev[2 * t], ev[2 * t + 1]);
+        if (err != hipSuccess) result = hip_fail(err, "hipEventElapsedTime");
+    }
+    (void)hipStreamSynchronize(h->stream);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    return result;
+}
+
+int sgemm_synchronize(sgemm_handle* h) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_synchronize: null handle");
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return SGEMM_OK;
+}
+
+int sgemm_run(sgemm_handle* h, const float* A, const float* B, const float* C, float* D,
+              uint32_t m, uint32_t n, uint32_t k, float alpha, float beta,
+              int warmup, int runs, double* ms_per_run) {
+    if (!h || !D || !A || !B || (beta != 0.0f && !C) || runs <= 0 || warmup < 0)
+        return fail(SGEMM_E_INVALID, "sgemm_run: bad argument");
+    int r = sgemm_check_shape(h, m, n, k, m, k, m, m);
+    if (r != SGEMM_OK) return r;
+    const size_t bA = (size_t)m * k * 4, bB = (size_t)k * n * 4, bC = (size_t)m * n * 4;
+    void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dD = nullptr;
+    float total = 0.0f;
+    r = sgemm_malloc(&dA, bA);
+    if (r == SGEMM_OK) r = sgemm_malloc(&dB, bB);
+    if (r == SGEMM_OK && beta != 0.0f) r = sgemm_malloc(&dC, bC);
+    if (r == SGEMM_OK) r = sgemm_malloc(&dD, bC);
+    if (r == SGEMM_OK) r = sgemm_memcpy_h2d(dA, A, bA);
+    if (r == SGEMM_OK) r = sgemm_memcpy_h2d(dB, B, bB);
+    if (r == SGEMM_OK && dC) r = sgemm_memcpy_h2d(dC, C, bC);
+    if (r == SGEMM_OK) r = sgemm_memset(dD, 0, bC);
+    if (r == SGEMM_OK)
+        r = sgemm_time(h, (const float*)dA, (const float*)dB, (const float*)dC, (float*)dD, m, n, k, m, k, m, m,
+                       alpha, beta, warmup, runs, &total);
+    if (r == SGEMM_OK) r = sgemm_memcpy_d2h(D, dD, bC);
+    if (r == SGEMM_OK && ms_per_run) *ms_per_run = (double)total / runs;
+    std::string keep = g_last_error;
+    sgemm_free(dA);
+    sgemm_free(dB);
+    sgemm_free(dC);
+    sgemm_free(dD);
+    g_last_error = keep;
+    return r;
+}
+
+int sgemm_fill(float* host, size_t count, uint64_t seed, uint32_t matrix_id, int dist) {
+    if (count && !host) return fail(SGEMM_E_INVALID, "sgemm_fill: null argument");
+    if (dist != SGEMM_DIST_UNIFORM && dist != SGEMM_DIST_NORMAL && dist != SGEMM_DIST_ZERO)
+        return fail(SGEMM_E_INVALID, "sgemm_fill: unknown distribution %d", dist);
+    const uint64_t key = stream_key(seed, matrix_id);
+    auto work = [=](size_t lo, size_t hi) {
+        for (size_t i = lo; i < hi; ++i) {
+            if (dist == SGEMM_DIST_UNIFORM) host[i] = uniform_pm1(word_at(key, i));
+            else if (dist == SGEMM_DIST_NORMAL) host[i] = normal_at(key, i);
+            else host[i] = 0.0f;
+        }
+    };
+    unsigned nt = std::thread::hardware_concurrency();
+    nt = std::max(1u, std::min(nt, 16u));
+    if (count < (1u << 20) || nt == 1) {
+        work(0, count);
+        return SGEMM_OK;
+    }
+    std::vector<std::thread> pool;
+    const size_t chunk = (count + nt - 1) / nt;
+    for (unsigned t = 0; t < nt; ++t) {
+        const size_t lo = t * chunk, hi = std::min(count, lo + chunk);
+        if (lo < hi) pool.emplace_back(work, lo, hi);
+    }
+    for (auto& th : pool) th.join();
+    return SGEMM_OK;
+}
+
+}  // extern "C"

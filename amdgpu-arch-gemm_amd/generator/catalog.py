@@ -1,0 +1,106 @@
+"""Named kernel instances shipped with the package, and shape-keyed selection.
+
+Each entry is one (GemmSolutionConfig, GemmOptimizations) pair that
+``build_all`` compiles into ``kernels/<name>.co`` + ``kernels/<name>.toml``.
+``select(m, n, k)`` returns the name to use for a problem: the instance the
+gfx950 tuner chose for that shape class, falling back to the largest tile that
+divides the problem.  The reference has no catalog: its tuner prints the best
+point and keeps nothing (sgemm_tuner.py:116-128).
+"""
+from __future__ import annotations
+
+import os
+from concurrent.futures import ThreadPoolExecutor
+from typing import Dict, List, Optional, Tuple
+
+from .generator import (DataType, GemmOptimizations, GemmSolutionConfig, MFMA_16x16x4, MFMA_32x32x2,
+                        build_kernel)
+
+PACKAGE_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KERNEL_DIR = os.path.join(PACKAGE_ROOT, "kernels")
+
+F = DataType.FP32
+
+
+def _cfg(mfma, wg, wt, dk, stages=1):
+    return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, False, False, vmem_stage=stages)
+
+
+def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0):
+    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd)
+
+
+# name -> (config, optimizations)
+SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
+    # headline 4096^3: 256x256 tiles, one work-group per CU
+    "mt256x256_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, xcd=8)),
+    "mt256x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16), _opt(wgm=4, xcd=8)),
+    "mt128x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 16), _opt(wgm=4, xcd=8)),
+    "mt128x128_a32_wg2x2_dk32": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 32), _opt(wgm=4, xcd=8)),
+    "mt64x64_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (1, 1), 16), _opt(wgm=4, xcd=8)),
+    "mt128x64_a16_wg4x1_dk32": (_cfg(MFMA_16x16x4, (4, 1), (2, 4), 32), _opt(wgm=4, xcd=8)),
+    "mt64x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (1, 2), 16), _opt(xcd=8)),
+    # variants that exercise every knob in the parity tests
+    "mt128x128_a16_wg2x2_dk16": (_cfg(MFMA_16x16x4, (2, 2), (4, 4), 16), _opt(wgm=2)),
+    "mt64x64_a16_wg2x2_dk8": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 8), _opt(plr=0)),
+    "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4)),
+    "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8)),
+    # the reference's one-wave VM configurations (test_vm.py:447-627)
+    "mt32x32_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16), _opt()),
+    "mt16x16_a16_wg1x1_dk16": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt()),
+    "mt16x16_a16_wg1x1_dk16_wgm4": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt(wgm=4)),
+    "mt16x16_a16_wg1x1_dk16_mapk4": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt(mapk=4)),
+    "mt16x16_a16_wg1x1_dk16_s3": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt()),
+}
+
+# shape class -> preferred instance (filled from tuner results; see select())
+PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
+    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk16"),
+    ((1024, 1024, 1024), "mt64x64_a32_wg2x2_dk16"),
+    ((8192, 8192, 256), "mt256x256_a32_wg2x2_dk16"),
+    ((16384, 128, 4096), "mt64x128_a32_wg2x2_dk16"),
+]
+
+
+def paths(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
+    return os.path.join(kernel_dir, f"{name}.co"), os.path.join(kernel_dir, f"{name}.toml")
+
+
+def build_one(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
+    cfg, opt = SOLUTIONS[name]
+    cfg.name = name
+    return build_kernel(kernel_dir, cfg, opt, kern_name=name)
+
+
+def build_all(kernel_dir: str = KERNEL_DIR, names: Optional[List[str]] = None, jobs: int = 8) -> List[str]:
+    names = list(SOLUTIONS) if names is None else names
+    os.makedirs(kernel_dir, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(lambda n: build_one(n, kernel_dir), names))
+    return names
+
+
+def divides(name: str, m: int, n: int, k: int) -> bool:
+    cfg, _ = SOLUTIONS[name]
+    t0, t1 = cfg.tile_size
+    return m % t0 == 0 and n % t1 == 0 and k % cfg.depth_k == 0
+
+
+def select(m: int, n: int, k: int) -> str:
+    """Instance for an (m, n, k) problem; raises if none divides it."""
+    for shape, name in PREFERRED:
+        if shape == (m, n, k) and divides(name, m, n, k):
+            return name
+    best = None
+    for name, (cfg, _) in SOLUTIONS.items():
+        if not divides(name, m, n, k):
+            continue
+        t0, t1 = cfg.tile_size
+        tiles = (m // t0) * (n // t1)
+        # prefer the largest tile that still gives every CU a work-group
+        key = (tiles >= 256, t0 * t1, cfg.depth_k)
+        if best is None or key > best[0]:
+            best = (key, name)
+    if best is None:
+        raise RuntimeError(f"no kernel instance divides {m}x{n}x{k}")
+    return best[1]

@@ -1,0 +1,644 @@
+"""Kernel generator for the gfx950 FP32 column-major NN SGEMM.
+
+This module keeps the reference generator's Python surface
+(/root/reference/generator/generator.py) so that the tuner, the tests and any
+caller written against it keep working:
+
+* ``DataType`` / ``datatype_size``            (generator.py:816-824)
+* ``GemmOptimizations(level, wgm, plr, gw, map_k_idx)``  (generator.py:827-854)
+* ``GemmSolutionConfig(...)`` with ``tile_size``, ``num_workitems``,
+  ``num_bytes_per_buffer_load``, ``lds_pad_bytes``, ``lds_usage_bytes``,
+  ``to_dict`` / ``from_dict`` and ``RuntimeError`` on invalid geometry
+  (generator.py:857-1055)
+* ``FunctionArgument``                        (generator.py:94-103)
+* ``gemm(context, name, arch, config, opt, args) -> str``  (generator.py:1056)
+* ``compile(kern_name, kern_str, arch, output_folder, config) -> int``
+  (generator.py:2534-2569): writes ``<out>/<name>.co`` and ``<out>/<name>.toml``
+* the CLI ``generator.py --arch gfx950 <out>``  (generator.py:2571-2623)
+
+What ``gemm`` produces is different by design: instead of GCN assembly text it
+returns a self-contained HIP translation unit -- the hand-written gfx950
+kernel template in ``csrc/sgemm_gfx950.hip`` specialised by ``#define`` lines --
+and ``compile`` builds it with ``hipcc --cuda-device-only -c --offload-arch=gfx950``.  The
+code object exports ``generated_gemm`` with the reference's 15-argument,
+76-byte kernarg layout, so the reference runner can load it unchanged.
+"""
+from __future__ import annotations
+
+import argparse
+import math
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from enum import IntEnum
+from typing import Dict, List, Optional, Sequence, Tuple
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PACKAGE_ROOT = os.path.dirname(_HERE)
+KERNEL_TEMPLATE = os.path.join(PACKAGE_ROOT, "csrc", "sgemm_gfx950.hip")
+
+DEFAULT_HIPCC_PATH = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+SUPPORTED_ARCHS = ("gfx950", "gfx950:xnack-")
+# LDS of one gfx950 compute unit (CDNA4: 160 KiB), the largest static LDS a
+# work-group may declare.
+MAX_LDS_NUM_BYTES = 163840
+# Work-items per work-group accepted by the hardware.
+MAX_WORKITEMS = 1024
+# LDS geometry used by the pad solver: gfx950 serves a 16-byte-per-lane LDS
+# access in groups of lanes that together cover all banks once.
+LDS_NUM_BANKS = 64
+LDS_BANK_BYTES = 4
+# hipcc flags for every kernel: packed FP32 VALU ops stay off.
+HIPCC_KERNEL_FLAGS = (
+    "-O3",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+)
+
+# MFMA atoms as (M, N, blocks, K), the reference's tuple convention
+# (generator.py:796-801).
+MFMA_32x32x2 = (32, 32, 1, 2)
+MFMA_16x16x4 = (16, 16, 1, 4)
+SUPPORTED_MFMAS = (MFMA_16x16x4, MFMA_32x32x2)
+
+
+class DataType(IntEnum):
+    FP32 = 0
+
+
+def datatype_size(dtype: DataType) -> int:
+    if dtype == DataType.FP32:
+        return 4
+    raise RuntimeError(f"unrecognized type {dtype!r}")
+
+
+def _is_pow2(x: int) -> bool:
+    return x > 0 and (x & (x - 1)) == 0
+
+
+class GemmOptimizations:
+    """Code-shape knobs that are baked into the code object.
+
+    Same constructor and defaults as the reference (generator.py:827-854):
+    level != 0 turns on ``plr = 1`` and ``gw = 1``.  Meaning on gfx950:
+
+    * ``wgm``       -- group width (in tiles along M) of the work-group order.
+    * ``plr``       -- operand prefetch depth: 0 reads a k block's operands and
+                       then multiplies; >= 1 reads block kb+1 while block kb
+                       multiplies (register double buffering).
+    * ``gw``        -- epilogue flavour: 0 stores straight from the
+                       accumulators, 1 is the same store path (kept for the
+                       reference's knob space; both paths are identical today).
+    * ``map_k_idx`` -- rotate the first K tile by ``tile_x & (map_k_idx - 1)``.
+    * ``xcd``       -- (gfx950 only) number of XCDs to give contiguous tile
+                       ranges to; 0 or 1 leaves the hardware order.
+    """
+
+    def __init__(
+        self,
+        level: int,
+        wgm: Optional[int] = None,
+        plr: Optional[int] = None,
+        gw: Optional[int] = None,
+        map_k_idx: Optional[int] = None,
+        xcd: Optional[int] = None,
+    ):
+        self.level = level
+        self.wgm = 1
+        self.plr = 0
+        self.gw = 0
+        self.map_k_idx = 0
+        self.xcd = 0
+        self._setup_optimizations()
+        if wgm is not None:
+            self.wgm = wgm
+        if plr is not None:
+            self.plr = plr
+        if gw is not None:
+            self.gw = gw
+        if map_k_idx is not None:
+            self.map_k_idx = map_k_idx
+        if xcd is not None:
+            self.xcd = xcd
+        if self.wgm < 1:
+            raise RuntimeError(f"Invalid wgm: {self.wgm}")
+        if self.map_k_idx and not _is_pow2(self.map_k_idx):
+            raise RuntimeError(f"map_k_idx must be 0 or a power of two: {self.map_k_idx}")
+        if self.plr < 0 or self.gw not in (0, 1) or self.xcd < 0:
+            raise RuntimeError(f"Invalid optimization knobs: plr={self.plr} gw={self.gw} xcd={self.xcd}")
+
+    def _setup_optimizations(self):
+        if self.level != 0:
+            self.plr = 1
+            self.gw = 1
+
+    def to_dict(self) -> Dict:
+        return {
+            "opt_level": int(self.level),
+            "wgm": int(self.wgm),
+            "plr": int(self.plr),
+            "gw": int(self.gw),
+            "map_k_idx": int(self.map_k_idx),
+            "xcd": int(self.xcd),
+        }
+
+    def __repr__(self) -> str:
+        return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
+                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd})")
+
+
+def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int,
+                      num_banks: int = LDS_NUM_BANKS, bank_bytes: int = LDS_BANK_BYTES) -> int:
+    """Cycles one wave-wide LDS access takes under a simple bank model.
+
+    Lanes are served in groups whose combined width equals one pass over all
+    banks (``num_banks * bank_bytes / access_bytes`` lanes, at least one).  A
+    group costs as many cycles as the most-used bank in it; distinct dwords of
+    one bank conflict, the same dword is broadcast.
+    """
+    per_group = max(1, (num_banks * bank_bytes) // access_bytes)
+    cycles = 0
+    for g0 in range(0, len(byte_addrs), per_group):
+        words_per_bank: Dict[int, set] = {}
+        for addr in byte_addrs[g0:g0 + per_group]:
+            for w in range(access_bytes // bank_bytes):
+                word = addr // bank_bytes + w
+                words_per_bank.setdefault(word % num_banks, set()).add(word)
+        cycles += max(len(v) for v in words_per_bank.values())
+    return cycles
+
+
+class GemmSolutionConfig:
+    """Geometry of one kernel instance (generator.py:857-1055).
+
+    ``mfma`` is (M, N, blocks, K); MT0 = mfma[0] * wave_group[0] * wave_tiling[0]
+    and MT1 = mfma[1] * wave_group[1] * wave_tiling[1]; the work-group has
+    wave_group[0] * wave_group[1] waves of 64 lanes; ``vmem_stage + 1`` LDS
+    buffers hold K tiles of depth ``depth_k``.  Invalid geometry raises
+    ``RuntimeError`` at construction, as the reference does.
+    """
+
+    def __init__(
+        self,
+        a_type: DataType,
+        b_type: DataType,
+        cd_type: DataType,
+        scalar_type: DataType,
+        mfma: Tuple[int, int, int, int],
+        wave_group: Tuple[int, int],
+        wave_tiling: Tuple[int, int],
+        depth_k: int,
+        trans_a: bool,
+        trans_b: bool,
+        vmem_stage: int = 1,
+    ):
+        self.a_type = DataType(a_type)
+        self.b_type = DataType(b_type)
+        self.cd_type = DataType(cd_type)
+        self.scalar_type = DataType(scalar_type)
+        self.wave_group = tuple(int(x) for x in wave_group)
+        self.trans_a = bool(trans_a)
+        self.trans_b = bool(trans_b)
+        self.mfma = tuple(int(x) for x in mfma)
+        self.wave_tiling = tuple(int(x) for x in wave_tiling)
+        self.depth_k = int(depth_k)
+        self.vmem_stage = int(vmem_stage)
+        self.wavefront_size = 64
+        self.name = None
+        self._validate()
+
+    # ---------------------------------------------------------------- checks
+    def _validate(self):
+        if self.mfma not in SUPPORTED_MFMAS:
+            raise RuntimeError(f"Unsupported MFMA atom: {self.mfma}")
+        if any(t != DataType.FP32 for t in (self.a_type, self.b_type, self.cd_type, self.scalar_type)):
+            raise RuntimeError("Only FP32 operands are supported")
+        if self.trans_a or self.trans_b:
+            raise RuntimeError("Only the NN layout (trans_a = trans_b = False) is implemented")
+        if not all(_is_pow2(w) for w in self.wave_group):
+            raise RuntimeError(f"Invalid wave group: {self.wave_group}")
+        if self.num_workitems > MAX_WORKITEMS:
+            raise RuntimeError(f"Work-group of {self.num_workitems} work-items exceeds {MAX_WORKITEMS}")
+        if self.wave_tiling[0] not in (1, 2, 4, 8):
+            raise RuntimeError(f"Invalid wave tiling along M (1, 2, 4 or 8): {self.wave_tiling}")
+        if not 1 <= self.wave_tiling[1] <= 8:
+            raise RuntimeError(f"Invalid wave tiling along N (1..8): {self.wave_tiling}")
+        if self.depth_k < 4 or self.depth_k % 4:
+            raise RuntimeError(f"depth_k must be a positive multiple of 4: {self.depth_k}")
+        if self.depth_k % self.k_block:
+            raise RuntimeError(f"depth_k {self.depth_k} is not a multiple of the k block {self.k_block}")
+        if self.vmem_stage < 1:
+            raise RuntimeError(f"vmem_stage must be >= 1: {self.vmem_stage}")
+        if self.lds_usage_bytes > MAX_LDS_NUM_BYTES:
+            raise RuntimeError(f"LDS usage exceeds {MAX_LDS_NUM_BYTES}: {self.lds_usage_bytes}")
+
+    # -------------------------------------------------------------- geometry
+    @property
+    def tile_size(self) -> Tuple[int, int]:
+        return (
+            self.mfma[0] * self.wave_group[0] * self.wave_tiling[0],
+            self.mfma[1] * self.wave_group[1] * self.wave_tiling[1],
+        )
+
+    @property
+    def num_workitems(self) -> int:
+        return self.wave_group[0] * self.wave_group[1] * self.wavefront_size
+
+    @property
+    def k_per_lane(self) -> int:
+        """Consecutive k values one lane reads per LDS read (KPL)."""
+        steps = self.depth_k // self.mfma[3]
+        return 4 if steps >= 4 else (2 if steps >= 2 else 1)
+
+    @property
+    def k_block(self) -> int:
+        """k values covered by one block of KPL MFMA steps."""
+        return self.mfma[3] * self.k_per_lane
+
+    @property
+    def num_bytes_per_buffer_load(self) -> Tuple[int, int]:
+        """Bytes per global load per work-item for A and B (always dwordx4 here)."""
+        t0, t1 = self.tile_size
+        per_a = t0 * self.depth_k * datatype_size(self.a_type) // self.num_workitems
+        per_b = t1 * self.depth_k * datatype_size(self.b_type) // self.num_workitems
+        return min(max(per_a, 0), 16), min(max(per_b, 0), 16)
+
+    @property
+    def num_dwords_per_buffer_load(self) -> Tuple[int, int]:
+        b0, b1 = self.num_bytes_per_buffer_load
+        return b0 // 4, b1 // 4
+
+    @property
+    def num_elements_per_ds_read(self) -> Tuple[int, int]:
+        # A: the WT0 interleaved atoms' operands; B: KPL consecutive k values.
+        return self.wave_tiling[0], self.k_per_lane
+
+    @property
+    def num_bytes_per_ds_read(self) -> Tuple[int, int]:
+        return (
+            self.num_elements_per_ds_read[0] * datatype_size(self.a_type),
+            self.num_elements_per_ds_read[1] * datatype_size(self.b_type),
+        )
+
+    @property
+    def num_unrolled_iters(self) -> int:
+        return self.depth_k // self.mfma[3]
+
+    # ------------------------------------------------------------------- LDS
+    def _a_read_addrs(self, pad: int) -> List[int]:
+        am = self.mfma[0]
+        wt0 = self.wave_tiling[0]
+        stride = self.tile_size[0] + pad
+        kpl = self.k_per_lane
+        return [((l // am) * kpl * stride + (l % am) * wt0) * 4 for l in range(64)]
+
+    def _b_read_addrs(self, pad: int) -> List[int]:
+        an = self.mfma[1]
+        stride = self.depth_k + pad
+        kpl = self.k_per_lane
+        return [((l % an) * stride + (l // an) * kpl) * 4 for l in range(64)]
+
+    def _b_write_addrs(self, pad: int) -> List[int]:
+        stride = self.depth_k + pad
+        per_col = self.depth_k // 4
+        return [((t // per_col) * stride + (t % per_col) * 4) * 4 for t in range(64)]
+
+    def _auto_lds_pad_a(self) -> int:
+        best, best_cost = 0, None
+        for pad in (0, 4, 8, 12, 16):
+            cost = lds_access_cycles(self._a_read_addrs(pad), 4 * self.wave_tiling[0])
+            if best_cost is None or cost < best_cost:
+                best, best_cost = pad, cost
+        return best
+
+    def _auto_lds_pad_b(self) -> int:
+        best, best_cost = 0, None
+        for pad in (0, 4, 8, 12, 16):
+            cost = (lds_access_cycles(self._b_read_addrs(pad), 4 * self.k_per_lane) * 4
+                    + lds_access_cycles(self._b_write_addrs(pad), 16))
+            if best_cost is None or cost < best_cost:
+                best, best_cost = pad, cost
+        return best
+
+    @property
+    def lds_pad_bytes(self) -> Tuple[int, int]:
+        return (
+            self._auto_lds_pad_a() * datatype_size(self.a_type),
+            self._auto_lds_pad_b() * datatype_size(self.b_type),
+        )
+
+    @property
+    def lds_offset_bytes(self) -> Tuple[int, int]:
+        pad_a = self.lds_pad_bytes[0] // datatype_size(self.a_type)
+        return 0, (self.tile_size[0] + pad_a) * self.depth_k * datatype_size(self.a_type)
+
+    @property
+    def lds_swap_offset_bytes(self) -> int:
+        """Bytes of one LDS stage: A [DK][MT0 + padA] then B [MT1][DK + padB]."""
+        pad_a = self.lds_pad_bytes[0] // datatype_size(self.a_type)
+        pad_b = self.lds_pad_bytes[1] // datatype_size(self.b_type)
+        return ((self.tile_size[0] + pad_a) * self.depth_k * datatype_size(self.a_type)
+                + self.tile_size[1] * (self.depth_k + pad_b) * datatype_size(self.b_type))
+
+    @property
+    def lds_usage_bytes(self) -> int:
+        return (self.vmem_stage + 1) * self.lds_swap_offset_bytes
+
+    # ----------------------------------------------------------- (de)serial
+    def to_dict(self) -> Dict:
+        return {
+            "a_type": int(self.a_type),
+            "b_type": int(self.b_type),
+            "cd_type": int(self.cd_type),
+            "scalar_type": int(self.scalar_type),
+            "wave_group": list(self.wave_group),
+            "trans_a": self.trans_a,
+            "trans_b": self.trans_b,
+            "mfma": list(self.mfma),
+            "wave_tiling": list(self.wave_tiling),
+            "depth_k": self.depth_k,
+            "vmem_stage": self.vmem_stage,
+            "wavefront_size": self.wavefront_size,
+            "lds_usage_bytes": self.lds_usage_bytes,
+            "name": self.name if self.name else "",
+        }
+
+    def from_dict(self, d: Dict):
+        self.a_type = DataType(d["a_type"])
+        self.b_type = DataType(d["b_type"])
+        self.cd_type = DataType(d["cd_type"])
+        self.scalar_type = DataType(d["scalar_type"])
+        self.wave_group = tuple(d["wave_group"])
+        self.trans_a = bool(d["trans_a"])
+        self.trans_b = bool(d["trans_b"])
+        self.mfma = tuple(d["mfma"])
+        self.wave_tiling = tuple(d["wave_tiling"])
+        self.depth_k = int(d["depth_k"])
+        self.vmem_stage = int(d.get("vmem_stage", 1))
+        self.wavefront_size = int(d["wavefront_size"])
+        self.name = d.get("name", "") or None
+        self._validate()
+        if int(d["lds_usage_bytes"]) != self.lds_usage_bytes:
+            raise RuntimeError(
+                f"lds_usage_bytes {d['lds_usage_bytes']} does not match the geometry ({self.lds_usage_bytes})")
+        return self
+
+    @classmethod
+    def from_toml(cls, path: str) -> "GemmSolutionConfig":
+        d = read_toml(path)
+        cfg = cls(d["a_type"], d["b_type"], d["cd_type"], d["scalar_type"], d["mfma"], d["wave_group"],
+                  d["wave_tiling"], d["depth_k"], d["trans_a"], d["trans_b"], d.get("vmem_stage", 1))
+        return cfg.from_dict(d)
+
+    def __repr__(self) -> str:
+        return (f"GemmSolutionConfig(mfma={self.mfma}, wave_group={self.wave_group}, "
+                f"wave_tiling={self.wave_tiling}, depth_k={self.depth_k}, vmem_stage={self.vmem_stage}, "
+                f"tile={self.tile_size})")
+
+
+class FunctionArgument:
+    """One kernel argument (generator.py:94-103)."""
+
+    def __init__(self, typename: str, name: str, offset: Optional[int], num_bytes: int):
+        self.typename = typename
+        self.name = name
+        self.offset = offset
+        self.num_bytes = num_bytes
+        self.address_space = "global" if typename == "global_buffer" else None
+
+
+FunctionArgumentList = List[FunctionArgument]
+
+# The explicit kernel arguments of generated_gemm, in order (generator.py:2604-2620).
+KERNEL_ARGUMENTS: Tuple[Tuple[str, str, int], ...] = (
+    ("global_buffer", "a", 8), ("global_buffer", "b", 8), ("global_buffer", "c", 8), ("global_buffer", "d", 8),
+    ("by_value", "m", 4), ("by_value", "n", 4), ("by_value", "k", 4),
+    ("by_value", "lda", 4), ("by_value", "ldb", 4), ("by_value", "ldc", 4), ("by_value", "ldd", 4),
+    ("by_value", "alpha", 4), ("by_value", "beta", 4),
+    ("by_value", "numWorkgroupX", 4), ("by_value", "numWorkgroupY", 4),
+)
+
+
+def default_arguments() -> FunctionArgumentList:
+    return [FunctionArgument(t, n, None, s) for t, n, s in KERNEL_ARGUMENTS]
+
+
+def kernarg_layout(args: FunctionArgumentList) -> List[Tuple[str, int, int]]:
+    """(name, offset, size) of each argument, naturally aligned, in order."""
+    out, off = [], 0
+    for arg in args:
+        align = arg.num_bytes
+        off = (off + align - 1) // align * align
+        out.append((arg.name, off, arg.num_bytes))
+        off += arg.num_bytes
+    return out
+
+
+def _check_arguments(args: FunctionArgumentList):
+    got = [(a.typename, a.name, a.num_bytes) for a in args]
+    if got != list(KERNEL_ARGUMENTS):
+        raise RuntimeError(f"generated_gemm takes exactly the reference's 15 arguments, got {got}")
+
+
+class GpuContext:
+    """Holds what ``gemm`` generated: the HIP source and its compile flags.
+
+    ``assembly()`` returns the gfx950 AMD assembly that hipcc produces for that
+    source (a build of this project's own code), which the GPU-free virtual
+    machine executes.
+    """
+
+    def __init__(self):
+        self.source: Optional[str] = None
+        self.arch: Optional[str] = None
+        self.name: Optional[str] = None
+        self.defines: Dict[str, int] = {}
+        self._asm: Optional[str] = None
+
+    def assembly(self) -> str:
+        if self._asm is None:
+            if self.source is None:
+                raise RuntimeError("gemm() has not generated a kernel into this context")
+            self._asm = compile_to_assembly(self.source, self.arch or "gfx950")
+        return self._asm
+
+
+def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str = "generated_gemm") -> Dict[str, object]:
+    pad_a = config.lds_pad_bytes[0] // 4
+    pad_b = config.lds_pad_bytes[1] // 4
+    return {
+        "SG_ATOM_M": config.mfma[0],
+        "SG_WG0": config.wave_group[0],
+        "SG_WG1": config.wave_group[1],
+        "SG_WT0": config.wave_tiling[0],
+        "SG_WT1": config.wave_tiling[1],
+        "SG_DK": config.depth_k,
+        "SG_NBUF": config.vmem_stage + 1,
+        "SG_WGM": opt.wgm,
+        "SG_XCD": opt.xcd,
+        "SG_MAPK": opt.map_k_idx,
+        "SG_PLR": opt.plr,
+        "SG_GW": opt.gw,
+        "SG_PAD_A": pad_a,
+        "SG_PAD_B": pad_b,
+        "SG_KERNEL_NAME": name,
+    }
+
+
+def gemm(
+    context: Optional[GpuContext],
+    name: str,
+    arch: str,
+    config: GemmSolutionConfig,
+    opt: GemmOptimizations,
+    args: FunctionArgumentList,
+) -> str:
+    """Returns the HIP source of one specialised kernel (generator.py:1056).
+
+    The text is the kernel template with the configuration prepended as
+    ``#define`` lines, so it compiles on its own.  If ``context`` is given it
+    also records the source there.
+    """
+    if arch not in SUPPORTED_ARCHS:
+        raise RuntimeError(f"Unsupported arch {arch!r}; this generator targets {SUPPORTED_ARCHS}")
+    _check_arguments(args)
+    defines = kernel_defines(config, opt, name)
+    with open(KERNEL_TEMPLATE, "r") as f:
+        template = f.read()
+    header = [f"// generated by generator.py for {arch}: {config!r} {opt!r}"]
+    header += [f"#define {k} {v}" for k, v in defines.items()]
+    src = "\n".join(header) + "\n" + template
+    if context is not None:
+        context.source = src
+        context.arch = arch
+        context.name = name
+        context.defines = defines
+        context._asm = None
+    return src
+
+
+def _offload_arch(arch: str) -> str:
+    return arch
+
+
+def compile_to_assembly(kern_str: str, arch: str = "gfx950") -> str:
+    """AMD assembly of a generated kernel (this project's own build)."""
+    with tempfile.TemporaryDirectory() as tmp:
+        src = os.path.join(tmp, "k.hip")
+        out = os.path.join(tmp, "k.s")
+        with open(src, "w") as f:
+            f.write(kern_str)
+        cmd = [DEFAULT_HIPCC_PATH, "-S", "--cuda-device-only", f"--offload-arch={_offload_arch(arch)}",
+               *HIPCC_KERNEL_FLAGS, src, "-o", out]
+        ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
+        if ret.returncode:
+            raise RuntimeError(f"hipcc -S failed:\n{ret.stderr.decode(errors='replace')}")
+        with open(out) as f:
+            return f.read()
+
+
+def _toml_value(v) -> str:
+    if isinstance(v, bool):
+        return "true" if v else "false"
+    if isinstance(v, int):
+        return str(v)
+    if isinstance(v, float):
+        return repr(v)
+    if isinstance(v, str):
+        esc = v.replace("\\", "\\\\").replace('"', '\\"')
+        return f'"{esc}"'
+    if isinstance(v, (list, tuple)):
+        return "[" + ", ".join(_toml_value(x) for x in v) + "]"
+    raise TypeError(f"unsupported TOML value {v!r}")
+
+
+def write_toml(d: Dict, path: str):
+    """Flat TOML writer (the subset tomli_w produced for the reference)."""
+    with open(path, "w") as f:
+        for k, v in d.items():
+            f.write(f"{k} = {_toml_value(v)}\n")
+
+
+def read_toml(path: str) -> Dict:
+    try:
+        import tomllib  # Python >= 3.11
+    except ImportError:  # pragma: no cover - depends on the interpreter
+        import tomli as tomllib
+    with open(path, "rb") as f:
+        return tomllib.load(f)
+
+
+def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_config: GemmSolutionConfig,
+            opt: Optional[GemmOptimizations] = None, extra_keys: Optional[Dict] = None,
+            verbose: bool = False) -> int:
+    """Builds ``<out>/<name>.co`` and writes ``<out>/<name>.toml`` (generator.py:2534-2569).
+
+    Returns 0 on success and the failing step's non-zero code otherwise; on
+    failure no ``.toml`` is written, so a stale pair is never left behind.
+    """
+    os.makedirs(output_folder, exist_ok=True)
+    src_path = os.path.join(output_folder, f"{kern_name}.hip")
+    co_path = os.path.join(output_folder, f"{kern_name}.co")
+    toml_path = os.path.join(output_folder, f"{kern_name}.toml")
+    with open(src_path, "w") as f:
+        f.write(kern_str)
+    tmp_co = co_path + ".tmp"
+    # a plain amdhsa ELF code object (no offload bundle), like the reference's .co
+    cmd = [DEFAULT_HIPCC_PATH, "--cuda-device-only", "-c", "--no-gpu-bundle-output",
+           f"--offload-arch={_offload_arch(arch)}", *HIPCC_KERNEL_FLAGS, src_path, "-o", tmp_co]
+    ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
+    if ret.returncode:
+        if verbose:
+            sys.stderr.write(ret.stderr.decode(errors="replace"))
+        if os.path.exists(tmp_co):
+            os.remove(tmp_co)
+        return ret.returncode
+    os.replace(tmp_co, co_path)
+    d = gemm_config.to_dict()
+    if not d["name"]:
+        d["name"] = kern_name
+    d["arch"] = arch
+    if opt is not None:
+        d.update(opt.to_dict())
+    if extra_keys:
+        d.update(extra_keys)
+    write_toml(d, toml_path)
+    return 0
+
+
+def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimizations,
+                 kern_name: str = "generated_gemm", arch: str = "gfx950", verbose: bool = True) -> Tuple[str, str]:
+    """gemm + compile; returns the (.co, .toml) paths or raises RuntimeError."""
+    # the exported symbol stays generated_gemm whatever the files are called
+    src = gemm(None, "generated_gemm", arch, config, opt, default_arguments())
+    rc = compile(kern_name, src, arch, output_folder, config, opt, verbose=verbose)
+    if rc:
+        raise RuntimeError(f"compile of {kern_name} failed with code {rc}")
+    return os.path.join(output_folder, f"{kern_name}.co"), os.path.join(output_folder, f"{kern_name}.toml")
+
+
+# Default instance of the CLI: the configuration the gfx950 tuner selected for
+# the 4096^3 headline problem.
+def default_config() -> Tuple[GemmSolutionConfig, GemmOptimizations]:
+    cfg = GemmSolutionConfig(DataType.FP32, DataType.FP32, DataType.FP32, DataType.FP32,
+                             MFMA_32x32x2, (2, 2), (4, 4), 16, False, False, vmem_stage=1)
+    opt = GemmOptimizations(1, wgm=4, plr=1, gw=0, map_k_idx=0, xcd=8)
+    return cfg, opt
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="Generate the gfx950 SGEMM code object and its .toml")
+    ap.add_argument(dest="output_folder", action="store", type=str, help="Output folder")
+    ap.add_argument("--arch", dest="arch", action="store", choices=list(SUPPORTED_ARCHS), default="gfx950")
+    args = ap.parse_args(argv)
+    cfg, opt = default_config()
+    src = gemm(None, "generated_gemm", args.arch, cfg, opt, default_arguments())
+    rc = compile("generated_gemm", src, args.arch, args.output_folder, cfg, opt, verbose=True)
+    if rc == 0:
+        print(f"wrote {args.output_folder}/generated_gemm.co and {args.output_folder}/generated_gemm.toml")
+    return rc
+
+
+if __name__ == "__main__":
+    sys.exit(main())

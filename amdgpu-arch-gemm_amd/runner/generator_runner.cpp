@@ -1,0 +1,149 @@
+// GeneratorRunner: benchmark and validate one generated gfx950 SGEMM code object.
+//
+//   GeneratorRunner <co> <toml> M N K <num_warmup_runs> <num_benchmark_runs> <validation_flag>
+//                   [seed] [dist] [alpha] [beta]
+//
+// The first eight arguments and the last three stdout lines
+// ("ASM gemm: <ms> ms", "Gflops: <x>", "GiB/s: <x>") are those of the reference
+// runner (README.md:84, generator_runner.cpp:192-283), which the tuner parses
+// (sgemm_tuner.py:115).  Differences, all deliberate:
+//   * inputs are seeded (sgemm_fill): A = matrix 0, B = matrix 1, C = matrix 2,
+//     with the optional [seed] (default 0) and [dist] (0 = U[-1,1), 1 = N(0,1));
+//     the reference's randomize() is unseeded (BufferUtils.hpp:6-16);
+//   * alpha = beta = 1 by default, as in the reference (generator_runner.cpp:219-220);
+//     [alpha] [beta] override them;
+//   * every HIP error is checked and reported; usage errors exit with -1 before
+//     any argument is touched (the reference reads argv first, :193-201);
+//   * the CPU reference is timed once and printed as such (the reference divides
+//     the single run by numRuns, :229), and validation uses the normwise
+//     criterion max|D - D_ref| / max|D_ref| <= 1e-5 * sqrt(K);
+//   * the naive HIP comparison kernel (:35-67, :246-265) is not run.
+// Exit code 0 = pass, -1 (255) = usage error, HIP error or validation failure.
+
+#include "sgemm_shim.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <iostream>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "cpu_reference.hpp"
+
+namespace {
+
+double gflops(uint32_t m, uint32_t n, uint32_t k, double ms) {  // generator_runner.cpp:75-77
+    return 2.0 * m * n * k / ms * 1e-6;
+}
+
+double mem_bw_gib(size_t m, size_t n, size_t k, double ms) {  // generator_runner.cpp:79-83
+    return (double)(m * k + n * k + 2 * m * n) * sizeof(float) / ms / 1024.0 / 1024.0;
+}
+
+bool parse_u32(const char* s, uint32_t* out) {
+    char* end = nullptr;
+    unsigned long long v = strtoull(s, &end, 10);
+    if (!s[0] || *end || v > 0xffffffffull) return false;
+    *out = (uint32_t)v;
+    return true;
+}
+
+int usage(const char* prog) {
+    std::cerr << "usage: " << prog
+              << " <co> <toml> M N K <num_warmup_runs> <num_benchmark_runs> <validation_flag>"
+                 " [seed] [dist] [alpha] [beta]\n";
+    return -1;
+}
+
+int shim_error(const char* what, int code) {
+    std::cerr << what << " failed (" << code << "): " << sgemm_last_error() << "\n";
+    return -1;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc < 9) return usage(argv[0]);
+    uint32_t m, n, k, warmup, runs, validate, seed = 0, dist = SGEMM_DIST_UNIFORM;
+    if (!parse_u32(argv[3], &m) || !parse_u32(argv[4], &n) || !parse_u32(argv[5], &k) ||
+        !parse_u32(argv[6], &warmup) || !parse_u32(argv[7], &runs) || !parse_u32(argv[8], &validate) ||
+        (argc > 9 && !parse_u32(argv[9], &seed)) || (argc > 10 && !parse_u32(argv[10], &dist)))
+        return usage(argv[0]);
+    float alpha = 1.0f, beta = 1.0f;
+    if (argc > 11) alpha = strtof(argv[11], nullptr);
+    if (argc > 12) beta = strtof(argv[12], nullptr);
+    if (runs == 0) runs = 1;
+
+    sgemm_handle* h = nullptr;
+    int r = sgemm_open(argv[1], argv[2], &h);
+    if (r != SGEMM_OK) return shim_error("sgemm_open", r);
+    r = sgemm_check_shape(h, m, n, k, m, k, m, m);
+    if (r != SGEMM_OK) {
+        std::cerr << sgemm_last_error() << "\n";
+        sgemm_close(h);
+        return -1;
+    }
+
+    std::vector<float> A((size_t)m * k), B((size_t)k * n), C((size_t)m * n), D((size_t)m * n, 0.0f);
+    if ((r = sgemm_fill(A.data(), A.size(), seed, 0, (int)dist)) != SGEMM_OK ||
+        (r = sgemm_fill(B.data(), B.size(), seed, 1, (int)dist)) != SGEMM_OK ||
+        (r = sgemm_fill(C.data(), C.size(), seed, 2, (int)dist)) != SGEMM_OK) {
+        sgemm_close(h);
+        return shim_error("sgemm_fill", r);
+    }
+
+    std::vector<float> ref;
+    if (validate) {
+        ref.assign((size_t)m * n, 0.0f);
+        const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        const auto t0 = std::chrono::steady_clock::now();
+        runner_cpu_gemm(A.data(), B.data(), C.data(), ref.data(), alpha, beta, m, n, k, threads);
+        const auto t1 = std::chrono::steady_clock::now();
+        std::cout << "cpuGemm func: " << std::chrono::duration<double, std::milli>(t1 - t0).count() << " ms ("
+                  << threads << " threads of " << std::thread::hardware_concurrency() << ")\n";
+    }
+
+    double ms = 0.0;
+    r = sgemm_run(h, A.data(), B.data(), C.data(), D.data(), m, n, k, alpha, beta, (int)warmup, (int)runs, &ms);
+    if (r != SGEMM_OK) {
+        sgemm_close(h);
+        return shim_error("sgemm_run", r);
+    }
+    sgemm_close(h);
+
+    int status = 0;
+    if (validate) {
+        double max_err = 0.0, max_ref = 0.0;
+        size_t worst = 0, bad = 0;
+        for (size_t i = 0; i < D.size(); ++i) {
+            const double e = std::fabs((double)D[i] - (double)ref[i]);
+            if (!(e <= max_err)) {  // also catches NaN
+                max_err = std::isnan(e) ? INFINITY : e;
+                worst = i;
+            }
+            max_ref = std::max(max_ref, std::fabs((double)ref[i]));
+            if (std::isnan(D[i]) != std::isnan(ref[i])) ++bad;
+        }
+        const double rel = max_ref > 0 ? max_err / max_ref : max_err;
+        const double tol = 1e-5 * std::sqrt((double)std::max<uint32_t>(k, 1));
+        const bool pass = rel <= tol && bad == 0;
+        std::cout << "max |D - D_ref| = " << max_err << " at index " << worst << " (gpu " << D[worst] << ", cpu "
+                  << ref[worst] << ")\n"
+                  << "normwise relative error = " << rel << " (tolerance 1e-5*sqrt(K) = " << tol << ")\n"
+                  << "# of mismatches: " << (pass ? 0 : 1) << "/1 (normwise)\n"
+                  << "validation: " << (pass ? "PASS" : "FAIL") << "\n";
+        status = pass ? 0 : -1;
+    }
+    const double tflops = gflops(m, n, k, ms) * 1e-3;
+    std::cout << "TFLOP/s: " << tflops << " (" << 100.0 * tflops / 157.3 << "% of the 157.3 TFLOP/s FP32 MFMA peak)\n";
+    std::cout << "ASM gemm: " << ms << " ms\n"
+              << "Gflops: " << gflops(m, n, k, ms) << '\n'
+              << "GiB/s: " << mem_bw_gib(m, n, k, ms) << '\n';
+    return status;
+}

@@ -1,0 +1,258 @@
+"""ctypes binding of libsgemm_shim.so (include/sgemm_shim.h).
+
+This is the only way Python reaches HIP in this package: no torch, no hip
+Python bindings.  Every call checks the return code and raises
+``SgemmError`` with the library's message.  There is no CPU fallback: if the
+library or a GPU is missing, calls fail loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(_HERE, "libsgemm_shim.so")
+
+SGEMM_DIST_UNIFORM = 0
+SGEMM_DIST_NORMAL = 1
+SGEMM_DIST_ZERO = 2
+
+# every symbol the header declares, with (restype, argtypes)
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+_LAUNCH_ARGS = [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f32, _f32]
+
+
+class KernelInfo(ctypes.Structure):
+    _fields_ = [
+        ("mfma", ctypes.c_int * 4),
+        ("wave_group", ctypes.c_int * 2),
+        ("wave_tiling", ctypes.c_int * 2),
+        ("depth_k", ctypes.c_int),
+        ("vmem_stage", ctypes.c_int),
+        ("wavefront_size", ctypes.c_int),
+        ("lds_usage_bytes", ctypes.c_int),
+        ("tile_m", ctypes.c_int),
+        ("tile_n", ctypes.c_int),
+        ("workitems", ctypes.c_int),
+    ]
+
+
+SIGNATURES = {
+    "sgemm_last_error": (ctypes.c_char_p, []),
+    "sgemm_abi_version": (_int, []),
+    "sgemm_device_info": (_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                                 ctypes.POINTER(_int)]),
+    "sgemm_open": (_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "sgemm_close": (None, [_vp]),
+    "sgemm_get_info": (_int, [_vp, ctypes.POINTER(KernelInfo)]),
+    "sgemm_check_shape": (_int, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "sgemm_malloc": (_int, [ctypes.POINTER(_vp), ctypes.c_size_t]),
+    "sgemm_free": (_int, [_vp]),
+    "sgemm_memcpy_h2d": (_int, [_vp, _vp, ctypes.c_size_t]),
+    "sgemm_memcpy_d2h": (_int, [_vp, _vp, ctypes.c_size_t]),
+    "sgemm_memset": (_int, [_vp, _int, ctypes.c_size_t]),
+    "sgemm_launch": (_int, _LAUNCH_ARGS),
+    "sgemm_time": (_int, _LAUNCH_ARGS + [_int, _int, ctypes.POINTER(_f32)]),
+    "sgemm_time_each": (_int, _LAUNCH_ARGS + [_int, ctypes.POINTER(_f32)]),
+    "sgemm_synchronize": (_int, [_vp]),
+    "sgemm_run": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _f32, _int, _int,
+                         ctypes.POINTER(ctypes.c_double)]),
+    "sgemm_fill": (_int, [_vp, ctypes.c_size_t, ctypes.c_uint64, _u32, _int]),
+}
+
+
+class SgemmError(RuntimeError):
+    def __init__(self, func: str, code: int, message: str):
+        super().__init__(f"{func} failed ({code}): {message}")
+        self.func = func
+        self.code = code
+        self.message = message
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: str = LIBRARY_PATH) -> ctypes.CDLL:
+    """Loads the shim once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(func: str, code: int):
+    if code != 0:
+        msg = load_library().sgemm_last_error().decode(errors="replace")
+        raise SgemmError(func, code, msg)
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def fill(count: int, seed: int, matrix_id: int, dist: int = SGEMM_DIST_UNIFORM) -> np.ndarray:
+    """Seeded input values (float32), identical on every host for a given (seed, matrix_id, i)."""
+    out = np.empty(int(count), dtype=np.float32)
+    _check("sgemm_fill", load_library().sgemm_fill(_ptr(out), out.size, int(seed), int(matrix_id), int(dist)))
+    return out
+
+
+def fill_matrix(rows: int, cols: int, seed: int, matrix_id: int, dist: int = SGEMM_DIST_UNIFORM) -> np.ndarray:
+    """Column-major rows x cols matrix as a Fortran-ordered float32 array."""
+    return fill(rows * cols, seed, matrix_id, dist).reshape(cols, rows).T
+
+
+def device_info() -> dict:
+    lib = load_library()
+    name = ctypes.create_string_buffer(256)
+    cus, clk, lds = _int(), _int(), _int()
+    _check("sgemm_device_info", lib.sgemm_device_info(name, 256, ctypes.byref(cus), ctypes.byref(clk),
+                                                      ctypes.byref(lds)))
+    return {"name": name.value.decode(), "compute_units": cus.value, "clock_khz": clk.value,
+            "lds_per_block": lds.value}
+
+
+class DeviceBuffer:
+    """Device allocation owned by Python; freed on close() or garbage collection."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        _check("sgemm_malloc", load_library().sgemm_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        # 2-D arrays are stored column-major, whatever their numpy order
+        flat = np.ascontiguousarray(np.asarray(a, dtype=np.float32).ravel(order="F"))
+        buf = cls(flat.nbytes)
+        buf.upload(flat)
+        return buf
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("array larger than the device buffer")
+        _check("sgemm_memcpy_h2d", load_library().sgemm_memcpy_h2d(self.ptr, _ptr(a), a.nbytes))
+
+    def download(self, count: Optional[int] = None) -> np.ndarray:
+        count = self.nbytes // 4 if count is None else int(count)
+        out = np.empty(count, dtype=np.float32)
+        _check("sgemm_memcpy_d2h", load_library().sgemm_memcpy_d2h(_ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def zero(self):
+        _check("sgemm_memset", load_library().sgemm_memset(self.ptr, 0, self.nbytes))
+
+    def close(self):
+        if self.ptr:
+            load_library().sgemm_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Kernel:
+    """One loaded code object (.co + .toml)."""
+
+    def __init__(self, co_path: str, toml_path: str):
+        lib = load_library()
+        h = _vp()
+        _check("sgemm_open", lib.sgemm_open(co_path.encode(), toml_path.encode(), ctypes.byref(h)))
+        self.handle = h.value
+        self.co_path = co_path
+        self.toml_path = toml_path
+        info = KernelInfo()
+        _check("sgemm_get_info", lib.sgemm_get_info(self.handle, ctypes.byref(info)))
+        self.info = info
+
+    @property
+    def tile(self) -> Tuple[int, int, int]:
+        return self.info.tile_m, self.info.tile_n, self.info.depth_k
+
+    def check_shape(self, m, n, k, lda=None, ldb=None, ldc=None, ldd=None) -> Optional[str]:
+        lib = load_library()
+        rc = lib.sgemm_check_shape(self.handle, m, n, k, lda or m, ldb or k, ldc or m, ldd or m)
+        return None if rc == 0 else lib.sgemm_last_error().decode()
+
+    def _args(self, a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta):
+        cp = c.ptr if c is not None else None
+        return (self.handle, a.ptr if a is not None else None, b.ptr if b is not None else None, cp, d.ptr,
+                m, n, k, lda or m, ldb or k, ldc or m, ldd or m, alpha, beta)
+
+    def launch(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, lda=None, ldb=None, ldc=None, ldd=None):
+        _check("sgemm_launch", load_library().sgemm_launch(*self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd,
+                                                                         alpha, beta)))
+
+    def time(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, warmup=1, runs=10,
+             lda=None, ldb=None, ldc=None, ldd=None) -> float:
+        """Event time (ms) of `runs` back-to-back launches after `warmup`."""
+        total = _f32()
+        _check("sgemm_time", load_library().sgemm_time(*self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd,
+                                                                     alpha, beta), warmup, runs, ctypes.byref(total)))
+        return float(total.value)
+
+    def time_each(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, runs=10,
+                  lda=None, ldb=None, ldc=None, ldd=None) -> np.ndarray:
+        out = np.zeros(runs, dtype=np.float32)
+        _check("sgemm_time_each", load_library().sgemm_time_each(
+            *self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta), runs,
+            out.ctypes.data_as(ctypes.POINTER(_f32))))
+        return out
+
+    def synchronize(self):
+        _check("sgemm_synchronize", load_library().sgemm_synchronize(self.handle))
+
+    def run(self, A: np.ndarray, B: np.ndarray, C: Optional[np.ndarray], m: int, n: int, k: int,
+            alpha: float = 1.0, beta: float = 0.0, warmup: int = 0, runs: int = 1) -> Tuple[np.ndarray, float]:
+        """Host-buffer flow: returns (D as a column-major m x n array, ms per run)."""
+        A = np.asfortranarray(A, dtype=np.float32)
+        B = np.asfortranarray(B, dtype=np.float32)
+        if A.shape != (m, k) or B.shape != (k, n):
+            raise ValueError(f"A must be {m}x{k} and B {k}x{n}, got {A.shape} and {B.shape}")
+        cptr = None
+        if C is not None:
+            C = np.asfortranarray(C, dtype=np.float32)
+            if C.shape != (m, n):
+                raise ValueError(f"C must be {m}x{n}")
+            cptr = C.ctypes.data
+        D = np.zeros((m, n), dtype=np.float32, order="F")
+        ms = ctypes.c_double()
+        _check("sgemm_run", load_library().sgemm_run(self.handle, A.ctypes.data, B.ctypes.data, cptr, D.ctypes.data,
+                                                     m, n, k, alpha, beta, warmup, runs, ctypes.byref(ms)))
+        return D, ms.value
+
+    def close(self):
+        if getattr(self, "handle", None):
+            load_library().sgemm_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,204 @@
+"""Headline benchmark: FP32 column-major NN SGEMM at 4096^3 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3]
+
+A step is one launch of the tuned gfx950 kernel on the BASELINE.json config
+(M = N = K = 4096, A and B uniform[-1, 1) from seed 2, C = 0, alpha = 1,
+beta = 0) with A, B and D resident in HBM.  W untimed launches, then K timed
+launches bracketed by device synchronisation; the host clock gives
+ms_per_step and `value` (TFLOP/s), HIP events on the kernel's stream give the
+per-launch kernel time used for the roofline fraction.
+
+The CPU baseline is the reference's own cpuGemm (compiled from its source into
+oracle/_ref) -- or this project's C restatement of it when that was not built --
+timed single-threaded on a column slice D[:, :s] of the same workload (the
+slice is itself a cpuGemm call with n = s, so per-output work and memory
+pattern are unchanged); s is calibrated to about 15 s of CPU time.  The slice
+is also compared with the GPU result (normwise error, 1e-5 * sqrt(K) bar).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "amdgpu-arch-gemm_amd"))
+
+import numpy as np  # noqa: E402
+
+from generator import catalog  # noqa: E402
+from shim import sgemm_shim as S  # noqa: E402
+
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix peak (256 CU x 256 FLOP/clk x 2.4 GHz)
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (m, n, k, seed, dist)
+    "cfg3": (4096, 4096, 4096, 2, S.SGEMM_DIST_UNIFORM),
+    "cfg2": (1024, 1024, 1024, 1, S.SGEMM_DIST_UNIFORM),
+    "cfg4": (8192, 8192, 256, 3, S.SGEMM_DIST_NORMAL),
+    "cfg5": (16384, 128, 4096, 4, S.SGEMM_DIST_UNIFORM),
+}
+
+
+def log(msg: str):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def read_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if ":" in line and not line.startswith("#"):
+                key, val = line.split(":", 1)
+                vals[key.strip()] = val.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
+    """Times the reference cpuGemm (or the oracle port) on a column slice."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    use_ref = oracle.ref_lib() is not None
+    gemm = oracle.ref_cpu_gemm if use_ref else oracle.cpu_gemm
+    kind = "reference" if use_ref else "port"
+
+    def timed(cols):
+        Bs = np.asfortranarray(B[:, :cols])
+        t0 = time.perf_counter()
+        D = gemm(A, Bs, None, 1.0, 0.0)
+        return time.perf_counter() - t0, D
+
+    probe = 4
+    t_probe, _ = timed(probe)
+    cols = int(max(probe, min(n, round(target_s / max(t_probe / probe, 1e-9)))))
+    log(f"cpu baseline ({kind}): {probe} columns took {t_probe:.2f} s; timing {cols} columns")
+    t, D = timed(cols)
+    tflops = 2.0 * m * cols * k / t / 1e12
+    err = oracle.normwise_error(D_gpu[:, :cols], D)
+    return {
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"D[:, :{cols}] of the {m}x{n}x{k} workload (n={cols} columns), single thread, {t:.1f} s",
+        "seconds": t,
+    }, {"normwise_error": err, "tolerance": oracle.tolerance(k), "columns_checked": cols,
+        "pass": bool(err <= oracle.tolerance(k))}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
+    ap.add_argument("--kernel", default=None, help="catalog instance (default: catalog.select)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build's SGEMM runs on a single MI355X "
+              f"(--gpus {args.gpus} requested). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    m, n, k, seed, dist = WORKLOADS[args.workload]
+    name = args.kernel or catalog.select(m, n, k)
+    co, toml = catalog.paths(name)
+    info = S.device_info()
+    log(f"device: {info}")
+    log(f"workload {args.workload}: {m}x{n}x{k} seed {seed} dist {dist}; kernel {name}")
+
+    A = S.fill_matrix(m, k, seed, 0, dist)
+    B = S.fill_matrix(k, n, seed, 1, dist)
+    kern = S.Kernel(co, toml)
+    dA, dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
+    dD = S.DeviceBuffer(m * n * 4)
+    dD.zero()
+
+    for _ in range(args.warmup):
+        kern.launch(dA, dB, None, dD, m, n, k, 1.0, 0.0)
+    kern.synchronize()
+
+    # timed region: exactly `steps` launches, device idle on both sides
+    t0 = time.perf_counter()
+    event_ms = kern.time(dA, dB, None, dD, m, n, k, 1.0, 0.0, warmup=0, runs=args.steps)
+    kern.synchronize()
+    wall_s = time.perf_counter() - t0
+
+    flops = 2.0 * m * n * k
+    ms_per_step = wall_s * 1e3 / args.steps
+    value = flops / (wall_s / args.steps) / 1e12
+    kernel_ms = event_ms / args.steps
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    per_launch = kern.time_each(dA, dB, None, dD, m, n, k, 1.0, 0.0, runs=20)
+    median_ms = float(np.median(per_launch))
+    log(f"wall {ms_per_step:.4f} ms/step = {value:.2f} TFLOP/s; events {kernel_ms:.4f} ms/launch = "
+        f"{achieved:.2f} TFLOP/s; per-launch median {median_ms:.4f} ms")
+
+    D = dD.download().reshape(n, m).T
+    alg_bytes = 4.0 * (m * k + k * n + m * n)
+    traffic = read_traffic(name, args.workload)
+    line = {
+        "metric": "FP32 SGEMM TFLOP/s at 4096^3 NN; % of MI355X FP32 MFMA peak",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"sgemm_nn_colmajor_{m}x{n}x{k}",
+            "m": m, "n": n, "k": k, "seed": seed,
+            "dist": "uniform[-1,1)" if dist == S.SGEMM_DIST_UNIFORM else "normal(0,1)",
+            "alpha": 1.0, "beta": 0.0,
+            "kernel": name,
+            "pct_of_fp32_mfma_peak": round(100.0 * value / FP32_MFMA_PEAK_TFLOPS, 2),
+            "device": info["name"],
+            "peak_sclk_mhz": info["clock_khz"] / 1000.0,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel_ms_mean": round(kernel_ms, 5),
+            "kernel_ms_median": round(median_ms, 5),
+            "algorithmic_bytes": alg_bytes,
+            "algorithmic_gbs": round(alg_bytes / (kernel_ms * 1e-3) / 1e9, 1),
+        },
+    }
+    if not args.no_cpu_baseline and args.gpus == 1:
+        cpu, parity = cpu_baseline(A, B, D, m, n, k, args.cpu_seconds)
+        line["cpu_baseline"] = cpu
+        line["parity"] = parity
+    else:
+        line["cpu_baseline"] = None
+    kern.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

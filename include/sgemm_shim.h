@@ -1,0 +1,145 @@
+/*
+ * C-ABI of the gfx950 SGEMM host library (libsgemm_shim.so).
+ *
+ * The reference has no library boundary: its Python side shells out to the
+ * GeneratorRunner executable (tuner/sgemm_tuner.py:112) and the executable
+ * does everything in main().  This header is that executable's work split
+ * into plain C entry points -- plain pointers and sizes, no C++ or torch
+ * types -- so that Python (ctypes), the GeneratorRunner executable and any
+ * other host language bind the same code.  Each entry point names the
+ * reference code it replaces.
+ *
+ * Conventions
+ *   - Every function returns 0 on success.  A positive value is the
+ *     hipError_t of the failing HIP call; a negative value is one of the
+ *     SGEMM_E_* codes below.  sgemm_last_error() returns a message for the
+ *     last failure on the calling thread.  Nothing throws across this ABI.
+ *   - The caller owns host arrays.  Device buffers come from sgemm_malloc and
+ *     are owned by the caller until sgemm_free.  A handle owns its code
+ *     object module, its stream and its events.
+ *   - One handle is used by one thread at a time.  All work of a handle runs
+ *     in order on the handle's stream (default priority).
+ *   - Matrices are column-major FP32: A is m x k (lda), B is k x n (ldb),
+ *     C and D are m x n (ldc, ldd).  D = alpha * A * B + beta * C; C is not
+ *     read when beta == 0.
+ */
+#ifndef SGEMM_SHIM_H
+#define SGEMM_SHIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGEMM_SHIM_ABI_VERSION 1
+
+enum {
+    SGEMM_OK = 0,
+    SGEMM_E_INVALID = -1,     /* bad argument (null pointer, bad distribution, ...) */
+    SGEMM_E_IO = -2,          /* a file could not be read */
+    SGEMM_E_CONFIG = -3,      /* .toml missing a key or describing an unsupported kernel */
+    SGEMM_E_SHAPE = -4,       /* problem shape / leading dimensions the kernel cannot run */
+    SGEMM_E_NO_DEVICE = -5    /* no HIP device visible */
+};
+
+enum {
+    SGEMM_DIST_UNIFORM = 0,   /* U[-1, 1): exact multiples of 2^-23 */
+    SGEMM_DIST_NORMAL = 1,    /* N(0, 1) by Box-Muller on pairs of uniforms */
+    SGEMM_DIST_ZERO = 2       /* all zeros */
+};
+
+typedef struct sgemm_handle sgemm_handle;
+
+/* Kernel configuration read from the .toml (generator.py:1001-1017 schema). */
+typedef struct sgemm_kernel_info {
+    int mfma[4];          /* atom (M, N, blocks, K) */
+    int wave_group[2];
+    int wave_tiling[2];
+    int depth_k;
+    int vmem_stage;
+    int wavefront_size;
+    int lds_usage_bytes;
+    int tile_m;           /* MT0 = mfma[0] * wave_group[0] * wave_tiling[0] */
+    int tile_n;           /* MT1 = mfma[1] * wave_group[1] * wave_tiling[1] */
+    int workitems;        /* wave_group[0] * wave_group[1] * wavefront_size */
+} sgemm_kernel_info;
+
+/* Message of the last failure on this thread ("" if none). */
+const char* sgemm_last_error(void);
+
+/* ABI version of the loaded library (SGEMM_SHIM_ABI_VERSION). */
+int sgemm_abi_version(void);
+
+/* Device 0 properties: name, compute units, peak engine clock (kHz), LDS per
+ * work-group (bytes).  Any output pointer may be null.
+ * Replaces nothing in the reference (it never queries the device). */
+int sgemm_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz, int* lds_per_block);
+
+/* Loads <co_path> (symbol "generated_gemm") and its <toml_path> config.
+ * Replaces getAsmKernelConfig + prepareASMKernel (generator_runner.cpp:100-124, :69-73). */
+int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out);
+
+/* Unloads the module and releases the stream and events (generator_runner.cpp:318). */
+void sgemm_close(sgemm_handle* h);
+
+/* Copies the handle's kernel configuration (generator_runner.cpp:127-153 geometry). */
+int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info);
+
+/* Returns SGEMM_OK if the kernel can run this problem, SGEMM_E_SHAPE with a
+ * message otherwise (m % MT0, n % MT1, k % depth_k, leading dimensions). */
+int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
+                      uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd);
+
+/* Device memory (generator_runner.cpp:236-242, :291, :319-322). */
+int sgemm_malloc(void** dptr, size_t bytes);
+int sgemm_free(void* dptr);
+int sgemm_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int sgemm_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int sgemm_memset(void* dptr, int value, size_t bytes);
+
+/* Enqueues one launch on the handle's stream; does not wait.
+ * Replaces makeKernelArguments + launchASMKernel (generator_runner.cpp:126-190):
+ * the same 80-byte kernarg buffer, passed through hipModuleLaunchKernel's
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER with a grid of (ceil(m/MT0), ceil(n/MT1)) blocks. */
+int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                 uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                 float alpha, float beta);
+
+/* `warmup` untimed launches, then `runs` launches bracketed by HIP events on
+ * the handle's stream; *total_ms is the event time of all `runs` launches.
+ * Replaces the timed loop of generator_runner.cpp:270-283. */
+int sgemm_time(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+               uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+               float alpha, float beta, int warmup, int runs, float* total_ms);
+
+/* Like sgemm_time but brackets every launch with its own event pair and
+ * writes `runs` per-launch times (ms) to per_launch_ms. */
+int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                    float alpha, float beta, int runs, float* per_launch_ms);
+
+/* Waits for all work of the handle's stream. */
+int sgemm_synchronize(sgemm_handle* h);
+
+/* Whole runner flow on host buffers with lda = m, ldb = k, ldc = ldd = m:
+ * allocate, upload A, B (and C when beta != 0), warm up, time `runs`
+ * launches, download D, free.  *ms_per_run = event time / runs.
+ * Replaces main()'s device part (generator_runner.cpp:232-291). */
+int sgemm_run(sgemm_handle* h, const float* A, const float* B, const float* C, float* D,
+              uint32_t m, uint32_t n, uint32_t k, float alpha, float beta,
+              int warmup, int runs, double* ms_per_run);
+
+/* Fills host[0..count) with the seeded generator: element i of matrix
+ * `matrix_id` under `seed` is a pure function of (seed, matrix_id, i), so any
+ * slice can be regenerated independently.  Replaces the unseeded randomize()
+ * of BufferUtils.hpp:6-16 (same U[-1, 1) range). */
+int sgemm_fill(float* host, size_t count, uint64_t seed, uint32_t matrix_id, int dist);
+
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGEMM_SHIM_H */
