@@ -586,7 +586,8 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     tmp_co = co_path + ".tmp"
     # a plain amdhsa ELF code object (no offload bundle), like the reference's .co
     cmd = [DEFAULT_HIPCC_PATH, "--cuda-device-only", "-c", "--no-gpu-bundle-output",
-           f"--offload-arch={_offload_arch(arch)}", *HIPCC_KERNEL_FLAGS, src_path, "-o", tmp_co]
+           f"--offload-arch={_offload_arch(arch)}", *HIPCC_KERNEL_FLAGS,
+           "-Rpass-analysis=kernel-resource-usage", src_path, "-o", tmp_co]
     ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
     if ret.returncode:
         if verbose:
@@ -601,10 +602,38 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     d["arch"] = arch
     if opt is not None:
         d.update(opt.to_dict())
+    d.update(parse_resource_usage(ret.stderr.decode(errors="replace")))
     if extra_keys:
         d.update(extra_keys)
     write_toml(d, toml_path)
     return 0
+
+
+_RESOURCE_KEYS = {
+    "VGPRs": "vgprs",
+    "AGPRs": "agprs",
+    "TotalSGPRs": "sgprs",
+    "ScratchSize [bytes/lane]": "scratch_bytes_per_lane",
+    "Occupancy [waves/SIMD]": "occupancy_waves_per_simd",
+    "LDS Size [bytes/block]": "lds_bytes_compiled",
+}
+
+
+def parse_resource_usage(remarks: str) -> Dict[str, int]:
+    """The compiler's kernel-resource-usage remark as integer TOML keys."""
+    out: Dict[str, int] = {}
+    for line in remarks.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        for label, key in _RESOURCE_KEYS.items():
+            if body.startswith(label + ":"):
+                val = body[len(label) + 1:].split("[")[0].strip()
+                try:
+                    out[key] = int(val)
+                except ValueError:
+                    pass
+    return out
 
 
 def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimizations,

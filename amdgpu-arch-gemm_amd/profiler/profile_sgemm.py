@@ -1,0 +1,222 @@
+"""rocprofv3 measurement of one SGEMM kernel instance on one workload.
+
+    python amdgpu-arch-gemm_amd/profiler/profile_sgemm.py --kernel NAME \
+        --workload cfg3 --out gpurun_out/prof_cfg3 [--summary profiles/NAME_cfg3.md]
+
+This script never touches the GPU itself: every measurement is a child
+process -- rocprofv3 wrapping the GeneratorRunner executable (the product's
+CLI, validation off) or the copy_probe calibration kernel -- each under its own
+time limit.  Passes, one rocprofv3 run each (counters are never mixed with
+tracing, and no pass asks for more than the hardware collects at once):
+
+  1. --kernel-trace --stats          kernel durations
+  2. --pmc FETCH_SIZE                HBM read KiB per dispatch
+  3. --pmc WRITE_SIZE                HBM write KiB per dispatch
+  4. --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES
+                                     MFMA utilisation and the effective clock
+  5. --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE
+  6./7. FETCH_SIZE and WRITE_SIZE of copy_probe (a plain copy of a known byte
+     count), whose ratio to the true bytes scales the SGEMM's counters.
+
+The summary (markdown) lists the commands and the figures; a one-line
+``<kernel>_<workload>_traffic.txt`` next to it carries the scaled HBM bytes per
+launch that bench.py reports as roofline.traffic.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+import shlex
+import statistics
+import subprocess
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+ROOT = os.path.dirname(PKG)
+sys.path.insert(0, PKG)
+
+from generator import catalog  # noqa: E402
+
+RUNNER = os.path.join(PKG, "runner", "GeneratorRunner")
+PROBE = os.path.join(HERE, "copy_probe")
+SIMD_PER_CU = 4
+PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+PROBE_BYTES = 1 << 30
+
+WORKLOADS = {
+    "cfg2": (1024, 1024, 1024, 1, 0),
+    "cfg3": (4096, 4096, 4096, 2, 0),
+    "cfg4": (8192, 8192, 256, 3, 1),
+    "cfg5": (16384, 128, 4096, 4, 0),
+}
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def run(cmd, timeout):
+    log("+ " + " ".join(shlex.quote(c) for c in cmd))
+    t0 = time.time()
+    ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=timeout)
+    out = ret.stdout.decode(errors="replace")
+    log(f"  rc={ret.returncode} in {time.time() - t0:.1f} s")
+    if ret.returncode != 0:
+        log(out[-3000:])
+        raise RuntimeError(f"command failed with rc={ret.returncode}: {cmd[0]}")
+    return out
+
+
+def find(out_dir, pattern):
+    hits = sorted(glob.glob(os.path.join(out_dir, "**", pattern), recursive=True))
+    if not hits:
+        raise RuntimeError(f"no {pattern} under {out_dir}")
+    return hits[-1]
+
+
+def counters_per_dispatch(csv_path, kernel_substr):
+    """{counter: [value per dispatch]} for dispatches whose kernel name matches."""
+    per = {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if kernel_substr not in row.get("Kernel_Name", ""):
+                continue
+            per.setdefault(row["Counter_Name"], {})[row["Dispatch_Id"]] = float(row["Counter_Value"])
+    return {k: [v[d] for d in sorted(v, key=int)] for k, v in per.items()}
+
+
+def kernel_stats(csv_path, kernel_substr):
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if kernel_substr in row["Name"]:
+                return {"calls": int(row["Calls"]), "avg_ns": float(row["AverageNs"]),
+                        "min_ns": float(row["MinNs"]), "max_ns": float(row["MaxNs"])}
+    raise RuntimeError(f"{kernel_substr} not in {csv_path}")
+
+
+def rocprof(args, out_dir, program, timeout):
+    cmd = ["rocprofv3", *args, "--output-format", "csv", "-d", out_dir, "-o", "run", "--", *program]
+    return run(["timeout", "-s", "KILL", str(timeout), *cmd], timeout + 30)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--kernel", required=True)
+    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
+    ap.add_argument("--out", required=True, help="raw rocprofv3 output folder (e.g. under gpurun_out/)")
+    ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
+    ap.add_argument("--runs", type=int, default=5)
+    ap.add_argument("--cus", type=int, default=256)
+    args = ap.parse_args()
+
+    m, n, k, seed, dist = WORKLOADS[args.workload]
+    co, toml = catalog.paths(args.kernel)
+    os.makedirs(args.out, exist_ok=True)
+    runner = [RUNNER, co, toml, str(m), str(n), str(k), "1", str(args.runs), "0", str(seed), str(dist), "1", "0"]
+    probe = [PROBE, str(PROBE_BYTES), "3"]
+    cmds = {}
+
+    d = os.path.join(args.out, "trace")
+    rocprof(["--kernel-trace", "--stats"], d, runner, 300)
+    cmds["trace"] = "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o run -- " + " ".join(
+        os.path.relpath(c, ROOT) if os.path.isabs(c) else c for c in runner)
+    ks = kernel_stats(find(d, "run_kernel_stats.csv"), "generated_gemm")
+
+    passes = {
+        "fetch": ["FETCH_SIZE"],
+        "write": ["WRITE_SIZE"],
+        "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES"],
+        "lds": ["SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"],
+    }
+    values = {}
+    for key, counters in passes.items():
+        d = os.path.join(args.out, f"pmc_{key}")
+        rocprof(["--pmc", *counters], d, runner, 120)
+        cmds[key] = f"rocprofv3 --pmc {' '.join(counters)} --output-format csv -d <out>/pmc_{key} -o run -- <runner>"
+        per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "generated_gemm")
+        for c in counters:
+            if c not in per:
+                raise RuntimeError(f"counter {c} missing from pass {key}")
+            values[c] = per[c]
+    probe_vals = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(args.out, f"probe_{c.lower()}")
+        rocprof(["--pmc", c], d, probe, 120)
+        per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "copy_probe")
+        probe_vals[c] = per[c]
+
+    med = {c: statistics.median(v) for c, v in values.items()}
+    probe_kib = PROBE_BYTES / 1024.0
+    fetch_scale = probe_kib / statistics.median(probe_vals["FETCH_SIZE"])
+    write_scale = probe_kib / statistics.median(probe_vals["WRITE_SIZE"])
+    fetch_bytes = med["FETCH_SIZE"] * 1024.0 * fetch_scale
+    write_bytes = med["WRITE_SIZE"] * 1024.0 * write_scale
+    traffic = fetch_bytes + write_bytes
+    avg_s = ks["avg_ns"] * 1e-9
+    flops = 2.0 * m * n * k
+    alg_bytes = 4.0 * (m * k + k * n + m * n)
+    simds = args.cus * SIMD_PER_CU
+    mfma_util = 100.0 * med["SQ_VALU_MFMA_BUSY_CYCLES"] / (med["GRBM_GUI_ACTIVE"] * simds)
+    clock_mhz = med["GRBM_GUI_ACTIVE"] / avg_s / 1e6
+    lds_rate = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
+    tflops = flops / avg_s / 1e12
+    clock_peak = args.cus * 256 * clock_mhz * 1e6 / 1e12
+
+    summary = args.summary or os.path.join(args.out, "summary.md")
+    os.makedirs(os.path.dirname(os.path.abspath(summary)), exist_ok=True)
+    lines = [
+        f"# rocprofv3: `{args.kernel}` on {args.workload} ({m}x{n}x{k}, seed {seed}, "
+        f"{'N(0,1)' if dist else 'U[-1,1)'}, alpha=1, beta=0)",
+        "",
+        "Command (from the repository root on the GPU box):",
+        "",
+        f"    python amdgpu-arch-gemm_amd/profiler/profile_sgemm.py --kernel {args.kernel} "
+        f"--workload {args.workload} --out gpurun_out/prof_{args.workload} --summary {os.path.relpath(summary, ROOT)}",
+        "",
+        "which runs, each in its own process (`<runner>` = `"
+        + " ".join(os.path.relpath(c, ROOT) if os.path.isabs(c) else c for c in runner) + "`):",
+        "",
+        f"    {cmds['trace']}",
+        *[f"    {cmds[k2]}" for k2 in passes],
+        f"    rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE ... -- amdgpu-arch-gemm_amd/profiler/copy_probe {PROBE_BYTES} 3",
+        "",
+        "| figure | value |",
+        "|---|---|",
+        f"| kernel-trace calls / avg / min / max | {ks['calls']} / {ks['avg_ns'] / 1e3:.2f} us / "
+        f"{ks['min_ns'] / 1e3:.2f} us / {ks['max_ns'] / 1e3:.2f} us |",
+        f"| achieved | {tflops:.2f} TFLOP/s = {100 * tflops / PEAK_TFLOPS:.1f}% of {PEAK_TFLOPS} (nominal) |",
+        f"| effective clock (GRBM_GUI_ACTIVE / duration) | {clock_mhz:.0f} MHz -> clock-adjusted peak "
+        f"{clock_peak:.1f} TFLOP/s, achieved {100 * tflops / clock_peak:.1f}% of it |",
+        f"| MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (GRBM_GUI_ACTIVE x {simds} SIMDs) | {mfma_util:.1f}% |",
+        f"| SQ_BUSY_CYCLES (median per dispatch) | {med['SQ_BUSY_CYCLES']:.4g} |",
+        f"| LDS bank conflicts / conflict-free accesses (SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE) | "
+        f"{lds_rate:.4f} ({med['SQ_LDS_BANK_CONFLICT']:.4g} / {med['SQ_LDS_IDX_ACTIVE']:.4g}) |",
+        f"| FETCH_SIZE / WRITE_SIZE raw (KiB per dispatch, median) | {med['FETCH_SIZE']:.1f} / {med['WRITE_SIZE']:.1f} |",
+        f"| copy_probe calibration ({PROBE_BYTES} B read + written) | FETCH_SIZE {statistics.median(probe_vals['FETCH_SIZE']):.1f} KiB "
+        f"(scale {fetch_scale:.4f}), WRITE_SIZE {statistics.median(probe_vals['WRITE_SIZE']):.1f} KiB (scale {write_scale:.4f}) |",
+        f"| HBM traffic per launch (scaled) | read {fetch_bytes / 1e6:.1f} MB + write {write_bytes / 1e6:.1f} MB = "
+        f"{traffic / 1e6:.1f} MB ({traffic / alg_bytes:.2f}x the {alg_bytes / 1e6:.1f} MB algorithmic) |",
+        f"| HBM bandwidth | {traffic / avg_s / 1e9:.1f} GB/s measured, {alg_bytes / avg_s / 1e9:.1f} GB/s algorithmic "
+        f"(peak {HBM_PEAK_GBS:.0f}) |",
+        "",
+    ]
+    with open(summary, "w") as f:
+        f.write("\n".join(lines))
+    traffic_path = os.path.join(os.path.dirname(os.path.abspath(summary)), f"{args.kernel}_{args.workload}_traffic.txt")
+    with open(traffic_path, "w") as f:
+        f.write(f"# from {os.path.relpath(summary, ROOT)}\n")
+        f.write(f"hbm_bytes_per_launch: {traffic:.0f}\n")
+        f.write(f"fetch_bytes_per_launch: {fetch_bytes:.0f}\n")
+        f.write(f"write_bytes_per_launch: {write_bytes:.0f}\n")
+        f.write(f"mfma_util_pct: {mfma_util:.2f}\n")
+        f.write(f"effective_clock_mhz: {clock_mhz:.0f}\n")
+    log("\n".join(lines))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,111 @@
+"""The C-ABI library and the runner executable, without a GPU (CPU only)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from generator import catalog
+from shim import sgemm_shim as S
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sgemm_shim.h")
+RUNNER = os.path.join(ROOT, "amdgpu-arch-gemm_amd", "runner", "GeneratorRunner")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sgemm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for must in ("sgemm_open", "sgemm_close", "sgemm_launch", "sgemm_time", "sgemm_run", "sgemm_fill",
+                 "sgemm_last_error", "sgemm_check_shape", "sgemm_malloc", "sgemm_free"):
+        assert must in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = S.load_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    # and the Python binding declares a signature for each of them
+    assert set(declared_functions()) == set(S.SIGNATURES)
+    assert lib.sgemm_abi_version() == 1
+
+
+def test_no_device_is_an_error_code_not_a_crash(tmp_path):
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is visible here")
+    lib = S.load_library()
+    co, toml = catalog.paths("mt64x64_a32_wg2x2_dk16")
+    h = ctypes.c_void_p()
+    rc = lib.sgemm_open(co.encode(), toml.encode(), ctypes.byref(h))
+    assert rc == -5 and h.value is None
+    assert b"no HIP device" in lib.sgemm_last_error()
+
+
+def test_open_reports_missing_files_and_bad_configs(tmp_path):
+    lib = S.load_library()
+    h = ctypes.c_void_p()
+    co, toml = catalog.paths("mt64x64_a32_wg2x2_dk16")
+    assert lib.sgemm_open(co.encode(), b"/nonexistent.toml", ctypes.byref(h)) == -2
+    bad = tmp_path / "bad.toml"
+    bad.write_text(open(toml).read().replace("depth_k = 16\n", ""))
+    assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+    assert b"depth_k" in lib.sgemm_last_error()
+    bad.write_text(open(toml).read().replace("trans_a = false", "trans_a = true"))
+    assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+    bad.write_text(open(toml).read().replace("mfma = [32, 32, 1, 2]", "mfma = [4, 4, 4, 4]"))
+    assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+    assert lib.sgemm_open(b"/nonexistent.co", toml.encode(), ctypes.byref(h)) == -2
+    assert lib.sgemm_open(None, toml.encode(), ctypes.byref(h)) == -1
+
+
+def test_null_arguments_are_rejected():
+    lib = S.load_library()
+    assert lib.sgemm_launch(None, None, None, None, None, 64, 64, 16, 64, 16, 64, 64, 1.0, 0.0) == -1
+    assert lib.sgemm_get_info(None, None) == -1
+    assert lib.sgemm_fill(None, 10, 0, 0, 0) == -1
+    assert lib.sgemm_fill(None, 0, 0, 0, 0) == 0
+
+
+def test_runner_usage_error_exit_code():
+    ret = subprocess.run([RUNNER], stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    assert ret.returncode == 255 and b"usage" in ret.stdout
+    ret = subprocess.run([RUNNER, "a", "b", "1", "2", "x", "1", "1", "0"], stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT)
+    assert ret.returncode == 255 and b"usage" in ret.stdout
+
+
+def test_runner_cpu_reference_matches_oracle():
+    """The runner's validation GEMM (runner/cpu_reference.hpp) is the same
+    arithmetic as the oracle: compile a tiny driver for it and compare bitwise."""
+    import oracle
+    import tempfile
+    src = os.path.join(ROOT, "amdgpu-arch-gemm_amd", "runner")
+    with tempfile.TemporaryDirectory() as tmp:
+        c = os.path.join(tmp, "d.cpp")
+        exe = os.path.join(tmp, "d")
+        with open(c, "w") as f:
+            f.write('#include "cpu_reference.hpp"\n#include <cstdio>\n#include <vector>\n'
+                    'int main(){unsigned m=37,n=29,k=301; std::vector<float> a(m*k),b(k*n),c(m*n),d(m*n);\n'
+                    'FILE* f=fopen("in.bin","rb"); fread(a.data(),4,a.size(),f); fread(b.data(),4,b.size(),f);'
+                    ' fread(c.data(),4,c.size(),f); fclose(f);\n'
+                    'runner_cpu_gemm(a.data(),b.data(),c.data(),d.data(),0.5f,-2.0f,m,n,k,3);\n'
+                    'f=fopen("out.bin","wb"); fwrite(d.data(),4,d.size(),f); fclose(f); return 0;}\n')
+        subprocess.run(["g++", "-O2", "-ffp-contract=off", "-std=c++17", "-I", src, c, "-o", exe, "-pthread"],
+                       check=True)
+        m, n, k = 37, 29, 301
+        A = oracle.fill_matrix(m, k, 8, 0)
+        B = oracle.fill_matrix(k, n, 8, 1)
+        C = oracle.fill_matrix(m, n, 8, 2)
+        with open(os.path.join(tmp, "in.bin"), "wb") as f:
+            for X in (A, B, C):
+                f.write(np.asarray(X, dtype=np.float32).ravel(order="F").tobytes())
+        subprocess.run([exe], cwd=tmp, check=True)
+        D = np.fromfile(os.path.join(tmp, "out.bin"), dtype=np.float32).reshape(n, m).T
+    assert np.array_equal(D, oracle.cpu_gemm(A, B, C, 0.5, -2.0))
