@@ -215,6 +215,36 @@ template <int W> __device__ __forceinline__ void global_load_row(const float* p,
     }
 }
 
+// Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SCHED_MFMA = 0x008;
+constexpr int SCHED_VMEM_READ = 0x020;
+constexpr int SCHED_DS_READ = 0x100;
+constexpr int SCHED_DS_WRITE = 0x200;
+
+// Orders one k block's instructions as MFMA, memory op, MFMA, memory op, ...:
+// first the NREAD LDS reads (operands of the next block), then the NWRITE LDS
+// writes and NLOAD global loads of the refill, alternating.  Memory ops beyond
+// the MFMA count are left to the scheduler.
+template <int NMFMA, int NREAD, int NWRITE, int NLOAD>
+__device__ __forceinline__ void interleave_block() {
+#pragma unroll
+    for (int i = 0; i < NMFMA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SCHED_MFMA, 1, 0);
+        if (i < NREAD) {
+            __builtin_amdgcn_sched_group_barrier(SCHED_DS_READ, 1, 0);
+        } else {
+            const int j = i - NREAD;
+            if (j < 2 * NWRITE && j < 2 * NLOAD) {
+                if (j % 2 == 0) __builtin_amdgcn_sched_group_barrier(SCHED_DS_WRITE, 1, 0);
+                else __builtin_amdgcn_sched_group_barrier(SCHED_VMEM_READ, 1, 0);
+            } else if (j < NWRITE + NLOAD) {
+                if (NWRITE > NLOAD) __builtin_amdgcn_sched_group_barrier(SCHED_DS_WRITE, 1, 0);
+                else __builtin_amdgcn_sched_group_barrier(SCHED_VMEM_READ, 1, 0);
+            }
+        }
+    }
+}
+
 // Maps the hardware work-group id to the logical (tile_x, tile_y).
 __device__ __forceinline__ void tile_coords(int bx, int by, int nwgx, int nwgy, int& tx, int& ty) {
     int z = bx + by * nwgx;
@@ -378,6 +408,9 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     };
 
     // ---- K loop: NBUF LDS buffers, one barrier per tile ----
+    // Tile t lives in buffer t % NBUF.  Buffer (t + NBUF - 1) % NBUF was last
+    // read in iteration t - 1, so after the barrier that ends iteration t - 1
+    // any point of iteration t may refill it.
 #pragma unroll
     for (int s = 0; s < NBUF - 1; ++s) {
         if (s < ktiles) {
@@ -388,15 +421,61 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     if (NBUF - 1 < ktiles) gload(NBUF - 1);
     __syncthreads();
 
-    for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+    if constexpr (SG_PLR >= 2) {
+        // Early refill: the next tile's LDS writes and the global loads after it
+        // are issued right after the first k block's MFMAs, so they overlap MFMA
+        // execution instead of sitting between the last MFMA and the barrier.
+        // With NBUF >= 3 the first operands of tile t + 1 (written in iteration
+        // t - 1) are read before the barrier too, so nothing but the barrier
+        // separates the last MFMA of one tile from the first of the next.
+        Frag cur, nxt;
+        if (ktiles > 0) load_frag(lds, 0, cur);
+        for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
 #pragma unroll
-        for (int u = 0; u < NBUF; ++u) {
-            const int t = t0 + u;
-            if (t < ktiles) {
-                compute(u);
-                if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
-                if (t + NBUF < ktiles) gload(t + NBUF);
-                __syncthreads();
+            for (int u = 0; u < NBUF; ++u) {
+                const int t = t0 + u;
+                if (t < ktiles) {
+                    const float* s = lds + u * G::STAGE;
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const bool last = kb + 1 == NKB;
+                        // Branch-free refill: past the last tile the loads repeat the
+                        // last tile and the writes land in the buffer of tile t - 1,
+                        // which no later iteration reads; the prefetch past the end
+                        // reads a valid buffer whose values go unused.
+                        if (!last) load_frag(s, kb + 1, nxt);
+                        else if (NBUF >= 3) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, nxt);
+                        mfma_frag(cur);
+                        if (kb == 0) {
+                            swrite((u + NBUF - 1) % NBUF);
+                            gload(min(t + NBUF, ktiles - 1));
+                        }
+                        if constexpr (SG_PLR >= 3) {
+                            constexpr int NMFMA = KPL * WT0 * WT1;
+                            constexpr int NREAD = KPL * (WT0 >= 4 ? WT0 / 4 : 1) + WT1;
+                            constexpr int NREAD_NEXT = (NKB > 1 || NBUF >= 3) ? NREAD : 0;
+                            if (kb == 0) interleave_block<NMFMA, NREAD_NEXT, G::LA + G::LB, G::LA + G::LB>();
+                            else if (!last || NBUF >= 3) interleave_block<NMFMA, NREAD, 0, 0>();
+                            else interleave_block<NMFMA, 0, 0, 0>();
+                        }
+                        if (!last || NBUF >= 3) cur = nxt;
+                    }
+                    __syncthreads();
+                    if (NBUF == 2 && t + 1 < ktiles) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, cur);
+                }
+            }
+        }
+    } else {
+        for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                const int t = t0 + u;
+                if (t < ktiles) {
+                    compute(u);
+                    if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
+                    if (t + NBUF < ktiles) gload(t + NBUF);
+                    __syncthreads();
+                }
             }
         }
     }

@@ -32,8 +32,14 @@ def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0):
 
 # name -> (config, optimizations)
 SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
-    # headline 4096^3: 256x256 tiles, one work-group per CU
+    # tuner winners on gfx950 (interleaved early refill, three LDS buffers)
+    "mt256x256_a32_wg2x2_dk16_s3": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    "mt64x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    "mt128x64_a16_wg2x2_dk16_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=2), _opt(wgm=4, plr=1, xcd=8)),
+    "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    # the first-generation schedule (refill after the last block), kept as a baseline
     "mt256x256_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, xcd=8)),
+    "mt256x256_a32_wg2x2_dk16_plr2": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, plr=2, xcd=8)),
     "mt256x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16), _opt(wgm=4, xcd=8)),
     "mt128x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 16), _opt(wgm=4, xcd=8)),
     "mt128x128_a32_wg2x2_dk32": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 32), _opt(wgm=4, xcd=8)),
@@ -43,8 +49,9 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     # variants that exercise every knob in the parity tests
     "mt128x128_a16_wg2x2_dk16": (_cfg(MFMA_16x16x4, (2, 2), (4, 4), 16), _opt(wgm=2)),
     "mt64x64_a16_wg2x2_dk8": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 8), _opt(plr=0)),
-    "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4)),
-    "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8)),
+    "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4, plr=3)),
+    "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8, plr=2)),
+    "mt16x16_a16_wg1x1_dk16_s3_plr3": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, mapk=4)),
     # the reference's one-wave VM configurations (test_vm.py:447-627)
     "mt32x32_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16), _opt()),
     "mt16x16_a16_wg1x1_dk16": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt()),
@@ -55,10 +62,10 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 
 # shape class -> preferred instance (filled from tuner results; see select())
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
-    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk16"),
-    ((1024, 1024, 1024), "mt64x64_a32_wg2x2_dk16"),
-    ((8192, 8192, 256), "mt256x256_a32_wg2x2_dk16"),
-    ((16384, 128, 4096), "mt64x128_a32_wg2x2_dk16"),
+    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk16_s3"),
+    ((1024, 1024, 1024), "mt64x64_a16_wg2x2_dk32_s3"),
+    ((8192, 8192, 256), "mt128x64_a16_wg2x2_dk16_s3"),
+    ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
 ]
 
 

@@ -84,9 +84,14 @@ class GemmOptimizations:
     level != 0 turns on ``plr = 1`` and ``gw = 1``.  Meaning on gfx950:
 
     * ``wgm``       -- group width (in tiles along M) of the work-group order.
-    * ``plr``       -- operand prefetch depth: 0 reads a k block's operands and
-                       then multiplies; >= 1 reads block kb+1 while block kb
-                       multiplies (register double buffering).
+    * ``plr``       -- K-loop schedule: 0 reads a k block's operands and then
+                       multiplies; 1 reads block kb+1 while block kb multiplies
+                       (register double buffering), refilling LDS after the
+                       tile's last block; 2 also issues the next tile's LDS
+                       writes and global loads right after the first block and,
+                       with >= 3 LDS buffers, reads the next tile's first
+                       operands before the barrier; 3 is 2 with the memory
+                       instructions interleaved one by one between MFMAs.
     * ``gw``        -- epilogue flavour: 0 stores straight from the
                        accumulators, 1 is the same store path (kept for the
                        reference's knob space; both paths are identical today).
@@ -125,7 +130,7 @@ class GemmOptimizations:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
             raise RuntimeError(f"map_k_idx must be 0 or a power of two: {self.map_k_idx}")
-        if self.plr < 0 or self.gw not in (0, 1) or self.xcd < 0:
+        if self.plr not in (0, 1, 2, 3) or self.gw not in (0, 1) or self.xcd < 0:
             raise RuntimeError(f"Invalid optimization knobs: plr={self.plr} gw={self.gw} xcd={self.xcd}")
 
     def _setup_optimizations(self):
@@ -651,8 +656,8 @@ def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimi
 # the 4096^3 headline problem.
 def default_config() -> Tuple[GemmSolutionConfig, GemmOptimizations]:
     cfg = GemmSolutionConfig(DataType.FP32, DataType.FP32, DataType.FP32, DataType.FP32,
-                             MFMA_32x32x2, (2, 2), (4, 4), 16, False, False, vmem_stage=1)
-    opt = GemmOptimizations(1, wgm=4, plr=1, gw=0, map_k_idx=0, xcd=8)
+                             MFMA_32x32x2, (2, 2), (4, 4), 16, False, False, vmem_stage=2)
+    opt = GemmOptimizations(1, wgm=4, plr=3, gw=0, map_k_idx=0, xcd=8)
     return cfg, opt
 
 

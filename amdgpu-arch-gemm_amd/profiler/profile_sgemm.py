@@ -80,14 +80,32 @@ def find(out_dir, pattern):
 
 
 def counters_per_dispatch(csv_path, kernel_substr):
-    """{counter: [value per dispatch]} for dispatches whose kernel name matches."""
+    """{counter: [value per dispatch]} for dispatches whose kernel name matches,
+    plus "duration_s": the dispatch's own start/end timestamps."""
     per = {}
     with open(csv_path) as f:
         for row in csv.DictReader(f):
             if kernel_substr not in row.get("Kernel_Name", ""):
                 continue
-            per.setdefault(row["Counter_Name"], {})[row["Dispatch_Id"]] = float(row["Counter_Value"])
+            d = row["Dispatch_Id"]
+            per.setdefault(row["Counter_Name"], {})[d] = float(row["Counter_Value"])
+            per.setdefault("duration_s", {})[d] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9
     return {k: [v[d] for d in sorted(v, key=int)] for k, v in per.items()}
+
+
+def steady(values):
+    """Median over the dispatches after the first (clocks ramp up on the first)."""
+    return statistics.median(values[1:] if len(values) > 2 else values)
+
+
+def trace_durations(out_dir, kernel_substr):
+    """Per-dispatch durations (s) of the kernel from --kernel-trace, in dispatch order."""
+    rows = []
+    with open(find(out_dir, "run_kernel_trace.csv")) as f:
+        for row in csv.DictReader(f):
+            if kernel_substr in row["Kernel_Name"]:
+                rows.append((int(row["Start_Timestamp"]), (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9))
+    return [d for _, d in sorted(rows)]
 
 
 def kernel_stats(csv_path, kernel_substr):
@@ -97,6 +115,15 @@ def kernel_stats(csv_path, kernel_substr):
                 return {"calls": int(row["Calls"]), "avg_ns": float(row["AverageNs"]),
                         "min_ns": float(row["MinNs"]), "max_ns": float(row["MaxNs"])}
     raise RuntimeError(f"{kernel_substr} not in {csv_path}")
+
+
+def gpu_agent(out_dir):
+    """(XCD count, CU count, SIMD count) of the GPU agent from rocprofv3's agent info."""
+    with open(find(out_dir, "run_agent_info.csv")) as f:
+        for row in csv.DictReader(f):
+            if row.get("Agent_Type") == "GPU":
+                return int(row["Num_Xcc"]), int(row["Cu_Count"]), int(row["Simd_Count"])
+    raise RuntimeError(f"no GPU agent in {out_dir}")
 
 
 def rocprof(args, out_dir, program, timeout):
@@ -110,14 +137,14 @@ def main():
     ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--out", required=True, help="raw rocprofv3 output folder (e.g. under gpurun_out/)")
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
-    ap.add_argument("--runs", type=int, default=5)
+    ap.add_argument("--runs", type=int, default=20)
     ap.add_argument("--cus", type=int, default=256)
     args = ap.parse_args()
 
     m, n, k, seed, dist = WORKLOADS[args.workload]
     co, toml = catalog.paths(args.kernel)
     os.makedirs(args.out, exist_ok=True)
-    runner = [RUNNER, co, toml, str(m), str(n), str(k), "1", str(args.runs), "0", str(seed), str(dist), "1", "0"]
+    runner = [RUNNER, co, toml, str(m), str(n), str(k), "5", str(args.runs), "0", str(seed), str(dist), "1", "0"]
     probe = [PROBE, str(PROBE_BYTES), "3"]
     cmds = {}
 
@@ -143,6 +170,7 @@ def main():
             if c not in per:
                 raise RuntimeError(f"counter {c} missing from pass {key}")
             values[c] = per[c]
+        values[f"duration_s_{key}"] = per["duration_s"]
     probe_vals = {}
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
         d = os.path.join(args.out, f"probe_{c.lower()}")
@@ -150,22 +178,25 @@ def main():
         per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "copy_probe")
         probe_vals[c] = per[c]
 
-    med = {c: statistics.median(v) for c, v in values.items()}
+    xcc, cus, simds = gpu_agent(os.path.join(args.out, "pmc_mfma"))
+    med = {c: steady(v) for c, v in values.items()}
     probe_kib = PROBE_BYTES / 1024.0
     fetch_scale = probe_kib / statistics.median(probe_vals["FETCH_SIZE"])
     write_scale = probe_kib / statistics.median(probe_vals["WRITE_SIZE"])
     fetch_bytes = med["FETCH_SIZE"] * 1024.0 * fetch_scale
     write_bytes = med["WRITE_SIZE"] * 1024.0 * write_scale
     traffic = fetch_bytes + write_bytes
-    avg_s = ks["avg_ns"] * 1e-9
+    avg_s = steady(trace_durations(os.path.join(args.out, "trace"), "generated_gemm"))
     flops = 2.0 * m * n * k
     alg_bytes = 4.0 * (m * k + k * n + m * n)
-    simds = args.cus * SIMD_PER_CU
-    mfma_util = 100.0 * med["SQ_VALU_MFMA_BUSY_CYCLES"] / (med["GRBM_GUI_ACTIVE"] * simds)
-    clock_mhz = med["GRBM_GUI_ACTIVE"] / avg_s / 1e6
+    # GRBM_GUI_ACTIVE is reported summed over the XCDs: divide for per-XCD cycles.
+    mfma = [(b, a / xcc, dur) for b, a, dur in zip(values["SQ_VALU_MFMA_BUSY_CYCLES"], values["GRBM_GUI_ACTIVE"],
+                                                   values["duration_s_mfma"])]
+    mfma_util = 100.0 * steady([b / (a * simds) for b, a, _ in mfma])
+    clock_mhz = steady([a / dur / 1e6 for _, a, dur in mfma])
     lds_rate = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
     tflops = flops / avg_s / 1e12
-    clock_peak = args.cus * 256 * clock_mhz * 1e6 / 1e12
+    clock_peak = cus * 256 * clock_mhz * 1e6 / 1e12
 
     summary = args.summary or os.path.join(args.out, "summary.md")
     os.makedirs(os.path.dirname(os.path.abspath(summary)), exist_ok=True)
@@ -187,12 +218,13 @@ def main():
         "",
         "| figure | value |",
         "|---|---|",
-        f"| kernel-trace calls / avg / min / max | {ks['calls']} / {ks['avg_ns'] / 1e3:.2f} us / "
+        f"| kernel-trace calls / mean / min / max | {ks['calls']} / {ks['avg_ns'] / 1e3:.2f} us / "
         f"{ks['min_ns'] / 1e3:.2f} us / {ks['max_ns'] / 1e3:.2f} us |",
-        f"| achieved | {tflops:.2f} TFLOP/s = {100 * tflops / PEAK_TFLOPS:.1f}% of {PEAK_TFLOPS} (nominal) |",
-        f"| effective clock (GRBM_GUI_ACTIVE / duration) | {clock_mhz:.0f} MHz -> clock-adjusted peak "
-        f"{clock_peak:.1f} TFLOP/s, achieved {100 * tflops / clock_peak:.1f}% of it |",
-        f"| MfmaUtil = sum(SQ_VALU_MFMA_BUSY_CYCLES) / (GRBM_GUI_ACTIVE x {simds} SIMDs) | {mfma_util:.1f}% |",
+        f"| kernel-trace duration, median after the first dispatch | {avg_s * 1e6:.2f} us |",
+        f"| achieved (median duration) | {tflops:.2f} TFLOP/s = {100 * tflops / PEAK_TFLOPS:.1f}% of {PEAK_TFLOPS} (nominal) |",
+        f"| effective clock (GRBM_GUI_ACTIVE / {xcc} XCDs / dispatch time, PMC pass) | {clock_mhz:.0f} MHz -> "
+        f"clock-adjusted peak {clock_peak:.1f} TFLOP/s, achieved {100 * tflops / clock_peak:.1f}% of it |",
+        f"| MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcc} x {simds} SIMDs) | {mfma_util:.1f}% |",
         f"| SQ_BUSY_CYCLES (median per dispatch) | {med['SQ_BUSY_CYCLES']:.4g} |",
         f"| LDS bank conflicts / conflict-free accesses (SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE) | "
         f"{lds_rate:.4f} ({med['SQ_LDS_BANK_CONFLICT']:.4g} / {med['SQ_LDS_IDX_ACTIVE']:.4g}) |",

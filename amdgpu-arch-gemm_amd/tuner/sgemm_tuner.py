@@ -12,7 +12,7 @@ stdout line) and print the best.  Additions:
 
 * ``--space gfx950`` (default): macro-tile {64,128,256}^2 x wave-group
   {2x2, 4x1} x MFMA atom {32x32x2, 16x16x4} (stage 1), then the code-shape
-  knobs depth_k {16,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {0,1}
+  knobs depth_k {16,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
   on the best ``--refine`` geometries (stage 2).  ``--space reference`` is the
   reference's own 9-knob product.
 * every result is appended to ``<out>/results.jsonl`` and a rerun skips
@@ -73,8 +73,8 @@ GFX950_DEPTH_K = [16, 32]
 GFX950_VMEM_STAGES = [1, 2]
 GFX950_WGM = [1, 4, 8]
 GFX950_XCD = [0, 8]
-GFX950_PLR = [0, 1]
-DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=1, wgm=4, xcd=8, plr=1, gw=0, map_k_idx=0)
+GFX950_PLR = [1, 2, 3]
+DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=2, wgm=4, xcd=8, plr=3, gw=0, map_k_idx=0)
 ARCH = "gfx950"
 VERBOSE = False
 
