@@ -15,9 +15,12 @@
 // SG_WG0 * SG_WG1 * 64 work-items; all LDS is static (the runner passes 0 B of
 // dynamic LDS, generator_runner.cpp:189).  numWorkgroupX = ceil(m / MT0),
 // numWorkgroupY = ceil(n / MT1) with MT0 = atom_m * WG0 * WT0 and
-// MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  The kernel needs
-// m % MT0 == 0, n % MT1 == 0, k % DK == 0 and lda/ldb/ldc/ldd % 4 == 0; the
-// host side (shim, runner) checks this before every launch.
+// MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  Any m, n, k works: tiles
+// that lie wholly inside D with 16-byte aligned columns (every leading
+// dimension a multiple of 4) take the vector path, edge tiles and unaligned
+// problems load and store element by element with bounds checks, and a K
+// remainder is zero-filled in the last K tile.  The host side (shim, runner)
+// checks that lda >= m, ldb >= k, ldc >= m, ldd >= m before every launch.
 //
 // Data path per K tile of depth DK:
 //   HBM --global_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
@@ -215,6 +218,10 @@ template <int W> __device__ __forceinline__ void global_load_row(const float* p,
     }
 }
 
+// Tags selecting the vector (interior, aligned) or element-wise (edge) loads.
+struct FastPath { static constexpr bool slow = false; };
+struct SlowPath { static constexpr bool slow = true; };
+
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SCHED_MFMA = 0x008;
 constexpr int SCHED_VMEM_READ = 0x020;
@@ -294,7 +301,14 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     tile_coords(blockIdx.x, blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
-    const int ktiles = (int)(k / DK);
+    const int ktiles = (int)((k + DK - 1) / DK);
+    // Uniform per work-group: the vector fast path needs a whole tile inside D
+    // and 16-byte aligned rows of every operand; otherwise loads and stores go
+    // element by element with bounds checks.  A K remainder makes only the last
+    // K tile masked.
+    const bool aligned = ((lda | ldb | ldc | ldd) & 3u) == 0;
+    const bool slow_mn = !aligned || row0 + MT0 > m || col0 + MT1 > n;
+    const int kt_partial = (k % DK) ? ktiles - 1 : -1;
 
     // ---- global -> VGPR staging addresses (element offsets, 64-bit bases) ----
     const float* a_tile = a + row0;                      // + kt * DK * lda
@@ -320,21 +334,58 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     int kt_first = 0;
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
 
-    auto gload = [&](int t) {
+    // gload(tag, t): global -> VGPR copy of K tile t.  With a SlowPath tag every
+    // element is loaded from a clamped (always valid) address and replaced by
+    // 0 when it lies outside A or B, so the code stays branch-free.
+    auto gload = [&](auto path, int t) __attribute__((always_inline)) {
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
-        const float* pa = a_tile + (size_t)kt * DK * lda;
-        const float* pb = b_tile + (size_t)kt * DK;
+        if constexpr (!decltype(path)::slow) {
+            const float* pa = a_tile + (size_t)kt * DK * lda;
+            const float* pb = b_tile + (size_t)kt * DK;
 #pragma unroll
-        for (int i = 0; i < G::LA; ++i)
-            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
-                ra[i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+            for (int i = 0; i < G::LA; ++i)
+                if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
+                    ra[i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
 #pragma unroll
-        for (int i = 0; i < G::LB; ++i)
-            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
-                rb[i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+            for (int i = 0; i < G::LB; ++i)
+                if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
+                    rb[i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+        } else {
+            const uint32_t k0 = (uint32_t)kt * DK;
+#pragma unroll
+            for (int i = 0; i < G::LA; ++i) {
+                const int ch = tid + i * NT;
+                if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
+                    const uint32_t row = row0 + (uint32_t)(ch % (MT0 / 4)) * 4;
+                    const uint32_t kk = k0 + (uint32_t)(ch / (MT0 / 4));
+                    const uint32_t kc = kk < k ? kk : k - 1;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t rc = row + e < m ? row + e : m - 1;
+                        const float x = a[(size_t)kc * lda + rc];
+                        ra[i][e] = (row + e < m && kk < k) ? x : 0.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < G::LB; ++i) {
+                const int ch = tid + i * NT;
+                if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
+                    const uint32_t kk = k0 + (uint32_t)(ch % (DK / 4)) * 4;
+                    const uint32_t col = col0 + (uint32_t)(ch / (DK / 4));
+                    const uint32_t cc = col < n ? col : n - 1;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t kc = kk + e < k ? kk + e : k - 1;
+                        const float x = b[(size_t)cc * ldb + kc];
+                        rb[i][e] = (col < n && kk + e < k) ? x : 0.0f;
+                    }
+                }
+            }
+        }
     };
-    auto swrite = [&](int buf) {
+    auto swrite = [&](int buf) __attribute__((always_inline)) {
         float* s = lds + buf * G::STAGE;
 #pragma unroll
         for (int i = 0; i < G::LA; ++i)
@@ -366,7 +417,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
         float a[KPL][WT0];
         float b[WT1][KPL];
     };
-    auto load_frag = [&](const float* s, int kb, Frag& f) {
+    auto load_frag = [&](const float* s, int kb, Frag& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < KPL; ++j) lds_read_row<WT0>(s + a_rd + (kb * KB + j) * G::A_LD, f.a[j]);
 #pragma unroll
@@ -378,7 +429,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             for (int j = 0; j < KPL; ++j) f.b[jn][j] = tmp[j];
         }
     };
-    auto mfma_frag = [&](const Frag& f) {
+    auto mfma_frag = [&](const Frag& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < KPL; ++j)
 #pragma unroll
@@ -386,7 +437,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
 #pragma unroll
                 for (int jn = 0; jn < WT1; ++jn) acc[i][jn] = AT::mfma(f.a[j][i], f.b[jn][j], acc[i][jn]);
     };
-    auto compute = [&](int buf) {
+    auto compute = [&](int buf) __attribute__((always_inline)) {
         const float* s = lds + buf * G::STAGE;
         if constexpr (SG_PLR > 0 && NKB > 1) {
             // software pipeline: operands of block kb+1 are read while block kb multiplies
@@ -408,77 +459,83 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     };
 
     // ---- K loop: NBUF LDS buffers, one barrier per tile ----
-    // Tile t lives in buffer t % NBUF.  Buffer (t + NBUF - 1) % NBUF was last
-    // read in iteration t - 1, so after the barrier that ends iteration t - 1
-    // any point of iteration t may refill it.
-#pragma unroll
-    for (int s = 0; s < NBUF - 1; ++s) {
-        if (s < ktiles) {
-            gload(s);
-            swrite(s);
+    // One instantiation of the K loop per load path; the choice is uniform
+    // per work-group, so neither loop carries a branch on it.
+    auto kloop = [&](auto path) __attribute__((always_inline)) {
+        // Tile t lives in buffer t % NBUF.  Buffer (t + NBUF - 1) % NBUF was last
+        // read in iteration t - 1, so after the barrier that ends iteration t - 1
+        // any point of iteration t may refill it.
+    #pragma unroll
+        for (int s = 0; s < NBUF - 1; ++s) {
+            if (s < ktiles) {
+                gload(path, s);
+                swrite(s);
+            }
         }
-    }
-    if (NBUF - 1 < ktiles) gload(NBUF - 1);
-    __syncthreads();
+        if (NBUF - 1 < ktiles) gload(path, NBUF - 1);
+        __syncthreads();
 
-    if constexpr (SG_PLR >= 2) {
-        // Early refill: the next tile's LDS writes and the global loads after it
-        // are issued right after the first k block's MFMAs, so they overlap MFMA
-        // execution instead of sitting between the last MFMA and the barrier.
-        // With NBUF >= 3 the first operands of tile t + 1 (written in iteration
-        // t - 1) are read before the barrier too, so nothing but the barrier
-        // separates the last MFMA of one tile from the first of the next.
-        Frag cur, nxt;
-        if (ktiles > 0) load_frag(lds, 0, cur);
-        for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
-#pragma unroll
-            for (int u = 0; u < NBUF; ++u) {
-                const int t = t0 + u;
-                if (t < ktiles) {
-                    const float* s = lds + u * G::STAGE;
-#pragma unroll
-                    for (int kb = 0; kb < NKB; ++kb) {
-                        const bool last = kb + 1 == NKB;
-                        // Branch-free refill: past the last tile the loads repeat the
-                        // last tile and the writes land in the buffer of tile t - 1,
-                        // which no later iteration reads; the prefetch past the end
-                        // reads a valid buffer whose values go unused.
-                        if (!last) load_frag(s, kb + 1, nxt);
-                        else if (NBUF >= 3) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, nxt);
-                        mfma_frag(cur);
-                        if (kb == 0) {
-                            swrite((u + NBUF - 1) % NBUF);
-                            gload(min(t + NBUF, ktiles - 1));
+        if constexpr (SG_PLR >= 2) {
+            // Early refill: the next tile's LDS writes and the global loads after it
+            // are issued right after the first k block's MFMAs, so they overlap MFMA
+            // execution instead of sitting between the last MFMA and the barrier.
+            // With NBUF >= 3 the first operands of tile t + 1 (written in iteration
+            // t - 1) are read before the barrier too, so nothing but the barrier
+            // separates the last MFMA of one tile from the first of the next.
+            Frag cur, nxt;
+            if (ktiles > 0) load_frag(lds, 0, cur);
+            for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+    #pragma unroll
+                for (int u = 0; u < NBUF; ++u) {
+                    const int t = t0 + u;
+                    if (t < ktiles) {
+                        const float* s = lds + u * G::STAGE;
+    #pragma unroll
+                        for (int kb = 0; kb < NKB; ++kb) {
+                            const bool last = kb + 1 == NKB;
+                            // Branch-free refill: past the last tile the loads repeat the
+                            // last tile and the writes land in the buffer of tile t - 1,
+                            // which no later iteration reads; the prefetch past the end
+                            // reads a valid buffer whose values go unused.
+                            if (!last) load_frag(s, kb + 1, nxt);
+                            else if (NBUF >= 3) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, nxt);
+                            mfma_frag(cur);
+                            if (kb == 0) {
+                                swrite((u + NBUF - 1) % NBUF);
+                                gload(path, min(t + NBUF, ktiles - 1));
+                            }
+                            if constexpr (SG_PLR >= 3) {
+                                constexpr int NMFMA = KPL * WT0 * WT1;
+                                constexpr int NREAD = KPL * (WT0 >= 4 ? WT0 / 4 : 1) + WT1;
+                                constexpr int NREAD_NEXT = (NKB > 1 || NBUF >= 3) ? NREAD : 0;
+                                if (kb == 0) interleave_block<NMFMA, NREAD_NEXT, G::LA + G::LB, G::LA + G::LB>();
+                                else if (!last || NBUF >= 3) interleave_block<NMFMA, NREAD, 0, 0>();
+                                else interleave_block<NMFMA, 0, 0, 0>();
+                            }
+                            if (!last || NBUF >= 3) cur = nxt;
                         }
-                        if constexpr (SG_PLR >= 3) {
-                            constexpr int NMFMA = KPL * WT0 * WT1;
-                            constexpr int NREAD = KPL * (WT0 >= 4 ? WT0 / 4 : 1) + WT1;
-                            constexpr int NREAD_NEXT = (NKB > 1 || NBUF >= 3) ? NREAD : 0;
-                            if (kb == 0) interleave_block<NMFMA, NREAD_NEXT, G::LA + G::LB, G::LA + G::LB>();
-                            else if (!last || NBUF >= 3) interleave_block<NMFMA, NREAD, 0, 0>();
-                            else interleave_block<NMFMA, 0, 0, 0>();
-                        }
-                        if (!last || NBUF >= 3) cur = nxt;
+                        __syncthreads();
+                        if (NBUF == 2 && t + 1 < ktiles) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, cur);
                     }
-                    __syncthreads();
-                    if (NBUF == 2 && t + 1 < ktiles) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, cur);
+                }
+            }
+        } else {
+            for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+    #pragma unroll
+                for (int u = 0; u < NBUF; ++u) {
+                    const int t = t0 + u;
+                    if (t < ktiles) {
+                        compute(u);
+                        if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
+                        if (t + NBUF < ktiles) gload(path, t + NBUF);
+                        __syncthreads();
+                    }
                 }
             }
         }
-    } else {
-        for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
-#pragma unroll
-            for (int u = 0; u < NBUF; ++u) {
-                const int t = t0 + u;
-                if (t < ktiles) {
-                    compute(u);
-                    if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
-                    if (t + NBUF < ktiles) gload(t + NBUF);
-                    __syncthreads();
-                }
-            }
-        }
-    }
+    };
+    if (slow_mn || kt_partial >= 0) kloop(SlowPath{});
+    else kloop(FastPath{});
 
     // ---- epilogue: D = alpha * acc + beta * C ----
     const int wrow = row0 + wm * (AT::M * WT0);
@@ -492,13 +549,25 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             float v[WT0];
 #pragma unroll
             for (int i = 0; i < WT0; ++i) v[i] = alpha * acc[i][jn][q];
-            if (beta != 0.0f) {
-                float cv[WT0];
-                global_load_row<WT0>(c + colo * ldc + rr, cv);
+            if (!slow_mn) {
+                if (beta != 0.0f) {
+                    float cv[WT0];
+                    global_load_row<WT0>(c + colo * ldc + rr, cv);
 #pragma unroll
-                for (int i = 0; i < WT0; ++i) v[i] = __builtin_fmaf(beta, cv[i], v[i]);
+                    for (int i = 0; i < WT0; ++i) v[i] = __builtin_fmaf(beta, cv[i], v[i]);
+                }
+                global_store_row<WT0>(d + colo * ldd + rr, v);
+            } else if (colo < n) {
+#pragma unroll
+                for (int i = 0; i < WT0; ++i) {
+                    const uint32_t row = (uint32_t)rr + i;
+                    if (row < m) {
+                        float x = v[i];
+                        if (beta != 0.0f) x = __builtin_fmaf(beta, c[colo * ldc + row], x);
+                        d[colo * ldd + row] = x;
+                    }
+                }
             }
-            global_store_row<WT0>(d + colo * ldd + rr, v);
         }
     }
 }

@@ -335,18 +335,19 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd) {
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_check_shape: null handle");
     const sgemm_kernel_info& i = h->info;
-    if (m % (uint32_t)i.tile_m || n % (uint32_t)i.tile_n || k % (uint32_t)i.depth_k)
-        return fail(SGEMM_E_SHAPE, "shape %ux%ux%u is not a multiple of the kernel tile %dx%d (depth_k %d)",
-                    m, n, k, i.tile_m, i.tile_n, i.depth_k);
-    if (lda < m || ldb < k || ldc < m || ldd < m)
-        return fail(SGEMM_E_SHAPE, "leading dimensions too small: lda=%u (m=%u) ldb=%u (k=%u) ldc=%u ldd=%u",
-                    lda, m, ldb, k, ldc, ldd);
-    if ((lda | ldb | ldc | ldd) & 3u)
-        return fail(SGEMM_E_SHAPE, "leading dimensions must be multiples of 4 (16-byte rows): %u %u %u %u",
-                    lda, ldb, ldc, ldd);
-    const uint64_t wgx = m / (uint32_t)i.tile_m, wgy = n / (uint32_t)i.tile_n;
-    if (wgx > 0x7fffffffull || wgy > 65535ull * 1024ull || wgx * wgy > 0x7fffffffull)
+    // Any m, n, k: the kernel masks edge tiles and a K remainder.  Leading
+    // dimensions must cover the matrices (the kernel reads A[row + col*lda]).
+    if (lda < m || ldb < k || ldc < m || ldd < m || lda == 0 || ldb == 0 || ldc == 0 || ldd == 0)
+        return fail(SGEMM_E_SHAPE, "leading dimensions too small: lda=%u (m=%u) ldb=%u (k=%u) ldc=%u ldd=%u (m=%u)",
+                    lda, m, ldb, k, ldc, ldd, m);
+    const uint64_t wgx = ((uint64_t)m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m;
+    const uint64_t wgy = ((uint64_t)n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n;
+    if (wgx > 0x7fffffffull || wgy > 65535ull || wgx * wgy > 0x7fffffffull)
         return fail(SGEMM_E_SHAPE, "grid %llux%llu too large", (unsigned long long)wgx, (unsigned long long)wgy);
+    // per-thread offsets inside one K tile are 32-bit: lda * depth_k and
+    // ldb * tile_n must stay below 2^32 elements
+    if ((uint64_t)lda * (uint32_t)i.depth_k >= (1ull << 32) || (uint64_t)ldb * (uint32_t)i.tile_n >= (1ull << 32))
+        return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets: lda=%u ldb=%u", lda, ldb);
     return SGEMM_OK;
 }
 

@@ -94,20 +94,21 @@ def divides(name: str, m: int, n: int, k: int) -> bool:
 
 
 def select(m: int, n: int, k: int) -> str:
-    """Instance for an (m, n, k) problem; raises if none divides it."""
+    """Instance for an (m, n, k) problem: the tuner's choice for a BASELINE
+    shape, else the tuned instance whose tiles best fill the GPU -- every CU
+    busy first, then the least padding at the edges, then the largest tile."""
+    if m <= 0 or n <= 0:
+        raise RuntimeError(f"empty problem {m}x{n}x{k}")
     for shape, name in PREFERRED:
-        if shape == (m, n, k) and divides(name, m, n, k):
+        if shape == (m, n, k):
             return name
     best = None
-    for name, (cfg, _) in SOLUTIONS.items():
-        if not divides(name, m, n, k):
-            continue
+    for name in dict.fromkeys(nm for _, nm in PREFERRED):
+        cfg, _ = SOLUTIONS[name]
         t0, t1 = cfg.tile_size
-        tiles = (m // t0) * (n // t1)
-        # prefer the largest tile that still gives every CU a work-group
-        key = (tiles >= 256, t0 * t1, cfg.depth_k)
+        tx, ty = -(-m // t0), -(-n // t1)
+        fill = (m * n) / (tx * t0 * ty * t1)
+        key = (tx * ty >= 256, round(fill, 1), t0 * t1, k % cfg.depth_k == 0)
         if best is None or key > best[0]:
             best = (key, name)
-    if best is None:
-        raise RuntimeError(f"no kernel instance divides {m}x{n}x{k}")
     return best[1]

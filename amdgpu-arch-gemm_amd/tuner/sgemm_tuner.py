@@ -99,10 +99,13 @@ def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd) 
 
 
 def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
+    """The reference skips tiles that do not divide the problem (sgemm_tuner.py:97-100)
+    because its kernel cannot mask edges; this kernel can, so only tiles larger
+    than the problem are skipped, plus the reference's vector-load filter
+    (:102-105): every work-item moves at least one 16-byte chunk of A and of B."""
     t0, t1 = cfg.tile_size
-    if m % t0 or n % t1 or k % cfg.depth_k:
+    if t0 > max(m, 1) or t1 > max(n, 1):
         return False
-    # every work-item moves at least one 16-byte chunk of A and of B per K tile
     return cfg.num_bytes_per_buffer_load == (16, 16)
 
 

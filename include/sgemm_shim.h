@@ -88,7 +88,9 @@ void sgemm_close(sgemm_handle* h);
 int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info);
 
 /* Returns SGEMM_OK if the kernel can run this problem, SGEMM_E_SHAPE with a
- * message otherwise (m % MT0, n % MT1, k % depth_k, leading dimensions). */
+ * message otherwise.  Any m, n, k is accepted (edge tiles and a K remainder are
+ * masked in the kernel); lda >= m, ldb >= k, ldc >= m, ldd >= m are required,
+ * and lda * depth_k, ldb * tile_n must stay below 2^32 elements. */
 int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd);
 

@@ -53,16 +53,32 @@ class Memory:
         self.mem = bytearray(int(num_bytes))
         self._u8 = np.frombuffer(self.mem, dtype=np.uint8)  # writable view of the same bytes
         self.name = name
+        # optional list of (start, end) byte ranges that kernels may touch; an
+        # access must lie entirely inside one of them (host accesses are free)
+        self.regions: Optional[List[Tuple[int, int]]] = None
 
     @property
     def size(self) -> int:
         return len(self.mem)
+
+    def allocate_region(self, start: int, nbytes: int, label: str = ""):
+        if self.regions is None:
+            self.regions = []
+        self.regions.append((int(start), int(start) + int(nbytes), label))
 
     def _check(self, addr: np.ndarray, nbytes: int, where: str):
         n = len(self.mem)
         if addr.size and (int(addr.min()) < 0 or int(addr.max()) + nbytes > n):
             bad = int(addr.max()) if int(addr.max()) + nbytes > n else int(addr.min())
             raise MemoryError(f"{where}: {self.name} access at byte {bad} (+{nbytes}) outside [0, {n})")
+        if self.regions is not None and where not in ("host write", "host read") and addr.size:
+            ok = np.zeros(addr.shape, dtype=bool)
+            for lo, hi, _ in self.regions:
+                ok |= (addr >= lo) & (addr + nbytes <= hi)
+            if not ok.all():
+                bad = int(addr[~ok][0])
+                raise MemoryError(f"{where}: {self.name} access at byte {bad} (+{nbytes}) is outside every "
+                                  f"allocated buffer {[(lo, hi, l) for lo, hi, l in self.regions]}")
 
     def read_u32(self, addr: np.ndarray, ndwords: int, where: str) -> np.ndarray:
         """addr: (L,) byte addresses; returns (ndwords, L) uint32."""
@@ -940,6 +956,25 @@ for _n, _f in (("eq", np.equal), ("ne", np.not_equal), ("lt", np.less), ("le", n
                ("gt", np.greater), ("ge", np.greater_equal)):
     _vcmp(f"v_cmp_{_n}_u32", _f)
     _vcmp(f"v_cmp_{_n}_i32", _f, signed=True)
+def _vcmp64(name, fn, signed=False):
+    def _impl(vm, ins, prog):
+        if len(ins.ops) == 3:
+            dst, a, b = ins.ops
+        else:
+            dst, (a, b) = Operand("vcc", text="vcc"), ins.ops
+        x, y = vm.rv64(a), vm.rv64(b)
+        if signed:
+            x, y = x.view(np.int64), y.view(np.int64)
+        res = fn(x, y) & vm.exec_mask()
+        vm.ws64(dst, GcnVirtualMachine._bits(res))
+    for suffix in ("_e32", "_e64"):
+        _DISPATCH[name + suffix] = _impl
+
+
+for _n, _f in (("eq", np.equal), ("ne", np.not_equal), ("lt", np.less), ("le", np.less_equal),
+               ("gt", np.greater), ("ge", np.greater_equal)):
+    _vcmp64(f"v_cmp_{_n}_u64", _f)
+    _vcmp64(f"v_cmp_{_n}_i64", _f, signed=True)
 _vcmp("v_cmp_eq_f32", np.equal, True)
 _vcmp("v_cmp_lt_f32", np.less, True)
 _vcmp("v_cmp_gt_f32", np.greater, True)
@@ -1187,24 +1222,42 @@ def pack_kernargs(a: int, b: int, c: int, d: int, m: int, n: int, k: int, lda: i
 
 def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: np.ndarray,
               C: Optional[np.ndarray] = None, alpha: float = 1.0, beta: float = 0.0,
-              lds: Optional[Tuple[int, int, int, int]] = None) -> Tuple[np.ndarray, Dict]:
-    """Runs a compiled SGEMM kernel on column-major A (m x k), B (k x n), C."""
+              mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None) -> Tuple[np.ndarray, Dict]:
+    """Runs a compiled SGEMM kernel on column-major A, B, C.
+
+    Without ``mnk`` the problem is A (m x k) @ B (k x n) with tight leading
+    dimensions.  With ``mnk = (m, n, k)`` the arrays are the full column-major
+    storage: A is lda x (>= k), B is ldb x (>= n), C is ldc x (>= n), so
+    lda = A.shape[0] etc.; D gets ``ldd`` rows (default m).  Returns D as the
+    full ldd x n storage when ``mnk`` is given, else m x n."""
     A = np.asfortranarray(A, dtype=np.float32)
     B = np.asfortranarray(B, dtype=np.float32)
-    m, k = A.shape
-    _, n = B.shape
-    lda, ldb, ldc, ldd = (lds or (m, k, m, m))
-    Cm = np.zeros((m, n), dtype=np.float32) if C is None else np.asfortranarray(C, dtype=np.float32)
-    blobs = [A.ravel(order="F"), B.ravel(order="F"), Cm.ravel(order="F"), np.zeros(m * n, dtype=np.float32)]
-    offs, pos = [], 256
+    if mnk is None:
+        m, k = A.shape
+        n = B.shape[1]
+        lda, ldb = m, k
+    else:
+        m, n, k = mnk
+        lda, ldb = A.shape[0], B.shape[0]
+    Cm = np.zeros((m, n), dtype=np.float32, order="F") if C is None else np.asfortranarray(C, dtype=np.float32)
+    ldc = Cm.shape[0]
+    ldd = ldd or m
+    blobs = [A.ravel(order="F"), B.ravel(order="F"), Cm.ravel(order="F"),
+             np.zeros(ldd * n, dtype=np.float32)]
+    # every buffer gets exactly its own bytes as an allocated region, with
+    # unallocated gaps between them: any access past a buffer raises
+    offs, pos = [], 4096
     for bl in blobs:
         offs.append(pos)
-        pos += (bl.nbytes + 255) // 256 * 256
+        pos += (bl.nbytes + 4095) // 4096 * 4096 + 4096
     mem = Memory(pos, "vmem")
-    for o, bl in zip(offs, blobs):
+    for o, bl, label in zip(offs, blobs, "ABCD"):
         mem.write_bytes(o, bl.tobytes())
+        mem.allocate_region(o, bl.nbytes, label)
     nwgx, nwgy = (m + tile[0] - 1) // tile[0], (n + tile[1] - 1) // tile[1]
     ka = pack_kernargs(offs[0], offs[1], offs[2], offs[3], m, n, k, lda, ldb, ldc, ldd, alpha, beta, nwgx, nwgy)
     count = run_kernel(program, (nwgx, nwgy), workitems, ka, mem)
-    D = np.frombuffer(mem.read_bytes(offs[3], m * n * 4), dtype=np.float32).reshape(n, m).T.copy()
+    D = np.frombuffer(mem.read_bytes(offs[3], ldd * n * 4), dtype=np.float32).reshape(n, ldd).T.copy()
+    if mnk is None:
+        D = D[:m, :]
     return D, {"instructions": count, "grid": (nwgx, nwgy), "d_offset": offs[3], "memory": mem}

@@ -213,9 +213,10 @@ def test_cli_writes_co_and_toml(tmp_path):
 
 # ------------------------------------------------------------- catalog
 def test_select_prefers_tuned_and_divisible():
-    assert catalog.select(4096, 4096, 4096) in catalog.SOLUTIONS
-    for m, n, k in ((1024, 1024, 1024), (8192, 8192, 256), (16384, 128, 4096), (96, 64, 48)):
-        name = catalog.select(m, n, k)
-        assert catalog.divides(name, m, n, k)
+    for shape, name in catalog.PREFERRED:
+        assert catalog.select(*shape) == name
+    # shapes outside the table: a tuned instance that fills the GPU and pads least
+    assert catalog.divides(catalog.select(8192, 8192, 8192), 8192, 8192, 8192)
+    assert catalog.select(100, 70, 33) in dict(catalog.PREFERRED).values()
     with pytest.raises(RuntimeError):
-        catalog.select(17, 16, 16)
+        catalog.select(0, 16, 16)

@@ -141,14 +141,49 @@ def test_k_zero_is_beta_c(kernels):
     assert np.array_equal(D, (np.float32(2.0) * C).astype(np.float32))
 
 
-def test_bad_shape_is_an_error_not_a_launch(kernels):
+def test_bad_leading_dimension_is_an_error_not_a_launch(kernels):
     name = "mt256x256_a32_wg2x2_dk16"
     with _kernel(name) as kern:
         d = S.DeviceBuffer(4 * 256 * 256)
-        with pytest.raises(S.SgemmError, match="multiple of the kernel tile"):
-            kern.launch(d, d, None, d, 255, 256, 16, alpha=1.0, beta=0.0)
-        with pytest.raises(S.SgemmError, match="multiples of 4"):
-            kern.launch(d, d, None, d, 256, 256, 16, alpha=1.0, beta=0.0, lda=258)
+        with pytest.raises(S.SgemmError, match="leading dimensions too small"):
+            kern.launch(d, d, None, d, 256, 256, 16, alpha=1.0, beta=0.0, lda=255)
+        with pytest.raises(S.SgemmError, match="leading dimensions too small"):
+            kern.launch(d, d, None, d, 256, 256, 16, alpha=1.0, beta=0.0, ldb=15)
+
+
+EDGE_SHAPES = [
+    # (instance, m, n, k, pad): edge tiles in M and N, K remainders, k < DK, odd leading dims
+    ("mt256x256_a32_wg2x2_dk16_s3", 1000, 999, 1001, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3", 257, 255, 17, 1),
+    ("mt64x64_a16_wg2x2_dk32_s3", 1023, 1025, 1027, 0),
+    ("mt64x64_a16_wg2x2_dk32_s3", 5, 3, 1, 1),
+    ("mt128x64_a16_wg2x2_dk16_s3", 8190, 130, 250, 0),
+    ("mt128x64_a16_wg2x2_dk32_s3", 16383, 127, 4095, 3),
+    ("mt128x64_a32_wg4x1_dk8_s3", 131, 123, 17, 1),
+    ("mt64x64_a32_wg1x1_dk16", 63, 65, 48, 2),
+    ("mt16x16_a16_wg1x1_dk16_s3_plr3", 19, 27, 33, 0),
+]
+
+
+@pytest.mark.parametrize("name,m,n,k,pad", EDGE_SHAPES)
+def test_arbitrary_shapes(kernels, name, m, n, k, pad):
+    """Any m, n, k and any leading dimensions >= the matrix: only the m x n block
+    of D changes, and it matches the oracle."""
+    _say(f"edge {name} {m}x{n}x{k} pad {pad}")
+    lda, ldb, ldc, ldd = m + pad, k + 2 * pad, m + pad, m + 3 * pad
+    Af = S.fill_matrix(lda, k, 6, 0)
+    Bf = S.fill_matrix(ldb, n, 6, 1)
+    Cf = S.fill_matrix(ldc, n, 6, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer.from_array(np.full((ldd, n), -3.5, dtype=np.float32))
+    with _kernel(name) as kern:
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=1.25, beta=-0.5, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd)
+        kern.synchronize()
+    Dfull = dD.download().reshape(n, ldd).T
+    cols = _sample_columns(n, 64, 7)
+    ref = oracle.cpu_gemm_mt(Af[:m, :k], Bf[:k, cols], Cf[:m, cols], 1.25, -0.5, threads=16)
+    _check(Dfull[:m, cols], ref, k, name)
+    assert np.all(Dfull[m:, :] == -3.5), "rows past m of D were written"
 
 
 # ---------------------------------------------------------------- configs
@@ -216,11 +251,14 @@ def test_generator_runner_validates(kernels):
     assert float(lines[-3].split(":")[-1]) > 0
 
 
-def test_generator_runner_rejects_bad_shape(kernels):
-    co, toml = catalog.paths("mt256x256_a32_wg2x2_dk16")
-    ret = _run([RUNNER, co, toml, "1000", "1024", "1024", "1", "1", "0"])
-    assert ret.returncode != 0
-    assert b"not a multiple" in ret.stdout
+def test_generator_runner_odd_shape_validates(kernels):
+    """A shape the reference tuner would skip (sgemm_tuner.py:97-100) runs and validates."""
+    co, toml = catalog.paths("mt256x256_a32_wg2x2_dk16_s3")
+    ret = _run([RUNNER, co, toml, "1000", "777", "1031", "1", "2", "1", "5", "1"])
+    out = ret.stdout.decode()
+    _say(out)
+    assert ret.returncode == 0, out
+    assert "validation: PASS" in out
 
 
 def test_reference_runner_loads_our_code_object(kernels):

@@ -230,16 +230,43 @@ def test_a_transposed_mfma_layout_is_caught(monkeypatch):
     assert oracle.normwise_error(D, oracle.gemm_f64(A, B)) > oracle.tolerance(k)
 
 
-def test_out_of_bounds_shape_is_caught():
-    # m = 40 is not a multiple of the 32-row tile: the second work-group along M
-    # reads past A and writes past D; the VM's bounds checks stop it
+EDGE_CASES = [  # (instance, m, n, k): partial tiles in M and N, K remainders, k < DK, tiny problems
+    ("mt32x32_a32_wg1x1_dk16", 35, 59, 33), ("mt32x32_a32_wg1x1_dk16", 5, 3, 1),
+    ("mt64x64_a16_wg2x2_dk32_s3", 67, 123, 65), ("mt64x64_a16_wg2x2_dk32_s3", 128, 64, 29),
+    ("mt128x64_a32_wg4x1_dk8_s3", 131, 123, 17), ("mt16x16_a16_wg1x1_dk16_s3_plr3", 15, 17, 48),
+    ("mt64x64_a32_wg1x1_dk16", 63, 65, 48),
+]
+
+
+@pytest.mark.parametrize("name,m,n,k", EDGE_CASES)
+@pytest.mark.parametrize("pad", [0, 1])
+def test_edge_shapes_stay_inside_every_buffer(name, m, n, k, pad):
+    """Arbitrary shapes: each of A, B, C, D is its own guarded region in the VM,
+    so any read or write outside the matrices raises MemoryError.  pad = 1 makes
+    every leading dimension odd (the element-wise path for all tiles)."""
+    prog, cfg = program(name)
+    lda, ldb, ldc, ldd = m + pad, k + pad, m + 2 * pad, m + 3 * pad
+    A = oracle.fill_matrix(lda, k, 3, 0)
+    B = oracle.fill_matrix(ldb, n, 3, 1)
+    C = oracle.fill_matrix(ldc, n, 3, 2)
+    D, _ = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=ldd)
+    ref = oracle.gemm_f64(A[:m, :k], B[:k, :n], C[:m, :n], 0.5, 1.5)
+    assert oracle.normwise_error(D[:m, :n], ref) <= oracle.tolerance(k)
+    assert np.all(D[m:, :] == 0), "rows past m of D were written"
+
+
+def test_an_undersized_buffer_is_caught():
+    # A one float short of m*k: the kernel's last read of A leaves the buffer
     prog, cfg = program("mt32x32_a32_wg1x1_dk16")
-    m, n, k = 40, 32, 16
-    mem = V.Memory(4 * (m * k + k * n + m * n), "vmem")
-    offs = [0, 4 * m * k, 4 * (m * k + k * n)]
-    ka = pack_kernargs(offs[0], offs[1], 0, offs[2], m, n, k, m, k, m, m, 1.0, 0.0, 2, 1)
-    with pytest.raises(MemoryError):
-        run_kernel(prog, (2, 1), cfg.num_workitems, ka, mem)
+    m, n, k = 32, 32, 16
+    mem = V.Memory(1 << 16, "vmem")
+    offs = [4096, 16384, 32768]
+    mem.allocate_region(offs[0], 4 * m * k - 4, "A")
+    mem.allocate_region(offs[1], 4 * k * n, "B")
+    mem.allocate_region(offs[2], 4 * m * n, "D")
+    ka = pack_kernargs(offs[0], offs[1], 0, offs[2], m, n, k, m, k, m, m, 1.0, 0.0, 1, 1)
+    with pytest.raises(MemoryError, match="outside every allocated buffer"):
+        run_kernel(prog, (1, 1), cfg.num_workitems, ka, mem)
 
 
 # ------------------------------------------------------ VM unit checks
