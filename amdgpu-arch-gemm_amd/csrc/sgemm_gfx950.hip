@@ -98,6 +98,12 @@
 #ifndef SG_PAD_B
 #define SG_PAD_B 4
 #endif
+#ifndef SG_TA
+#define SG_TA 0
+#endif
+#ifndef SG_TB
+#define SG_TB 0
+#endif
 #ifndef SG_KERNEL_NAME
 #define SG_KERNEL_NAME generated_gemm
 #endif
@@ -310,24 +316,45 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     const bool slow_mn = !aligned || row0 + MT0 > m || col0 + MT1 > n;
     const int kt_partial = (k % DK) ? ktiles - 1 : -1;
 
-    // ---- global -> VGPR staging addresses (element offsets, 64-bit bases) ----
-    const float* a_tile = a + row0;                      // + kt * DK * lda
-    const float* b_tile = b + (size_t)col0 * ldb;        // + kt * DK
+    // ---- global -> VGPR staging (element offsets inside a K tile, 64-bit bases) ----
+    // Every thread moves float4 chunks.  A chunk runs along the operand's
+    // contiguous dimension: m for A (NN) or k for A^T, k for B (NN) or n for
+    // B^T.  Chunks along the LDS row direction are written with one
+    // ds_write_b128; chunks across it (the transposed operands) are scattered
+    // with four ds_write_b32, so the LDS layouts and reads never change:
+    //   A: [DK][MT0 + PAD_A] (m contiguous), B: [MT1][DK + PAD_B] (k contiguous).
+    constexpr bool TA = SG_TA != 0, TB = SG_TB != 0;
+    // per chunk: (i0, i1) = position along (contiguous dim / 4, other dim)
+    constexpr int A_C0 = TA ? DK / 4 : MT0 / 4;   // chunks along the contiguous dim of A
+    constexpr int B_C0 = TB ? MT1 / 4 : DK / 4;   // chunks along the contiguous dim of B
+    // element (row, kk) of op(A) is a[row + kk*lda] (NN) or a[kk + row*lda] (T)
+    const float* a_tile = TA ? a + (size_t)row0 * lda : a + row0;
+    const float* b_tile = TB ? b + col0 : b + (size_t)col0 * ldb;
     uint32_t a_off[G::LA], b_off[G::LB];
     int a_lds[G::LA], b_lds[G::LB];
 #pragma unroll
     for (int i = 0; i < G::LA; ++i) {
         const int ch = tid + i * NT;
-        const int mc = ch % (MT0 / 4), kc = ch / (MT0 / 4);
-        a_off[i] = (uint32_t)(mc * 4) + (uint32_t)kc * lda;
-        a_lds[i] = kc * G::A_LD + mc * 4;
+        const int c0 = ch % A_C0, c1 = ch / A_C0;
+        if constexpr (!TA) {  // c0: m / 4, c1: k
+            a_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * lda;
+            a_lds[i] = c1 * G::A_LD + c0 * 4;
+        } else {              // c0: k / 4, c1: m
+            a_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * lda;
+            a_lds[i] = (c0 * 4) * G::A_LD + c1;
+        }
     }
 #pragma unroll
     for (int i = 0; i < G::LB; ++i) {
         const int ch = tid + i * NT;
-        const int kc = ch % (DK / 4), nc = ch / (DK / 4);
-        b_off[i] = (uint32_t)(kc * 4) + (uint32_t)nc * ldb;
-        b_lds[i] = G::A_STAGE + nc * G::B_LD + kc * 4;
+        const int c0 = ch % B_C0, c1 = ch / B_C0;
+        if constexpr (!TB) {  // c0: k / 4, c1: n
+            b_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * ldb;
+            b_lds[i] = G::A_STAGE + c1 * G::B_LD + c0 * 4;
+        } else {              // c0: n / 4, c1: k
+            b_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * ldb;
+            b_lds[i] = G::A_STAGE + (c0 * 4) * G::B_LD + c1;
+        }
     }
     f32x4 ra[G::LA], rb[G::LB];
 
@@ -341,8 +368,8 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
         if constexpr (!decltype(path)::slow) {
-            const float* pa = a_tile + (size_t)kt * DK * lda;
-            const float* pb = b_tile + (size_t)kt * DK;
+            const float* pa = a_tile + (TA ? (size_t)kt * DK : (size_t)kt * DK * lda);
+            const float* pb = b_tile + (TB ? (size_t)kt * DK * ldb : (size_t)kt * DK);
 #pragma unroll
             for (int i = 0; i < G::LA; ++i)
                 if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
@@ -357,14 +384,15 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             for (int i = 0; i < G::LA; ++i) {
                 const int ch = tid + i * NT;
                 if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
-                    const uint32_t row = row0 + (uint32_t)(ch % (MT0 / 4)) * 4;
-                    const uint32_t kk = k0 + (uint32_t)(ch / (MT0 / 4));
-                    const uint32_t kc = kk < k ? kk : k - 1;
+                    const int c0 = ch % A_C0, c1 = ch / A_C0;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uint32_t rc = row + e < m ? row + e : m - 1;
-                        const float x = a[(size_t)kc * lda + rc];
-                        ra[i][e] = (row + e < m && kk < k) ? x : 0.0f;
+                        const uint32_t row = row0 + (TA ? (uint32_t)c1 : (uint32_t)(c0 * 4 + e));
+                        const uint32_t kk = k0 + (TA ? (uint32_t)(c0 * 4 + e) : (uint32_t)c1);
+                        const uint32_t rc = row < m ? row : m - 1;
+                        const uint32_t kc = kk < k ? kk : k - 1;
+                        const float x = TA ? a[(size_t)rc * lda + kc] : a[(size_t)kc * lda + rc];
+                        ra[i][e] = (row < m && kk < k) ? x : 0.0f;
                     }
                 }
             }
@@ -372,14 +400,15 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             for (int i = 0; i < G::LB; ++i) {
                 const int ch = tid + i * NT;
                 if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
-                    const uint32_t kk = k0 + (uint32_t)(ch % (DK / 4)) * 4;
-                    const uint32_t col = col0 + (uint32_t)(ch / (DK / 4));
-                    const uint32_t cc = col < n ? col : n - 1;
+                    const int c0 = ch % B_C0, c1 = ch / B_C0;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uint32_t kc = kk + e < k ? kk + e : k - 1;
-                        const float x = b[(size_t)cc * ldb + kc];
-                        rb[i][e] = (col < n && kk + e < k) ? x : 0.0f;
+                        const uint32_t col = col0 + (TB ? (uint32_t)(c0 * 4 + e) : (uint32_t)c1);
+                        const uint32_t kk = k0 + (TB ? (uint32_t)c1 : (uint32_t)(c0 * 4 + e));
+                        const uint32_t cc = col < n ? col : n - 1;
+                        const uint32_t kc = kk < k ? kk : k - 1;
+                        const float x = TB ? b[(size_t)kc * ldb + cc] : b[(size_t)cc * ldb + kc];
+                        rb[i][e] = (col < n && kk < k) ? x : 0.0f;
                     }
                 }
             }
@@ -389,12 +418,24 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
         float* s = lds + buf * G::STAGE;
 #pragma unroll
         for (int i = 0; i < G::LA; ++i)
-            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
-                *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[i];
+            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS) {
+                if constexpr (!TA) {
+                    *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[i];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[a_lds[i] + e * G::A_LD] = ra[i][e];
+                }
+            }
 #pragma unroll
         for (int i = 0; i < G::LB; ++i)
-            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
-                *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[i];
+            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS) {
+                if constexpr (!TB) {
+                    *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[i];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[b_lds[i] + e * G::B_LD] = rb[i][e];
+                }
+            }
     };
 
     // ---- LDS -> MFMA operand addresses ----

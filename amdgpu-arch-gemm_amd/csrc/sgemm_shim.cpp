@@ -185,7 +185,8 @@ int load_config(const char* path, sgemm_kernel_info* info) {
     CFG_TRY(toml_int(t, "lds_usage_bytes", &info->lds_usage_bytes));
     CFG_TRY(toml_int(t, "vmem_stage", &info->vmem_stage, false, 1));
     if (a_type || b_type || cd_type || scalar_type) return fail(SGEMM_E_CONFIG, "only FP32 (type 0) kernels are supported");
-    if (trans_a || trans_b) return fail(SGEMM_E_CONFIG, "only the NN layout is supported");
+    info->trans_a = trans_a ? 1 : 0;
+    info->trans_b = trans_b ? 1 : 0;
     if (info->wavefront_size != 64) return fail(SGEMM_E_CONFIG, "wavefront_size must be 64 on gfx950");
     const int* mf = info->mfma;
     const bool atom32 = mf[0] == 32 && mf[1] == 32 && mf[2] == 1 && mf[3] == 2;
@@ -336,17 +337,21 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_check_shape: null handle");
     const sgemm_kernel_info& i = h->info;
     // Any m, n, k: the kernel masks edge tiles and a K remainder.  Leading
-    // dimensions must cover the matrices (the kernel reads A[row + col*lda]).
-    if (lda < m || ldb < k || ldc < m || ldd < m || lda == 0 || ldb == 0 || ldc == 0 || ldd == 0)
-        return fail(SGEMM_E_SHAPE, "leading dimensions too small: lda=%u (m=%u) ldb=%u (k=%u) ldc=%u ldd=%u (m=%u)",
-                    lda, m, ldb, k, ldc, ldd, m);
+    // dimensions must cover the stored matrices: A is m x k (k x m when
+    // transposed), B is k x n (n x k when transposed), C and D are m x n.
+    const uint32_t a_rows = i.trans_a ? k : m, b_rows = i.trans_b ? n : k;
+    if (lda < a_rows || ldb < b_rows || ldc < m || ldd < m || lda == 0 || ldb == 0 || ldc == 0 || ldd == 0)
+        return fail(SGEMM_E_SHAPE, "leading dimensions too small: lda=%u (needs %u) ldb=%u (needs %u) ldc=%u ldd=%u (m=%u)",
+                    lda, a_rows, ldb, b_rows, ldc, ldd, m);
     const uint64_t wgx = ((uint64_t)m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m;
     const uint64_t wgy = ((uint64_t)n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n;
     if (wgx > 0x7fffffffull || wgy > 65535ull || wgx * wgy > 0x7fffffffull)
         return fail(SGEMM_E_SHAPE, "grid %llux%llu too large", (unsigned long long)wgx, (unsigned long long)wgy);
     // per-thread offsets inside one K tile are 32-bit: lda * depth_k and
     // ldb * tile_n must stay below 2^32 elements
-    if ((uint64_t)lda * (uint32_t)i.depth_k >= (1ull << 32) || (uint64_t)ldb * (uint32_t)i.tile_n >= (1ull << 32))
+    const uint64_t a_span = (uint64_t)lda * (uint32_t)(i.trans_a ? i.tile_m : i.depth_k);
+    const uint64_t b_span = (uint64_t)ldb * (uint32_t)(i.trans_b ? i.depth_k : i.tile_n);
+    if (a_span >= (1ull << 32) || b_span >= (1ull << 32))
         return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets: lda=%u ldb=%u", lda, ldb);
     return SGEMM_OK;
 }
@@ -470,7 +475,8 @@ int sgemm_run(sgemm_handle* h, const float* A, const float* B, const float* C, f
               int warmup, int runs, double* ms_per_run) {
     if (!h || !D || !A || !B || (beta != 0.0f && !C) || runs <= 0 || warmup < 0)
         return fail(SGEMM_E_INVALID, "sgemm_run: bad argument");
-    int r = sgemm_check_shape(h, m, n, k, m, k, m, m);
+    const uint32_t lda = h->info.trans_a ? k : m, ldb = h->info.trans_b ? n : k;
+    int r = sgemm_check_shape(h, m, n, k, lda, ldb, m, m);
     if (r != SGEMM_OK) return r;
     const size_t bA = (size_t)m * k * 4, bB = (size_t)k * n * 4, bC = (size_t)m * n * 4;
     void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dD = nullptr;
@@ -484,7 +490,7 @@ int sgemm_run(sgemm_handle* h, const float* A, const float* B, const float* C, f
     if (r == SGEMM_OK && dC) r = sgemm_memcpy_h2d(dC, C, bC);
     if (r == SGEMM_OK) r = sgemm_memset(dD, 0, bC);
     if (r == SGEMM_OK)
-        r = sgemm_time(h, (const float*)dA, (const float*)dB, (const float*)dC, (float*)dD, m, n, k, m, k, m, m,
+        r = sgemm_time(h, (const float*)dA, (const float*)dB, (const float*)dC, (float*)dD, m, n, k, lda, ldb, m, m,
                        alpha, beta, warmup, runs, &total);
     if (r == SGEMM_OK) r = sgemm_memcpy_d2h(D, dD, bC);
     if (r == SGEMM_OK && ms_per_run) *ms_per_run = (double)total / runs;

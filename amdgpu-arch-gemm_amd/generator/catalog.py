@@ -22,8 +22,8 @@ KERNEL_DIR = os.path.join(PACKAGE_ROOT, "kernels")
 F = DataType.FP32
 
 
-def _cfg(mfma, wg, wt, dk, stages=1):
-    return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, False, False, vmem_stage=stages)
+def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
+    return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
 def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0):
@@ -52,6 +52,17 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4, plr=3)),
     "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8, plr=2)),
     "mt16x16_a16_wg1x1_dk16_s3_plr3": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, mapk=4)),
+    # transposed layouts (TN, NT, TT): op(A) = A^T and/or op(B) = B^T
+    "mt256x256_a32_wg2x2_dk16_s3_tn": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2, ta=True),
+                                       _opt(wgm=4, plr=3, xcd=8)),
+    "mt256x256_a32_wg2x2_dk16_s3_nt": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2, tb=True),
+                                       _opt(wgm=4, plr=3, xcd=8)),
+    "mt256x256_a32_wg2x2_dk16_s3_tt": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2, ta=True, tb=True),
+                                       _opt(wgm=4, plr=3, xcd=8)),
+    "mt64x64_a16_wg2x2_dk32_s3_tn": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2, ta=True),
+                                     _opt(wgm=4, plr=3, xcd=8)),
+    "mt32x32_a32_wg1x1_dk16_tt": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, ta=True, tb=True), _opt()),
+    "mt16x16_a16_wg1x1_dk16_nt": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, tb=True), _opt(plr=3)),
     # the reference's one-wave VM configurations (test_vm.py:447-627)
     "mt32x32_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16), _opt()),
     "mt16x16_a16_wg1x1_dk16": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt()),

@@ -219,8 +219,6 @@ class GemmSolutionConfig:
             raise RuntimeError(f"Unsupported MFMA atom: {self.mfma}")
         if any(t != DataType.FP32 for t in (self.a_type, self.b_type, self.cd_type, self.scalar_type)):
             raise RuntimeError("Only FP32 operands are supported")
-        if self.trans_a or self.trans_b:
-            raise RuntimeError("Only the NN layout (trans_a = trans_b = False) is implemented")
         if not all(_is_pow2(w) for w in self.wave_group):
             raise RuntimeError(f"Invalid wave group: {self.wave_group}")
         if self.num_workitems > MAX_WORKITEMS:
@@ -304,15 +302,30 @@ class GemmSolutionConfig:
         kpl = self.k_per_lane
         return [((l % an) * stride + (l // an) * kpl) * 4 for l in range(64)]
 
-    def _b_write_addrs(self, pad: int) -> List[int]:
+    def _a_write_addrs(self, pad: int) -> Tuple[List[int], int]:
+        """Byte addresses of one wave's A-tile LDS write and its width."""
+        stride = self.tile_size[0] + pad
+        if not self.trans_a:  # float4 along m into one row
+            per_row = self.tile_size[0] // 4
+            return [((t // per_row) * stride + (t % per_row) * 4) * 4 for t in range(64)], 16
+        per_m = self.depth_k // 4  # float4 along k scattered down a column, first dword shown
+        return [((t % per_m) * 4 * stride + t // per_m) * 4 for t in range(64)], 4
+
+    def _b_write_addrs(self, pad: int) -> Tuple[List[int], int]:
         stride = self.depth_k + pad
-        per_col = self.depth_k // 4
-        return [((t // per_col) * stride + (t % per_col) * 4) * 4 for t in range(64)]
+        if not self.trans_b:  # float4 along k into one row
+            per_col = self.depth_k // 4
+            return [((t // per_col) * stride + (t % per_col) * 4) * 4 for t in range(64)], 16
+        per_k = self.tile_size[1] // 4  # float4 along n scattered across rows
+        return [((t % per_k) * 4 * stride + t // per_k) * 4 for t in range(64)], 4
 
     def _auto_lds_pad_a(self) -> int:
         best, best_cost = 0, None
         for pad in (0, 4, 8, 12, 16):
-            cost = lds_access_cycles(self._a_read_addrs(pad), 4 * self.wave_tiling[0])
+            waddr, wbytes = self._a_write_addrs(pad)
+            writes = 1 if wbytes == 16 else 4
+            cost = (lds_access_cycles(self._a_read_addrs(pad), 4 * self.wave_tiling[0]) * self.k_per_lane
+                    + lds_access_cycles(waddr, wbytes) * writes)
             if best_cost is None or cost < best_cost:
                 best, best_cost = pad, cost
         return best
@@ -320,8 +333,10 @@ class GemmSolutionConfig:
     def _auto_lds_pad_b(self) -> int:
         best, best_cost = 0, None
         for pad in (0, 4, 8, 12, 16):
+            waddr, wbytes = self._b_write_addrs(pad)
+            writes = 1 if wbytes == 16 else 4
             cost = (lds_access_cycles(self._b_read_addrs(pad), 4 * self.k_per_lane) * 4
-                    + lds_access_cycles(self._b_write_addrs(pad), 16))
+                    + lds_access_cycles(waddr, wbytes) * writes)
             if best_cost is None or cost < best_cost:
                 best, best_cost = pad, cost
         return best
@@ -485,6 +500,8 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_MAPK": opt.map_k_idx,
         "SG_PLR": opt.plr,
         "SG_GW": opt.gw,
+        "SG_TA": int(config.trans_a),
+        "SG_TB": int(config.trans_b),
         "SG_PAD_A": pad_a,
         "SG_PAD_B": pad_b,
         "SG_KERNEL_NAME": name,

@@ -83,7 +83,12 @@ int main(int argc, char** argv) {
     sgemm_handle* h = nullptr;
     int r = sgemm_open(argv[1], argv[2], &h);
     if (r != SGEMM_OK) return shim_error("sgemm_open", r);
-    r = sgemm_check_shape(h, m, n, k, m, k, m, m);
+    sgemm_kernel_info info{};
+    if ((r = sgemm_get_info(h, &info)) != SGEMM_OK) {
+        sgemm_close(h);
+        return shim_error("sgemm_get_info", r);
+    }
+    r = sgemm_check_shape(h, m, n, k, info.trans_a ? k : m, info.trans_b ? n : k, m, m);
     if (r != SGEMM_OK) {
         std::cerr << sgemm_last_error() << "\n";
         sgemm_close(h);
@@ -101,9 +106,26 @@ int main(int argc, char** argv) {
     std::vector<float> ref;
     if (validate) {
         ref.assign((size_t)m * n, 0.0f);
+        // The stored A is k x m and B is n x k for transposed kernels; the CPU
+        // reference multiplies the column-major op(A) (m x k) and op(B) (k x n).
+        std::vector<float> opA, opB;
+        const float* pa = A.data();
+        const float* pb = B.data();
+        if (info.trans_a) {
+            opA.resize(A.size());
+            for (uint32_t l = 0; l < k; ++l)
+                for (uint32_t i = 0; i < m; ++i) opA[i + (size_t)l * m] = A[l + (size_t)i * k];
+            pa = opA.data();
+        }
+        if (info.trans_b) {
+            opB.resize(B.size());
+            for (uint32_t j = 0; j < n; ++j)
+                for (uint32_t l = 0; l < k; ++l) opB[l + (size_t)j * k] = B[j + (size_t)l * n];
+            pb = opB.data();
+        }
         const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
         const auto t0 = std::chrono::steady_clock::now();
-        runner_cpu_gemm(A.data(), B.data(), C.data(), ref.data(), alpha, beta, m, n, k, threads);
+        runner_cpu_gemm(pa, pb, C.data(), ref.data(), alpha, beta, m, n, k, threads);
         const auto t1 = std::chrono::steady_clock::now();
         std::cout << "cpuGemm func: " << std::chrono::duration<double, std::milli>(t1 - t0).count() << " ms ("
                   << threads << " threads of " << std::thread::hardware_concurrency() << ")\n";

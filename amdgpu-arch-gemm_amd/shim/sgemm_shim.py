@@ -40,6 +40,8 @@ class KernelInfo(ctypes.Structure):
         ("tile_m", ctypes.c_int),
         ("tile_n", ctypes.c_int),
         ("workitems", ctypes.c_int),
+        ("trans_a", ctypes.c_int),
+        ("trans_b", ctypes.c_int),
     ]
 
 
@@ -188,15 +190,21 @@ class Kernel:
     def tile(self) -> Tuple[int, int, int]:
         return self.info.tile_m, self.info.tile_n, self.info.depth_k
 
+    def default_lds(self, m, n, k) -> Tuple[int, int]:
+        """Tight (lda, ldb) for this kernel's transposition."""
+        return (k if self.info.trans_a else m), (n if self.info.trans_b else k)
+
     def check_shape(self, m, n, k, lda=None, ldb=None, ldc=None, ldd=None) -> Optional[str]:
         lib = load_library()
-        rc = lib.sgemm_check_shape(self.handle, m, n, k, lda or m, ldb or k, ldc or m, ldd or m)
+        da, db = self.default_lds(m, n, k)
+        rc = lib.sgemm_check_shape(self.handle, m, n, k, lda or da, ldb or db, ldc or m, ldd or m)
         return None if rc == 0 else lib.sgemm_last_error().decode()
 
     def _args(self, a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta):
         cp = c.ptr if c is not None else None
+        da, db = self.default_lds(m, n, k)
         return (self.handle, a.ptr if a is not None else None, b.ptr if b is not None else None, cp, d.ptr,
-                m, n, k, lda or m, ldb or k, ldc or m, ldd or m, alpha, beta)
+                m, n, k, lda or da, ldb or db, ldc or m, ldd or m, alpha, beta)
 
     def launch(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, lda=None, ldb=None, ldc=None, ldd=None):
         _check("sgemm_launch", load_library().sgemm_launch(*self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd,
@@ -223,11 +231,15 @@ class Kernel:
 
     def run(self, A: np.ndarray, B: np.ndarray, C: Optional[np.ndarray], m: int, n: int, k: int,
             alpha: float = 1.0, beta: float = 0.0, warmup: int = 0, runs: int = 1) -> Tuple[np.ndarray, float]:
-        """Host-buffer flow: returns (D as a column-major m x n array, ms per run)."""
+        """Host-buffer flow: returns (D as a column-major m x n array, ms per run).
+        A and B are the stored matrices: m x k (k x m for a trans_a kernel) and
+        k x n (n x k for a trans_b kernel)."""
         A = np.asfortranarray(A, dtype=np.float32)
         B = np.asfortranarray(B, dtype=np.float32)
-        if A.shape != (m, k) or B.shape != (k, n):
-            raise ValueError(f"A must be {m}x{k} and B {k}x{n}, got {A.shape} and {B.shape}")
+        sa = (k, m) if self.info.trans_a else (m, k)
+        sb = (n, k) if self.info.trans_b else (k, n)
+        if A.shape != sa or B.shape != sb:
+            raise ValueError(f"A must be {sa[0]}x{sa[1]} and B {sb[0]}x{sb[1]}, got {A.shape} and {B.shape}")
         cptr = None
         if C is not None:
             C = np.asfortranarray(C, dtype=np.float32)

@@ -69,6 +69,9 @@ SUPPORTED_VMEM_STAGES = [1, 2]
 # gfx950 space
 GFX950_MACRO_TILES = [(a, b) for a in (64, 128, 256) for b in (64, 128, 256)]
 GFX950_WAVE_GROUPS = [(2, 2), (4, 1)]
+# --space gfx950-wide: also 32-wide tiles and every wave group of the reference
+GFX950_WIDE_MACRO_TILES = [(a, b) for a in (32, 64, 128, 256) for b in (32, 64, 128, 256)]
+GFX950_WIDE_WAVE_GROUPS = SUPPORTED_WAVE_GROUPS + [(4, 1), (1, 4)]
 GFX950_DEPTH_K = [16, 32]
 GFX950_VMEM_STAGES = [1, 2]
 GFX950_WGM = [1, 4, 8]
@@ -109,8 +112,10 @@ def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
     return cfg.num_bytes_per_buffer_load == (16, 16)
 
 
-def geometry_points(knobs: Dict) -> Iterable[Point]:
-    for (mt0, mt1), wg, mfma in product(GFX950_MACRO_TILES, GFX950_WAVE_GROUPS, SUPPORTED_MFMAS):
+def geometry_points(knobs: Dict, wide: bool = False) -> Iterable[Point]:
+    tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
+    groups = GFX950_WIDE_WAVE_GROUPS if wide else GFX950_WAVE_GROUPS
+    for (mt0, mt1), wg, mfma in product(tiles, groups, SUPPORTED_MFMAS):
         if mt0 % (mfma[0] * wg[0]) or mt1 % (mfma[1] * wg[1]):
             continue
         wt = (mt0 // (mfma[0] * wg[0]), mt1 // (mfma[1] * wg[1]))
@@ -273,7 +278,7 @@ def main(argv=None):
     ap.add_argument("--k", dest="k", type=int, required=True, action="store")
     ap.add_argument("--bench", dest="bench", type=str, required=True, action="store")
     ap.add_argument("--output-folder", dest="output_folder", type=str, required=True, action="store")
-    ap.add_argument("--space", choices=["gfx950", "reference"], default="gfx950")
+    ap.add_argument("--space", choices=["gfx950", "gfx950-wide", "reference"], default="gfx950")
     ap.add_argument("--refine", type=int, default=3, help="geometries refined in stage 2")
     ap.add_argument("--results", default=None, help="JSONL results file (default <out>/results.jsonl)")
     ap.add_argument("--compile-only", action="store_true")
@@ -296,11 +301,12 @@ def main(argv=None):
     if args.space == "reference":
         stage1 = [p for p in reference_points() if fits(p[0], m, n, k)]
     else:
-        stage1 = [p for p in geometry_points(DEFAULT_KNOBS) if fits(p[0], m, n, k)]
+        stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide")
+                  if fits(p[0], m, n, k)]
 
     if args.compile_only:
         pts = list(stage1)
-        if args.all_shapes and args.space == "gfx950":
+        if args.all_shapes and args.space != "reference":
             for cfg, _ in stage1:
                 pts += [p for p in knob_points(cfg) if fits(p[0], m, n, k)]
         res = build_points(out, pts, args.jobs)
@@ -319,7 +325,7 @@ def main(argv=None):
         return build_points(out, points, args.jobs)
 
     recs = sweep(stage1, out, m, n, k, bench, args.timeout, results_path, compiled_for(stage1))
-    if args.space == "gfx950" and args.refine > 0:
+    if args.space != "reference" and args.refine > 0:
         ranked = sorted((r for r in recs if r["status"] == "ok"), key=lambda r: -r["gflops"])[:args.refine]
         by_key = {point_key(*p): p for p in stage1}
         stage2: List[Point] = []

@@ -19,9 +19,11 @@
  *     object module, its stream and its events.
  *   - One handle is used by one thread at a time.  All work of a handle runs
  *     in order on the handle's stream (default priority).
- *   - Matrices are column-major FP32: A is m x k (lda), B is k x n (ldb),
- *     C and D are m x n (ldc, ldd).  D = alpha * A * B + beta * C; C is not
- *     read when beta == 0.
+ *   - Matrices are column-major FP32.  D = alpha * op(A) * op(B) + beta * C
+ *     with op(A) m x k and op(B) k x n; A is stored m x k (lda >= m), or
+ *     k x m (lda >= k) for a kernel built with trans_a; B is stored k x n
+ *     (ldb >= k), or n x k (ldb >= n) with trans_b; C and D are m x n
+ *     (ldc, ldd >= m).  C is not read when beta == 0.
  */
 #ifndef SGEMM_SHIM_H
 #define SGEMM_SHIM_H
@@ -33,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 1
+#define SGEMM_SHIM_ABI_VERSION 2
 
 enum {
     SGEMM_OK = 0,
@@ -64,6 +66,8 @@ typedef struct sgemm_kernel_info {
     int tile_m;           /* MT0 = mfma[0] * wave_group[0] * wave_tiling[0] */
     int tile_n;           /* MT1 = mfma[1] * wave_group[1] * wave_tiling[1] */
     int workitems;        /* wave_group[0] * wave_group[1] * wavefront_size */
+    int trans_a;          /* 1: A is stored k x m (lda >= k), op(A) = A^T */
+    int trans_b;          /* 1: B is stored n x k (ldb >= n), op(B) = B^T */
 } sgemm_kernel_info;
 
 /* Message of the last failure on this thread ("" if none). */
@@ -89,8 +93,10 @@ int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info);
 
 /* Returns SGEMM_OK if the kernel can run this problem, SGEMM_E_SHAPE with a
  * message otherwise.  Any m, n, k is accepted (edge tiles and a K remainder are
- * masked in the kernel); lda >= m, ldb >= k, ldc >= m, ldd >= m are required,
- * and lda * depth_k, ldb * tile_n must stay below 2^32 elements. */
+ * masked in the kernel); the leading dimensions must cover the stored
+ * matrices (lda >= m, or k with trans_a; ldb >= k, or n with trans_b;
+ * ldc, ldd >= m), and one tile's span of A and of B must stay below 2^32
+ * elements. */
 int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd);
 
@@ -125,7 +131,8 @@ int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const flo
 /* Waits for all work of the handle's stream. */
 int sgemm_synchronize(sgemm_handle* h);
 
-/* Whole runner flow on host buffers with lda = m, ldb = k, ldc = ldd = m:
+/* Whole runner flow on host buffers with tight leading dimensions (lda = m
+ * or k, ldb = k or n as the kernel's transposition says, ldc = ldd = m):
  * allocate, upload A, B (and C when beta != 0), warm up, time `runs`
  * launches, download D, free.  *ms_per_run = event time / runs.
  * Replaces main()'s device part (generator_runner.cpp:232-291). */

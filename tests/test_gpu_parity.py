@@ -186,6 +186,48 @@ def test_arbitrary_shapes(kernels, name, m, n, k, pad):
     assert np.all(Dfull[m:, :] == -3.5), "rows past m of D were written"
 
 
+TRANS_CASES = [
+    # (instance, m, n, k, pad)
+    ("mt256x256_a32_wg2x2_dk16_s3_tn", 1024, 768, 512, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_nt", 1000, 700, 333, 1),
+    ("mt256x256_a32_wg2x2_dk16_s3_tt", 512, 512, 1024, 0),
+    ("mt64x64_a16_wg2x2_dk32_s3_tn", 300, 200, 100, 3),
+    ("mt32x32_a32_wg1x1_dk16_tt", 35, 59, 33, 1),
+    ("mt16x16_a16_wg1x1_dk16_nt", 19, 27, 33, 0),
+]
+
+
+@pytest.mark.parametrize("name,m,n,k,pad", TRANS_CASES)
+def test_transposed_layouts(kernels, name, m, n, k, pad):
+    """TN / NT / TT: A stored k x m (lda >= k) and/or B stored n x k (ldb >= n);
+    checked against the oracle on the explicitly transposed operands."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    _say(f"trans {name} {m}x{n}x{k} pad {pad}")
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    Af = S.fill_matrix(ra + pad, ca, 9, 0)
+    Bf = S.fill_matrix(rb + pad, cb, 9, 1)
+    C = S.fill_matrix(m, n, 9, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, C))
+    dD = S.DeviceBuffer(4 * m * n)
+    with _kernel(name) as kern:
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=1.5, lda=ra + pad, ldb=rb + pad, ldc=m, ldd=m)
+        kern.synchronize()
+    D = dD.download().reshape(n, m).T
+    opA = np.asfortranarray(Af[:ra, :ca].T if cfg.trans_a else Af[:m, :k])
+    opB = np.asfortranarray(Bf[:rb, :cb].T if cfg.trans_b else Bf[:k, :n])
+    _check(D, oracle.cpu_gemm_mt(opA, opB, C, 0.5, 1.5, threads=16), k, name)
+
+
+def test_runner_validates_a_transposed_kernel(kernels):
+    co, toml = catalog.paths("mt256x256_a32_wg2x2_dk16_s3_tt")
+    ret = _run([RUNNER, co, toml, "777", "1000", "515", "1", "2", "1", "3"])
+    out = ret.stdout.decode()
+    _say(out)
+    assert ret.returncode == 0, out
+    assert "validation: PASS" in out
+
+
 # ---------------------------------------------------------------- configs
 BASELINE_CONFIGS = [
     # (id, m, n, k, seed, dist)

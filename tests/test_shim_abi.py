@@ -34,7 +34,8 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 1
+    assert lib.sgemm_abi_version() == 2
+    assert ctypes.sizeof(S.KernelInfo) == 4 * 19
 
 
 def test_no_device_is_an_error_code_not_a_crash(tmp_path):
@@ -57,7 +58,9 @@ def test_open_reports_missing_files_and_bad_configs(tmp_path):
     bad.write_text(open(toml).read().replace("depth_k = 16\n", ""))
     assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
     assert b"depth_k" in lib.sgemm_last_error()
-    bad.write_text(open(toml).read().replace("trans_a = false", "trans_a = true"))
+    bad.write_text(open(toml).read().replace("a_type = 0", "a_type = 1"))
+    assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+    bad.write_text(open(toml).read().replace("trans_a = false", "trans_a = 1"))
     assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
     bad.write_text(open(toml).read().replace("mfma = [32, 32, 1, 2]", "mfma = [4, 4, 4, 4]"))
     assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3

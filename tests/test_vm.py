@@ -255,6 +255,25 @@ def test_edge_shapes_stay_inside_every_buffer(name, m, n, k, pad):
     assert np.all(D[m:, :] == 0), "rows past m of D were written"
 
 
+@pytest.mark.parametrize("name", ["mt32x32_a32_wg1x1_dk16_tt", "mt16x16_a16_wg1x1_dk16_nt",
+                                  "mt64x64_a16_wg2x2_dk32_s3_tn"])
+@pytest.mark.parametrize("shape,pad", [((None, None, None), 0), ((35, 59, 33), 1), ((5, 3, 1), 0)])
+def test_transposed_layouts_in_vm(name, shape, pad):
+    """op(A) = A^T and/or op(B) = B^T, with guarded buffers."""
+    prog, cfg = program(name)
+    t0, t1 = cfg.tile_size
+    m, n, k = (2 * t0, 2 * t1, 3 * cfg.depth_k) if shape[0] is None else shape
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    A = oracle.fill_matrix(ra + pad, ca, 4, 0)
+    B = oracle.fill_matrix(rb + pad, cb, 4, 1)
+    C = oracle.fill_matrix(m, n, 4, 2)
+    D, _ = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m)
+    opA = A[:ra, :ca].T if cfg.trans_a else A[:m, :k]
+    opB = B[:rb, :cb].T if cfg.trans_b else B[:k, :n]
+    assert oracle.normwise_error(D[:m, :n], oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+
+
 def test_an_undersized_buffer_is_caught():
     # A one float short of m*k: the kernel's last read of A leaves the buffer
     prog, cfg = program("mt32x32_a32_wg1x1_dk16")
