@@ -54,7 +54,6 @@ def test_gfx950_lds_limit_is_160k():
     (dict(wt=(1, 9)), "wave tiling"),
     (dict(dk=6), "depth_k"),
     (dict(dk=12), "k block"),
-    (dict(ta=True), "NN layout"),
     (dict(stages=0), "vmem_stage"),
     (dict(wg=(8, 4), wt=(1, 1)), "exceeds 1024"),
 ])

@@ -45,16 +45,26 @@ def _small_shape(name, mult=(2, 3, 3)):
 
 
 @pytest.mark.parametrize("name", list(catalog.SOLUTIONS))
+def _operands(name, m, n, k, seed, dist=S.SGEMM_DIST_UNIFORM):
+    """(stored A, stored B, op(A), op(B)) for an instance's transposition."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    A = S.fill_matrix(*((k, m) if cfg.trans_a else (m, k)), seed, 0, dist)
+    B = S.fill_matrix(*((n, k) if cfg.trans_b else (k, n)), seed, 1, dist)
+    opA = np.asfortranarray(A.T) if cfg.trans_a else A
+    opB = np.asfortranarray(B.T) if cfg.trans_b else B
+    return A, B, opA, opB
+
+
+@pytest.mark.parametrize("name", list(catalog.SOLUTIONS))
 def test_every_instance_alpha_beta(kernels, name):
-    """D = alpha*A*B + beta*C on a 2x3-tile grid with 3 K tiles, C read."""
+    """D = alpha*op(A)*op(B) + beta*C on a 2x3-tile grid with 3 K tiles, C read."""
     m, n, k = _small_shape(name)
     _say(f"instance {name} {m}x{n}x{k}")
-    A = S.fill_matrix(m, k, 11, 0)
-    B = S.fill_matrix(k, n, 11, 1)
+    A, B, opA, opB = _operands(name, m, n, k, 11)
     C = S.fill_matrix(m, n, 11, 2)
     with _kernel(name) as kern:
         D, _ = kern.run(A, B, C, m, n, k, alpha=0.75, beta=-1.5)
-    _check(D, oracle.cpu_gemm(A, B, C, 0.75, -1.5), k, name)
+    _check(D, oracle.cpu_gemm(opA, opB, C, 0.75, -1.5), k, name)
 
 
 @pytest.mark.parametrize("name", list(catalog.SOLUTIONS))
@@ -62,8 +72,7 @@ def test_every_instance_beta0_ignores_c(kernels, name):
     """beta = 0: C is not read (a NaN-filled C must not leak into D)."""
     m, n, k = _small_shape(name, (1, 2, 5))
     _say(f"instance {name} beta0 {m}x{n}x{k}")
-    A = S.fill_matrix(m, k, 12, 0, S.SGEMM_DIST_NORMAL)
-    B = S.fill_matrix(k, n, 12, 1, S.SGEMM_DIST_NORMAL)
+    A, B, opA, opB = _operands(name, m, n, k, 12, S.SGEMM_DIST_NORMAL)
     dA, dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
     dC = S.DeviceBuffer.from_array(np.full((m, n), np.nan, dtype=np.float32))
     dD = S.DeviceBuffer(m * n * 4)
@@ -71,7 +80,7 @@ def test_every_instance_beta0_ignores_c(kernels, name):
         kern.launch(dA, dB, dC, dD, m, n, k, alpha=1.0, beta=0.0)
         kern.synchronize()
     D = dD.download().reshape(n, m).T
-    _check(D, oracle.cpu_gemm(A, B, None, 1.0, 0.0), k, name)
+    _check(D, oracle.cpu_gemm(opA, opB, None, 1.0, 0.0), k, name)
 
 
 # The reference VM's full-kernel cases (test_vm.py:447-537 and :539-627):
