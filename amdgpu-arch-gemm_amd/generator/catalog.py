@@ -37,6 +37,11 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt64x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     "mt128x64_a16_wg2x2_dk16_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=2), _opt(wgm=4, plr=1, xcd=8)),
     "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    # winners of the wide sweep (all wave groups, 32..256 tiles)
+    "mt256x256_a32_wg4x2_dk16_s3": (_cfg(MFMA_32x32x2, (4, 2), (2, 4), 16, stages=2), _opt(wgm=8, plr=3, xcd=8)),
+    "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2), _opt(wgm=8, plr=3, xcd=8)),
+    "mt128x64_a16_wg2x2_dk16_s2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1), _opt(wgm=1, plr=3, xcd=0)),
+    "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     # the first-generation schedule (refill after the last block), kept as a baseline
     "mt256x256_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, xcd=8)),
     "mt256x256_a32_wg2x2_dk16_plr2": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, plr=2, xcd=8)),
@@ -74,8 +79,8 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 # shape class -> preferred instance (filled from tuner results; see select())
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk16_s3"),
-    ((1024, 1024, 1024), "mt64x64_a16_wg2x2_dk32_s3"),
-    ((8192, 8192, 256), "mt128x64_a16_wg2x2_dk16_s3"),
+    ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
+    ((8192, 8192, 256), "mt128x64_a16_wg2x2_dk16_s2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
 ]
 
