@@ -89,6 +89,9 @@
 #ifndef SG_PLR
 #define SG_PLR 1
 #endif
+#ifndef SG_PD
+#define SG_PD 1
+#endif
 #ifndef SG_GW
 #define SG_GW 0
 #endif
@@ -356,7 +359,11 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             b_lds[i] = G::A_STAGE + (c0 * 4) * G::B_LD + c1;
         }
     }
-    f32x4 ra[G::LA], rb[G::LB];
+    // PD register staging sets: with the early-refill schedules a K tile's
+    // global loads are issued PD tiles before its LDS writes.
+    constexpr int PD = (SG_PLR >= 2) ? SG_PD : 1;
+    static_assert(PD == 1 || PD == 2, "prefetch depth must be 1 or 2");
+    f32x4 ra[PD][G::LA], rb[PD][G::LB];
 
     int kt_first = 0;
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
@@ -364,7 +371,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     // gload(tag, t): global -> VGPR copy of K tile t.  With a SlowPath tag every
     // element is loaded from a clamped (always valid) address and replaced by
     // 0 when it lies outside A or B, so the code stays branch-free.
-    auto gload = [&](auto path, int t) __attribute__((always_inline)) {
+    auto gload = [&](auto path, int t, int set) __attribute__((always_inline)) {
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
         if constexpr (!decltype(path)::slow) {
@@ -373,11 +380,11 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
 #pragma unroll
             for (int i = 0; i < G::LA; ++i)
                 if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
-                    ra[i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+                    ra[set][i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
 #pragma unroll
             for (int i = 0; i < G::LB; ++i)
                 if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
-                    rb[i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+                    rb[set][i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
         } else {
             const uint32_t k0 = (uint32_t)kt * DK;
 #pragma unroll
@@ -392,7 +399,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
                         const uint32_t rc = row < m ? row : m - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TA ? a[(size_t)rc * lda + kc] : a[(size_t)kc * lda + rc];
-                        ra[i][e] = (row < m && kk < k) ? x : 0.0f;
+                        ra[set][i][e] = (row < m && kk < k) ? x : 0.0f;
                     }
                 }
             }
@@ -408,32 +415,32 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
                         const uint32_t cc = col < n ? col : n - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TB ? b[(size_t)kc * ldb + cc] : b[(size_t)cc * ldb + kc];
-                        rb[i][e] = (col < n && kk < k) ? x : 0.0f;
+                        rb[set][i][e] = (col < n && kk < k) ? x : 0.0f;
                     }
                 }
             }
         }
     };
-    auto swrite = [&](int buf) __attribute__((always_inline)) {
+    auto swrite = [&](int buf, int set) __attribute__((always_inline)) {
         float* s = lds + buf * G::STAGE;
 #pragma unroll
         for (int i = 0; i < G::LA; ++i)
             if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS) {
                 if constexpr (!TA) {
-                    *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[i];
+                    *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[set][i];
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) s[a_lds[i] + e * G::A_LD] = ra[i][e];
+                    for (int e = 0; e < 4; ++e) s[a_lds[i] + e * G::A_LD] = ra[set][i][e];
                 }
             }
 #pragma unroll
         for (int i = 0; i < G::LB; ++i)
             if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS) {
                 if constexpr (!TB) {
-                    *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[i];
+                    *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[set][i];
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) s[b_lds[i] + e * G::B_LD] = rb[i][e];
+                    for (int e = 0; e < 4; ++e) s[b_lds[i] + e * G::B_LD] = rb[set][i][e];
                 }
             }
     };
@@ -509,11 +516,14 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     #pragma unroll
         for (int s = 0; s < NBUF - 1; ++s) {
             if (s < ktiles) {
-                gload(path, s);
-                swrite(s);
+                gload(path, s, 0);
+                swrite(s, 0);
             }
         }
-        if (NBUF - 1 < ktiles) gload(path, NBUF - 1);
+        // tiles NBUF - 1 .. NBUF + PD - 2 go to the register sets
+    #pragma unroll
+        for (int j = 0; j < PD; ++j)
+            if (NBUF - 1 + j < ktiles) gload(path, NBUF - 1 + j, (NBUF - 1 + j) % PD);
         __syncthreads();
 
         if constexpr (SG_PLR >= 2) {
@@ -523,12 +533,18 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
             // With NBUF >= 3 the first operands of tile t + 1 (written in iteration
             // t - 1) are read before the barrier too, so nothing but the barrier
             // separates the last MFMA of one tile from the first of the next.
+            // Iteration t writes tile t + NBUF - 1 from register set
+            // (t + NBUF - 1) % PD and refills that set with tile t + NBUF - 1 + PD,
+            // so a tile's global loads have PD iterations to arrive.
+            constexpr int U = (PD == 2 && NBUF % 2) ? 2 * NBUF : NBUF;  // lcm(NBUF, PD)
             Frag cur, nxt;
             if (ktiles > 0) load_frag(lds, 0, cur);
-            for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+            for (int t0 = 0; t0 < ktiles; t0 += U) {
     #pragma unroll
-                for (int u = 0; u < NBUF; ++u) {
-                    const int t = t0 + u;
+                for (int uu = 0; uu < U; ++uu) {
+                    const int t = t0 + uu;
+                    const int u = uu % NBUF;
+                    const int set = (uu + NBUF - 1) % PD;
                     if (t < ktiles) {
                         const float* s = lds + u * G::STAGE;
     #pragma unroll
@@ -542,8 +558,8 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
                             else if (NBUF >= 3) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, nxt);
                             mfma_frag(cur);
                             if (kb == 0) {
-                                swrite((u + NBUF - 1) % NBUF);
-                                gload(path, min(t + NBUF, ktiles - 1));
+                                swrite((u + NBUF - 1) % NBUF, set);
+                                gload(path, min(t + NBUF - 1 + PD, ktiles - 1), set);
                             }
                             if constexpr (SG_PLR >= 3) {
                                 constexpr int NMFMA = KPL * WT0 * WT1;
@@ -567,8 +583,8 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
                     const int t = t0 + u;
                     if (t < ktiles) {
                         compute(u);
-                        if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF);
-                        if (t + NBUF < ktiles) gload(path, t + NBUF);
+                        if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF, 0);
+                        if (t + NBUF < ktiles) gload(path, t + NBUF, 0);
                         __syncthreads();
                     }
                 }

@@ -26,8 +26,8 @@ def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0):
-    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd)
+def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0, pd=1):
+    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd)
 
 
 # name -> (config, optimizations)
@@ -42,6 +42,17 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2), _opt(wgm=8, plr=3, xcd=8)),
     "mt128x64_a16_wg2x2_dk16_s2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1), _opt(wgm=1, plr=3, xcd=0)),
     "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
+    "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
+                                       _opt(wgm=4, plr=3, xcd=8, pd=2)),
+    "mt128x64_a16_wg2x2_dk16_s2_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1),
+                                       _opt(wgm=1, plr=3, xcd=0, pd=2)),
+    "mt64x64_a16_wg1x4_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2),
+                                      _opt(wgm=8, plr=3, xcd=8, pd=2)),
+    "mt256x256_a32_wg2x2_dk16_s3_pd2": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2),
+                                        _opt(wgm=4, plr=3, xcd=8, pd=2)),
+    "mt16x16_a16_wg1x1_dk16_s3_pd2": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, mapk=4, pd=2)),
+    "mt32x32_a32_wg1x1_dk16_s2_pd2": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, stages=1), _opt(plr=2, pd=2)),
     # the first-generation schedule (refill after the last block), kept as a baseline
     "mt256x256_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, xcd=8)),
     "mt256x256_a32_wg2x2_dk16_plr2": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16), _opt(wgm=4, plr=2, xcd=8)),

@@ -98,6 +98,9 @@ class GemmOptimizations:
     * ``map_k_idx`` -- rotate the first K tile by ``tile_x & (map_k_idx - 1)``.
     * ``xcd``       -- (gfx950 only) number of XCDs to give contiguous tile
                        ranges to; 0 or 1 leaves the hardware order.
+    * ``pd``        -- (gfx950 only) prefetch depth of the early-refill
+                       schedules: a K tile's global loads are issued ``pd``
+                       tiles before its LDS writes (1 or 2 register sets).
     """
 
     def __init__(
@@ -108,6 +111,7 @@ class GemmOptimizations:
         gw: Optional[int] = None,
         map_k_idx: Optional[int] = None,
         xcd: Optional[int] = None,
+        pd: Optional[int] = None,
     ):
         self.level = level
         self.wgm = 1
@@ -115,6 +119,7 @@ class GemmOptimizations:
         self.gw = 0
         self.map_k_idx = 0
         self.xcd = 0
+        self.pd = 1
         self._setup_optimizations()
         if wgm is not None:
             self.wgm = wgm
@@ -126,12 +131,16 @@ class GemmOptimizations:
             self.map_k_idx = map_k_idx
         if xcd is not None:
             self.xcd = xcd
+        if pd is not None:
+            self.pd = pd
         if self.wgm < 1:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
             raise RuntimeError(f"map_k_idx must be 0 or a power of two: {self.map_k_idx}")
         if self.plr not in (0, 1, 2, 3) or self.gw not in (0, 1) or self.xcd < 0:
             raise RuntimeError(f"Invalid optimization knobs: plr={self.plr} gw={self.gw} xcd={self.xcd}")
+        if self.pd not in (1, 2) or (self.pd == 2 and self.plr < 2):
+            raise RuntimeError(f"Invalid prefetch depth {self.pd} (2 needs plr >= 2)")
 
     def _setup_optimizations(self):
         if self.level != 0:
@@ -146,11 +155,12 @@ class GemmOptimizations:
             "gw": int(self.gw),
             "map_k_idx": int(self.map_k_idx),
             "xcd": int(self.xcd),
+            "pd": int(self.pd),
         }
 
     def __repr__(self) -> str:
         return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
-                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd})")
+                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd})")
 
 
 def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int,
@@ -497,6 +507,7 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_NBUF": config.vmem_stage + 1,
         "SG_WGM": opt.wgm,
         "SG_XCD": opt.xcd,
+        "SG_PD": opt.pd,
         "SG_MAPK": opt.map_k_idx,
         "SG_PLR": opt.plr,
         "SG_GW": opt.gw,

@@ -13,6 +13,7 @@ stdout line) and print the best.  Additions:
 * ``--space gfx950`` (default): macro-tile {64,128,256}^2 x wave-group
   {2x2, 4x1} x MFMA atom {32x32x2, 16x16x4} (stage 1), then the code-shape
   knobs depth_k {16,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
+  x prefetch depth {1,2}
   on the best ``--refine`` geometries (stage 2).  ``--space reference`` is the
   reference's own 9-knob product.
 * every result is appended to ``<out>/results.jsonl`` and a rerun skips
@@ -77,6 +78,7 @@ GFX950_VMEM_STAGES = [1, 2]
 GFX950_WGM = [1, 4, 8]
 GFX950_XCD = [0, 8]
 GFX950_PLR = [1, 2, 3]
+GFX950_PD = [1, 2]
 DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=2, wgm=4, xcd=8, plr=3, gw=0, map_k_idx=0)
 ARCH = "gfx950"
 VERBOSE = False
@@ -87,13 +89,14 @@ Point = Tuple[GemmSolutionConfig, GemmOptimizations]
 
 def point_key(cfg: GemmSolutionConfig, opt: GemmOptimizations) -> str:
     return (f"a{cfg.mfma[0]}_wg{cfg.wave_group[0]}x{cfg.wave_group[1]}_wt{cfg.wave_tiling[0]}x{cfg.wave_tiling[1]}"
-            f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}")
+            f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}"
+            + (f"_pd{opt.pd}" if opt.pd != 1 else ""))
 
 
-def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd) -> Optional[Point]:
+def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1) -> Optional[Point]:
     try:
         cfg = GemmSolutionConfig(F, F, F, F, mfma, wg, wt, depth_k, False, False, vmem_stage=vmem_stage)
-        opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd)
+        opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd, pd=pd)
     except RuntimeError as e:
         if VERBOSE:
             print(e)
@@ -126,8 +129,11 @@ def geometry_points(knobs: Dict, wide: bool = False) -> Iterable[Point]:
 
 
 def knob_points(cfg: GemmSolutionConfig) -> Iterable[Point]:
-    for dk, st, wgm, xcd, plr in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM, GFX950_XCD, GFX950_PLR):
-        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, 0, 0, xcd)
+    for dk, st, wgm, xcd, plr, pd in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM, GFX950_XCD,
+                                             GFX950_PLR, GFX950_PD):
+        if pd == 2 and plr < 2:
+            continue
+        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, 0, 0, xcd, pd)
         if p:
             yield p
 
