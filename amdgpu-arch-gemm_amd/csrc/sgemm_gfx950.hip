@@ -92,6 +92,9 @@
 #ifndef SG_PD
 #define SG_PD 1
 #endif
+#ifndef SG_OCC
+#define SG_OCC 0
+#endif
 #ifndef SG_GW
 #define SG_GW 0
 #endif
@@ -110,12 +113,25 @@
 #ifndef SG_KERNEL_NAME
 #define SG_KERNEL_NAME generated_gemm
 #endif
+#ifndef SG_SPLITK
+#define SG_SPLITK 0
+#endif
+#ifndef SG_KERNEL_NAME_SPLITK
+#define SG_KERNEL_NAME_SPLITK generated_gemm_splitk
+#endif
 
 namespace sg {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family GPUs.
+constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
+// Cache-policy operand of the buffer intrinsics on gfx94x/gfx950: bit 0 sc0,
+// bit 1 nt, bit 4 sc1; sc1 alone is device scope (coherent across XCDs).
+constexpr int CPOL_SC1 = 0x10;
 
 template <int N> struct Vec;
 template <> struct Vec<1> { typedef float type; };
@@ -286,17 +302,34 @@ __device__ __forceinline__ void tile_coords(int bx, int by, int nwgx, int nwgy, 
 
 }  // namespace sg
 
-extern "C" __global__ void __launch_bounds__(sg::G::NT)
-SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
-               const float* __restrict__ c, float* __restrict__ d,
-               uint32_t m, uint32_t n, uint32_t k,
-               uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
-               float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY) {
+// SG_OCC > 0 asks the compiler for at least SG_OCC waves per SIMD (registers
+// capped at 512 / SG_OCC per lane), so that SG_OCC work-groups of one wave
+// per SIMD can share a CU and hide each other's barrier waits.
+#if SG_OCC > 0
+#define SG_OCC_ATTR __attribute__((amdgpu_waves_per_eu(SG_OCC, SG_OCC)))
+#else
+#define SG_OCC_ATTR
+#endif
+
+// One output tile: the K loop over [0, k) of the (already offset) operands,
+// then the epilogue.  With SPLIT the work-group covers K range blockIdx.z of
+// `splits` equal ranges (whole K tiles), writes its raw partial tile to `ws`,
+// and the last of the tile's work-groups to take a ticket reduces the
+// partials and runs the epilogue.
+template <bool SPLIT>
+__device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const float* __restrict__ b,
+                                          const float* __restrict__ c, float* __restrict__ d,
+                                          uint32_t m, uint32_t n, uint32_t k_total,
+                                          uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                                          float alpha, float beta, int32_t numWorkgroupX,
+                                          int32_t numWorkgroupY, float* ws, uint32_t* tickets,
+                                          uint32_t splits) {
     using namespace sg;
     typedef G::atom AT;
     typedef AT::acc_t acc_t;
     constexpr int NT = G::NT, MT0 = G::MT0, MT1 = G::MT1, DK = SG_DK, NBUF = SG_NBUF;
     constexpr int WT0 = SG_WT0, WT1 = SG_WT1, KPL = G::KPL, KB = G::KB;
+    constexpr bool TA = SG_TA != 0, TB = SG_TB != 0;
 
     __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
 
@@ -310,6 +343,21 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     tile_coords(blockIdx.x, blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
+
+    // K range of this work-group: all of it, or split blockIdx.z of `splits`
+    // ranges of whole K tiles (the last range takes the remainder; ranges past
+    // the end are empty and contribute a zero partial).
+    uint32_t k = k_total;
+    if constexpr (SPLIT) {
+        const uint32_t kt_all = (k_total + DK - 1) / DK;
+        const uint32_t per = (kt_all + splits - 1) / splits;
+        const uint32_t t_first = min((uint32_t)blockIdx.z * per, kt_all);
+        const uint32_t k_first = t_first * DK;
+        const uint32_t k_end = min(k_first + per * DK, k_total);
+        k = k_end > k_first ? k_end - k_first : 0u;
+        a += TA ? (size_t)k_first : (size_t)k_first * lda;
+        b += TB ? (size_t)k_first * ldb : (size_t)k_first;
+    }
     const int ktiles = (int)((k + DK - 1) / DK);
     // Uniform per work-group: the vector fast path needs a whole tile inside D
     // and 16-byte aligned rows of every operand; otherwise loads and stores go
@@ -326,7 +374,6 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     // ds_write_b128; chunks across it (the transposed operands) are scattered
     // with four ds_write_b32, so the LDS layouts and reads never change:
     //   A: [DK][MT0 + PAD_A] (m contiguous), B: [MT1][DK + PAD_B] (k contiguous).
-    constexpr bool TA = SG_TA != 0, TB = SG_TB != 0;
     // per chunk: (i0, i1) = position along (contiguous dim / 4, other dim)
     constexpr int A_C0 = TA ? DK / 4 : MT0 / 4;   // chunks along the contiguous dim of A
     constexpr int B_C0 = TB ? MT1 / 4 : DK / 4;   // chunks along the contiguous dim of B
@@ -594,6 +641,78 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
     if (slow_mn || kt_partial >= 0) kloop(SlowPath{});
     else kloop(FastPath{});
 
+    if constexpr (SPLIT) {
+        // ---- split-K: publish the partial, the tile's last arrival reduces ----
+        // Partial s of a tile: float4 chunk ch of thread tid (slots 4h..4h+3
+        // of atom (i, j), ch = (i * WT1 + j) * ACC / 4 + h) is float4 number
+        // (s * CH + ch) * NT + tid of the tile's workspace.
+        //
+        // Partials are written and read with device-scope (sc1) buffer
+        // accesses, coherent across the XCDs' L2 caches by themselves, and the
+        // ticket is an agent-scope relaxed atomic: no device-scope fence, which
+        // would write back and invalidate a whole L2 per use.  Ordering: each
+        // wave waits for its partial stores to be acknowledged (vmcnt(0))
+        // before the barrier after which one thread takes the ticket, and the
+        // last arrival issues its partial loads only after its ticket returned.
+        constexpr int HC = AT::ACC / 4;
+        constexpr int CH = WT0 * WT1 * HC;
+        constexpr uint32_t PART_BYTES = (uint32_t)CH * NT * 16;
+        const uint32_t tile = (uint32_t)tx + (uint32_t)ty * (uint32_t)numWorkgroupX;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)tile * splits * (PART_BYTES / 4), (short)0,
+                                              (int)(splits * PART_BYTES), BUFFER_RSRC_WORD3);
+#pragma unroll
+        for (int i = 0; i < WT0; ++i)
+#pragma unroll
+            for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                for (int h = 0; h < HC; ++h) {
+                    const int ch = (i * WT1 + j) * HC + h;
+                    f32x4 v;
+                    v.x = acc[i][j][4 * h]; v.y = acc[i][j][4 * h + 1];
+                    v.z = acc[i][j][4 * h + 2]; v.w = acc[i][j][4 * h + 3];
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (ch * NT + tid) * 16,
+                                                           (int)(blockIdx.z * PART_BYTES), CPOL_SC1);
+                }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __shared__ uint32_t arrived;
+        __syncthreads();
+        if (tid == 0)
+            arrived = __hip_atomic_fetch_add(tickets + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived + 1 != splits) return;
+        // Sum partials 0, 1, ..., splits - 1 in that order (the own one is
+        // re-read too), so the result does not depend on the arrival order.
+        auto read_part = [&](uint32_t sp, int ch) __attribute__((always_inline)) {
+            return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (ch * NT + tid) * 16,
+                                                                                    (int)(sp * PART_BYTES), CPOL_SC1));
+        };
+#pragma unroll
+        for (int i = 0; i < WT0; ++i)
+#pragma unroll
+            for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                for (int h = 0; h < HC; ++h) {
+                    const f32x4 v = read_part(0, (i * WT1 + j) * HC + h);
+                    acc[i][j][4 * h] = v.x; acc[i][j][4 * h + 1] = v.y;
+                    acc[i][j][4 * h + 2] = v.z; acc[i][j][4 * h + 3] = v.w;
+                }
+        for (uint32_t sp = 1; sp < splits; ++sp) {
+#pragma unroll
+            for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                    for (int h = 0; h < HC; ++h) {
+                        const f32x4 v = read_part(sp, (i * WT1 + j) * HC + h);
+                        acc[i][j][4 * h] += v.x; acc[i][j][4 * h + 1] += v.y;
+                        acc[i][j][4 * h + 2] += v.z; acc[i][j][4 * h + 3] += v.w;
+                    }
+        }
+        // every arrival of this launch has been counted: re-arm for the next one
+        if (tid == 0) __hip_atomic_store(tickets + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // ---- epilogue: D = alpha * acc + beta * C ----
     const int wrow = row0 + wm * (AT::M * WT0);
     const int wcol = col0 + wn * (AT::N * WT1);
@@ -628,3 +747,33 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
         }
     }
 }
+
+extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
+SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
+               const float* __restrict__ c, float* __restrict__ d,
+               uint32_t m, uint32_t n, uint32_t k,
+               uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+               float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY) {
+    gemm_tile<false>(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, numWorkgroupX, numWorkgroupY,
+                     nullptr, nullptr, 1u);
+}
+
+#if SG_SPLITK
+// Split-K variant: the reference's 15 arguments, then
+//   offset 80 ws (float*)   88 tickets (uint32_t*)   96 splits (uint32_t) -> 100 B, padded to 104
+// Launch: grid = (numWorkgroupX, numWorkgroupY, splits), splits >= 1.
+// ws holds numWorkgroupX * numWorkgroupY * splits * MT0 * MT1 floats;
+// tickets holds numWorkgroupX * numWorkgroupY zeros before the first launch
+// and is left zeroed by every launch.  Launches sharing ws/tickets must not
+// overlap.
+extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
+SG_KERNEL_NAME_SPLITK(const float* __restrict__ a, const float* __restrict__ b,
+                      const float* __restrict__ c, float* __restrict__ d,
+                      uint32_t m, uint32_t n, uint32_t k,
+                      uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                      float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY,
+                      float* ws, uint32_t* tickets, uint32_t splits) {
+    gemm_tile<true>(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, numWorkgroupX, numWorkgroupY,
+                    ws, tickets, splits);
+}
+#endif

@@ -184,6 +184,10 @@ int load_config(const char* path, sgemm_kernel_info* info) {
     CFG_TRY(toml_int(t, "wavefront_size", &info->wavefront_size));
     CFG_TRY(toml_int(t, "lds_usage_bytes", &info->lds_usage_bytes));
     CFG_TRY(toml_int(t, "vmem_stage", &info->vmem_stage, false, 1));
+    // default split count of generated_gemm_splitk (absent: no split; 0: per problem)
+    CFG_TRY(toml_int(t, "split_k", &info->split_k, false, 1));
+    if (info->split_k < 0 || info->split_k > SGEMM_MAX_SPLIT_K)
+        return fail(SGEMM_E_CONFIG, "split_k = %d outside 0..%d", info->split_k, SGEMM_MAX_SPLIT_K);
     if (a_type || b_type || cd_type || scalar_type) return fail(SGEMM_E_CONFIG, "only FP32 (type 0) kernels are supported");
     info->trans_a = trans_a ? 1 : 0;
     info->trans_b = trans_b ? 1 : 0;
@@ -221,6 +225,50 @@ static_assert(sizeof(KernArgs) == 80, "kernarg image must be 80 bytes");
 static_assert(offsetof(KernArgs, m) == 32 && offsetof(KernArgs, ldd) == 56, "kernarg offsets");
 static_assert(offsetof(KernArgs, alpha) == 60 && offsetof(KernArgs, beta) == 64, "kernarg offsets");
 static_assert(offsetof(KernArgs, num_wg_x) == 68 && offsetof(KernArgs, num_wg_y) == 72, "kernarg offsets");
+
+// generated_gemm_splitk: the same 15 arguments, then its workspace, the
+// per-tile tickets and the split count: 100 bytes, padded to 104.
+struct KernArgsSplit {
+    KernArgs base;
+    float* ws;
+    uint32_t* tickets;
+    uint32_t splits;
+    uint32_t pad;
+};
+static_assert(sizeof(KernArgsSplit) == 104, "split kernarg image must be 104 bytes");
+static_assert(offsetof(KernArgsSplit, ws) == 80 && offsetof(KernArgsSplit, tickets) == 88 &&
+              offsetof(KernArgsSplit, splits) == 96, "split kernarg offsets");
+
+// K ranges a launch really uses: the configured count (or, for 0, the
+// per-problem choice documented at sgemm_set_split_k), at most one per K tile.
+uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_t m, uint32_t n, uint32_t k) {
+    const uint32_t ktiles = (k + (uint32_t)i.depth_k - 1) / (uint32_t)i.depth_k;
+    uint64_t s = (uint32_t)i.split_k;
+    if (s == 0) {
+        // Work-groups run in rounds of one per compute unit; a range of K/s
+        // per work-group makes the time ~ rounds(T * s) / s.  Pick the s with
+        // the fewest rounds per unit of K work (the smallest s among ties),
+        // keeping at least 4 K tiles per range.
+        const uint64_t tiles = (uint64_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+                               ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+        const uint64_t cus = compute_units > 0 ? (uint64_t)compute_units : 1;
+        s = 1;
+        if (tiles > 0 && tiles < cus) {
+            uint64_t smax = (uint64_t)i.split_k_max;
+            if (smax > ktiles / 4) smax = ktiles / 4;
+            uint64_t best_rounds = 1;  // rounds(T * s) / s compared as fractions
+            for (uint64_t c = 2; c <= smax; ++c) {
+                const uint64_t rounds = (tiles * c + cus - 1) / cus;
+                if (rounds * s < best_rounds * c) {
+                    s = c;
+                    best_rounds = rounds;
+                }
+            }
+        }
+    }
+    if (s > ktiles) s = ktiles;
+    return s < 1 ? 1 : (uint32_t)s;
+}
 
 // ------------------------------------------------------- seeded values ---
 const uint64_t kGamma = 0x9E3779B97F4A7C15ull;
@@ -261,6 +309,12 @@ struct sgemm_handle {
     hipEvent_t ev_start = nullptr;
     hipEvent_t ev_stop = nullptr;
     sgemm_kernel_info info{};
+    hipFunction_t function_splitk = nullptr;  // null when the code object has none
+    void* ws = nullptr;                       // split partials, grown on demand
+    size_t ws_bytes = 0;
+    uint32_t* tickets = nullptr;              // one per output tile, zero between launches
+    size_t ticket_count = 0;
+    int compute_units = 0;                    // of the device the module is loaded on
 };
 
 extern "C" {
@@ -305,6 +359,24 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
         return hip_fail(err, "hipModuleLoad");
     }
     err = hipModuleGetFunction(&h->function, h->module, "generated_gemm");
+    if (err == hipSuccess) {
+        // optional second kernel; its absence only limits split_k to 1
+        if (hipModuleGetFunction(&h->function_splitk, h->module, "generated_gemm_splitk") != hipSuccess) {
+            h->function_splitk = nullptr;
+            (void)hipGetLastError();
+        }
+        h->info.split_k_max = h->function_splitk ? SGEMM_MAX_SPLIT_K : 1;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&h->compute_units, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            h->compute_units = 0;
+            (void)hipGetLastError();
+        }
+        if (h->info.split_k > h->info.split_k_max) {
+            sgemm_close(h);
+            return fail(SGEMM_E_CONFIG, "split_k = %d but %s has no generated_gemm_splitk", info.split_k, co_path);
+        }
+    }
     if (err == hipSuccess) err = hipStreamCreate(&h->stream);
     if (err == hipSuccess) err = hipEventCreate(&h->ev_start);
     if (err == hipSuccess) err = hipEventCreate(&h->ev_stop);
@@ -322,6 +394,8 @@ void sgemm_close(sgemm_handle* h) {
     if (h->ev_start) (void)hipEventDestroy(h->ev_start);
     if (h->ev_stop) (void)hipEventDestroy(h->ev_stop);
     if (h->stream) (void)hipStreamDestroy(h->stream);
+    if (h->ws) (void)hipFree(h->ws);
+    if (h->tickets) (void)hipFree(h->tickets);
     if (h->module) (void)hipModuleUnload(h->module);
     delete h;
 }
@@ -353,6 +427,35 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
     const uint64_t b_span = (uint64_t)ldb * (uint32_t)(i.trans_b ? i.depth_k : i.tile_n);
     if (a_span >= (1ull << 32) || b_span >= (1ull << 32))
         return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets: lda=%u ldb=%u", lda, ldb);
+    return SGEMM_OK;
+}
+
+int sgemm_set_split_k(sgemm_handle* h, int splits) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_split_k: null handle");
+    if (splits < 0 || splits > SGEMM_MAX_SPLIT_K)
+        return fail(SGEMM_E_INVALID, "split count %d outside 0..%d", splits, SGEMM_MAX_SPLIT_K);
+    if (splits > h->info.split_k_max)
+        return fail(SGEMM_E_CONFIG, "split count %d needs generated_gemm_splitk, absent from this code object", splits);
+    h->info.split_k = splits;
+    return SGEMM_OK;
+}
+
+int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes) {
+    if (!h || !bytes) return fail(SGEMM_E_INVALID, "sgemm_workspace_size: null argument");
+    const sgemm_kernel_info& i = h->info;
+    const uint32_t s = effective_splits(i, h->compute_units, m, n, k);
+    *bytes = 0;
+    if (s > 1 && m && n) {
+        const size_t tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+                             ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+        *bytes = tiles * s * (size_t)i.tile_m * (size_t)i.tile_n * 4 + tiles * 4;
+    }
+    return SGEMM_OK;
+}
+
+int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits) {
+    if (!h || !splits) return fail(SGEMM_E_INVALID, "sgemm_launch_splits: null argument");
+    *splits = (int)effective_splits(h->info, h->compute_units, m, n, k);
     return SGEMM_OK;
 }
 
@@ -405,9 +508,45 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
     ka.alpha = alpha; ka.beta = beta;
     ka.num_wg_x = (int32_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m);
     ka.num_wg_y = (int32_t)((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
-    size_t size = sizeof(ka);
-    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-    HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
+    const uint32_t splits = effective_splits(i, h->compute_units, m, n, k);
+    if (splits == 1) {
+        size_t size = sizeof(ka);
+        void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+        HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
+                                      (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+        return SGEMM_OK;
+    }
+    // split-K: partials of every (tile, split) plus one ticket per tile; both
+    // buffers grow on demand and tickets start (and stay) zero
+    const size_t tiles = (size_t)ka.num_wg_x * (size_t)ka.num_wg_y;
+    const size_t ws_need = tiles * splits * (size_t)i.tile_m * (size_t)i.tile_n * 4;
+    if (h->ws_bytes < ws_need || h->ticket_count < tiles) {
+        HIP_TRY(hipStreamSynchronize(h->stream));
+        if (h->ws_bytes < ws_need) {
+            if (h->ws) HIP_TRY(hipFree(h->ws));
+            h->ws = nullptr;
+            h->ws_bytes = 0;
+            HIP_TRY(hipMalloc(&h->ws, ws_need));
+            h->ws_bytes = ws_need;
+        }
+        if (h->ticket_count < tiles) {
+            if (h->tickets) HIP_TRY(hipFree(h->tickets));
+            h->tickets = nullptr;
+            h->ticket_count = 0;
+            HIP_TRY(hipMalloc((void**)&h->tickets, tiles * 4));
+            HIP_TRY(hipMemset(h->tickets, 0, tiles * 4));
+            h->ticket_count = tiles;
+        }
+    }
+    KernArgsSplit ks;
+    memset(&ks, 0, sizeof(ks));
+    ks.base = ka;
+    ks.ws = (float*)h->ws;
+    ks.tickets = h->tickets;
+    ks.splits = splits;
+    size_t size = sizeof(ks);
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ks, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+    HIP_TRY(hipModuleLaunchKernel(h->function_splitk, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, splits,
                                   (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
     return SGEMM_OK;
 }

@@ -13,34 +13,44 @@ import os
 from concurrent.futures import ThreadPoolExecutor
 from typing import Dict, List, Optional, Tuple
 
-from .generator import (DataType, GemmOptimizations, GemmSolutionConfig, MFMA_16x16x4, MFMA_32x32x2,
-                        build_kernel)
+from .generator import (MAX_SPLIT_K, DataType, GemmOptimizations, GemmSolutionConfig, MFMA_16x16x4,
+                        MFMA_32x32x2, build_kernel)
 
 PACKAGE_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 KERNEL_DIR = os.path.join(PACKAGE_ROOT, "kernels")
 
 F = DataType.FP32
+# compute units of an MI355X (gfx950); the host library reads the real count
+GFX950_COMPUTE_UNITS = 256
 
 
 def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0, pd=1):
-    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd)
+def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0, pd=1, occ=0, sk=1):
+    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk)
 
 
 # name -> (config, optimizations)
 SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
-    # tuner winners on gfx950 (interleaved early refill, three LDS buffers)
+    # tuner winners on gfx950 (interleaved early refill, three LDS buffers);
+    # sk=0: the code object also holds the split-K kernel, used when a
+    # problem's tiles cannot fill the GPU (not for 256 x 256 tiles, whose
+    # 256 accumulators per lane leave no registers for the split epilogue)
     "mt256x256_a32_wg2x2_dk16_s3": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
-    "mt64x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    "mt64x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8, sk=0)),
     "mt128x64_a16_wg2x2_dk16_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=2), _opt(wgm=4, plr=1, xcd=8)),
-    "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8, sk=0)),
     # winners of the wide sweep (all wave groups, 32..256 tiles)
     "mt256x256_a32_wg4x2_dk16_s3": (_cfg(MFMA_32x32x2, (4, 2), (2, 4), 16, stages=2), _opt(wgm=8, plr=3, xcd=8)),
-    "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2), _opt(wgm=8, plr=3, xcd=8)),
-    "mt128x64_a16_wg2x2_dk16_s2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1), _opt(wgm=1, plr=3, xcd=0)),
+    "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2), _opt(wgm=8, plr=3, xcd=8, sk=0)),
+    "mt128x64_a16_wg2x2_dk16_s2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1), _opt(wgm=1, plr=3, xcd=0, sk=0)),
+    # two work-groups per CU (registers capped for 2 waves per SIMD)
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
+                                        _opt(wgm=4, plr=3, xcd=8, occ=2, sk=0)),
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16, stages=2),
+                                         _opt(wgm=4, plr=3, xcd=8, occ=2)),
     "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
     "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
@@ -68,6 +78,9 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4, plr=3)),
     "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8, plr=2)),
     "mt16x16_a16_wg1x1_dk16_s3_plr3": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, mapk=4)),
+    # split-K (default split count 4) on a one-wave tile, plain and transposed
+    "mt32x32_a32_wg1x1_dk16_s3_sk4": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, sk=4)),
+    "mt32x32_a32_wg1x1_dk16_sk4_tt": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, ta=True, tb=True), _opt(sk=4)),
     # transposed layouts (TN, NT, TT): op(A) = A^T and/or op(B) = B^T
     "mt256x256_a32_wg2x2_dk16_s3_tn": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2, ta=True),
                                        _opt(wgm=4, plr=3, xcd=8)),
@@ -120,10 +133,36 @@ def divides(name: str, m: int, n: int, k: int) -> bool:
     return m % t0 == 0 and n % t1 == 0 and k % cfg.depth_k == 0
 
 
+def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> int:
+    """K ranges the host library uses for an instance built with split_k = 0
+    (the rule of sgemm_set_split_k): none when the tiles fill the compute
+    units, else the s <= min(16, K tiles / 4) with the fewest rounds of
+    work-groups per unit of K work, ceil(tiles * s / CUs) / s (smallest s
+    among ties)."""
+    cfg, opt = SOLUTIONS[name]
+    t0, t1 = cfg.tile_size
+    tiles = -(-m // t0) * -(-n // t1)
+    ktiles = -(-k // cfg.depth_k)
+    if opt.split_k == 1:
+        return 1
+    if opt.split_k > 1:
+        s = opt.split_k
+    elif tiles >= compute_units or tiles == 0:
+        s = 1
+    else:
+        s, best = 1, 1.0
+        for c in range(2, min(MAX_SPLIT_K, ktiles // 4) + 1):
+            rounds = -(-tiles * c // compute_units)
+            if rounds * s < best * c:
+                s, best = c, rounds
+    return max(1, min(s, ktiles))
+
+
 def select(m: int, n: int, k: int) -> str:
     """Instance for an (m, n, k) problem: the tuner's choice for a BASELINE
-    shape, else the tuned instance whose tiles best fill the GPU -- every CU
-    busy first, then the least padding at the edges, then the largest tile."""
+    shape, else the tuned instance that best fills the GPU -- the most
+    work-groups (tiles times K splits) up to one per CU first, then no split,
+    then the least padding at the edges, then the largest tile."""
     if m <= 0 or n <= 0:
         raise RuntimeError(f"empty problem {m}x{n}x{k}")
     for shape, name in PREFERRED:
@@ -135,7 +174,9 @@ def select(m: int, n: int, k: int) -> str:
         t0, t1 = cfg.tile_size
         tx, ty = -(-m // t0), -(-n // t1)
         fill = (m * n) / (tx * t0 * ty * t1)
-        key = (tx * ty >= 256, round(fill, 1), t0 * t1, k % cfg.depth_k == 0)
+        splits = auto_split(name, m, n, k)
+        key = (min(tx * ty * splits, GFX950_COMPUTE_UNITS), splits == 1, round(fill, 1), t0 * t1,
+               k % cfg.depth_k == 0)
         if best is None or key > best[0]:
             best = (key, name)
     return best[1]

@@ -44,6 +44,8 @@ SUPPORTED_ARCHS = ("gfx950", "gfx950:xnack-")
 # LDS of one gfx950 compute unit (CDNA4: 160 KiB), the largest static LDS a
 # work-group may declare.
 MAX_LDS_NUM_BYTES = 163840
+# most K ranges one output tile may be split into (generated_gemm_splitk)
+MAX_SPLIT_K = 16
 # Work-items per work-group accepted by the hardware.
 MAX_WORKITEMS = 1024
 # LDS geometry used by the pad solver: gfx950 serves a 16-byte-per-lane LDS
@@ -101,6 +103,16 @@ class GemmOptimizations:
     * ``pd``        -- (gfx950 only) prefetch depth of the early-refill
                        schedules: a K tile's global loads are issued ``pd``
                        tiles before its LDS writes (1 or 2 register sets).
+    * ``occ``       -- (gfx950 only) 0 lets the compiler size registers for
+                       one wave per SIMD; n >= 2 caps them so that n waves
+                       per SIMD (n work-groups of one wave per SIMD) fit.
+    * ``split_k``   -- (gfx950 only) 1 builds the reference's single kernel
+                       only; any other value also builds
+                       ``generated_gemm_splitk``, which splits each output
+                       tile's K into ranges and reduces them in the kernel.
+                       The value is the launch's default split count: 0 lets
+                       the host pick one per problem (split only when the
+                       tiles cannot fill the GPU), 2..16 fixes it.
     """
 
     def __init__(
@@ -112,6 +124,8 @@ class GemmOptimizations:
         map_k_idx: Optional[int] = None,
         xcd: Optional[int] = None,
         pd: Optional[int] = None,
+        occ: Optional[int] = None,
+        split_k: Optional[int] = None,
     ):
         self.level = level
         self.wgm = 1
@@ -120,6 +134,8 @@ class GemmOptimizations:
         self.map_k_idx = 0
         self.xcd = 0
         self.pd = 1
+        self.occ = 0
+        self.split_k = 1
         self._setup_optimizations()
         if wgm is not None:
             self.wgm = wgm
@@ -133,6 +149,10 @@ class GemmOptimizations:
             self.xcd = xcd
         if pd is not None:
             self.pd = pd
+        if occ is not None:
+            self.occ = occ
+        if split_k is not None:
+            self.split_k = split_k
         if self.wgm < 1:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
@@ -141,6 +161,10 @@ class GemmOptimizations:
             raise RuntimeError(f"Invalid optimization knobs: plr={self.plr} gw={self.gw} xcd={self.xcd}")
         if self.pd not in (1, 2) or (self.pd == 2 and self.plr < 2):
             raise RuntimeError(f"Invalid prefetch depth {self.pd} (2 needs plr >= 2)")
+        if self.occ not in (0, 1, 2, 3, 4, 8):
+            raise RuntimeError(f"Invalid occupancy target {self.occ}")
+        if not 0 <= self.split_k <= MAX_SPLIT_K:
+            raise RuntimeError(f"Invalid split_k {self.split_k} (0 = auto, or 1..{MAX_SPLIT_K})")
 
     def _setup_optimizations(self):
         if self.level != 0:
@@ -156,11 +180,13 @@ class GemmOptimizations:
             "map_k_idx": int(self.map_k_idx),
             "xcd": int(self.xcd),
             "pd": int(self.pd),
+            "occ": int(self.occ),
+            "split_k": int(self.split_k),
         }
 
     def __repr__(self) -> str:
         return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
-                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd})")
+                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, split_k={self.split_k})")
 
 
 def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int,
@@ -508,6 +534,8 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_WGM": opt.wgm,
         "SG_XCD": opt.xcd,
         "SG_PD": opt.pd,
+        "SG_OCC": opt.occ,
+        "SG_SPLITK": int(opt.split_k != 1),
         "SG_MAPK": opt.map_k_idx,
         "SG_PLR": opt.plr,
         "SG_GW": opt.gw,
@@ -635,7 +663,10 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     d["arch"] = arch
     if opt is not None:
         d.update(opt.to_dict())
-    d.update(parse_resource_usage(ret.stderr.decode(errors="replace")))
+    remarks = ret.stderr.decode(errors="replace")
+    d.update(parse_resource_usage(remarks))
+    if opt is not None and opt.split_k != 1:
+        d.update({f"splitk_{k}": v for k, v in parse_resource_usage(remarks, "generated_gemm_splitk").items()})
     if extra_keys:
         d.update(extra_keys)
     write_toml(d, toml_path)
@@ -652,13 +683,20 @@ _RESOURCE_KEYS = {
 }
 
 
-def parse_resource_usage(remarks: str) -> Dict[str, int]:
-    """The compiler's kernel-resource-usage remark as integer TOML keys."""
+def parse_resource_usage(remarks: str, kernel: str = "generated_gemm") -> Dict[str, int]:
+    """The compiler's kernel-resource-usage remark for ``kernel`` as integer
+    TOML keys (a code object may hold several kernels)."""
     out: Dict[str, int] = {}
+    current = None
     for line in remarks.splitlines():
         if "remark:" not in line:
             continue
         body = line.split("remark:", 1)[1].strip()
+        if body.startswith("Function Name:"):
+            current = body[len("Function Name:"):].split("[")[0].strip()
+            continue
+        if current is not None and current != kernel:
+            continue
         for label, key in _RESOURCE_KEYS.items():
             if body.startswith(label + ":"):
                 val = body[len(label) + 1:].split("[")[0].strip()

@@ -42,6 +42,8 @@ class KernelInfo(ctypes.Structure):
         ("workitems", ctypes.c_int),
         ("trans_a", ctypes.c_int),
         ("trans_b", ctypes.c_int),
+        ("split_k", ctypes.c_int),
+        ("split_k_max", ctypes.c_int),
     ]
 
 
@@ -54,6 +56,9 @@ SIGNATURES = {
     "sgemm_close": (None, [_vp]),
     "sgemm_get_info": (_int, [_vp, ctypes.POINTER(KernelInfo)]),
     "sgemm_check_shape": (_int, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "sgemm_set_split_k": (_int, [_vp, _int]),
+    "sgemm_workspace_size": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
+    "sgemm_launch_splits": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
     "sgemm_malloc": (_int, [ctypes.POINTER(_vp), ctypes.c_size_t]),
     "sgemm_free": (_int, [_vp]),
     "sgemm_memcpy_h2d": (_int, [_vp, _vp, ctypes.c_size_t]),
@@ -199,6 +204,29 @@ class Kernel:
         da, db = self.default_lds(m, n, k)
         rc = lib.sgemm_check_shape(self.handle, m, n, k, lda or da, ldb or db, ldc or m, ldd or m)
         return None if rc == 0 else lib.sgemm_last_error().decode()
+
+    def _refresh_info(self):
+        _check("sgemm_get_info", load_library().sgemm_get_info(self.handle, ctypes.byref(self.info)))
+
+    @property
+    def split_k(self) -> int:
+        return self.info.split_k
+
+    def set_split_k(self, splits: int):
+        """K ranges per output tile for later launches (1 = the reference's kernel)."""
+        _check("sgemm_set_split_k", load_library().sgemm_set_split_k(self.handle, int(splits)))
+        self._refresh_info()
+
+    def workspace_size(self, m, n, k) -> int:
+        out = ctypes.c_size_t()
+        _check("sgemm_workspace_size", load_library().sgemm_workspace_size(self.handle, m, n, k, ctypes.byref(out)))
+        return int(out.value)
+
+    def launch_splits(self, m, n, k) -> int:
+        """K ranges a launch of this shape uses with the current setting (1 = no split)."""
+        out = _int()
+        _check("sgemm_launch_splits", load_library().sgemm_launch_splits(self.handle, m, n, k, ctypes.byref(out)))
+        return int(out.value)
 
     def _args(self, a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta):
         cp = c.ptr if c is not None else None

@@ -39,7 +39,7 @@ import sys
 import time
 from concurrent.futures import ThreadPoolExecutor
 from itertools import product
-from typing import Dict, Iterable, List, Optional, Tuple
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if _PKG not in sys.path:
@@ -90,13 +90,16 @@ Point = Tuple[GemmSolutionConfig, GemmOptimizations]
 def point_key(cfg: GemmSolutionConfig, opt: GemmOptimizations) -> str:
     return (f"a{cfg.mfma[0]}_wg{cfg.wave_group[0]}x{cfg.wave_group[1]}_wt{cfg.wave_tiling[0]}x{cfg.wave_tiling[1]}"
             f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}"
-            + (f"_pd{opt.pd}" if opt.pd != 1 else ""))
+            + (f"_pd{opt.pd}" if opt.pd != 1 else "") + (f"_occ{opt.occ}" if opt.occ else "")
+            + (f"_sk{opt.split_k}" if opt.split_k > 1 else ""))
 
 
-def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1) -> Optional[Point]:
+def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1, occ=0,
+               split_k=1) -> Optional[Point]:
     try:
         cfg = GemmSolutionConfig(F, F, F, F, mfma, wg, wt, depth_k, False, False, vmem_stage=vmem_stage)
-        opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd, pd=pd)
+        opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd, pd=pd, occ=occ,
+                                split_k=split_k)
     except RuntimeError as e:
         if VERBOSE:
             print(e)
@@ -128,12 +131,14 @@ def geometry_points(knobs: Dict, wide: bool = False) -> Iterable[Point]:
             yield p
 
 
-def knob_points(cfg: GemmSolutionConfig) -> Iterable[Point]:
-    for dk, st, wgm, xcd, plr, pd in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM, GFX950_XCD,
-                                             GFX950_PLR, GFX950_PD):
+def knob_points(cfg: GemmSolutionConfig, split_ks: Sequence[int] = (1,), occs: Sequence[int] = (0,)) -> Iterable[Point]:
+    """Stage-2 candidates of one geometry; ``split_ks`` and ``occs`` add the
+    gfx950-only split-K (0 = chosen per problem) and occupancy knobs."""
+    for dk, st, wgm, xcd, plr, pd, sk, occ in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM, GFX950_XCD,
+                                                      GFX950_PLR, GFX950_PD, split_ks, occs):
         if pd == 2 and plr < 2:
             continue
-        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, 0, 0, xcd, pd)
+        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, 0, 0, xcd, pd, occ, sk)
         if p:
             yield p
 
@@ -297,8 +302,14 @@ def main(argv=None):
     ap.add_argument("--points-dir", default=None, help="compiled candidates (default <out>/points)")
     ap.add_argument("--all-shapes", action="store_true",
                     help="with --compile-only: build the stage-2 candidates of every geometry")
+    ap.add_argument("--split-k", default="1",
+                    help="comma-separated split-K values for stage 2 (0 = chosen per problem; default 1: no split)")
+    ap.add_argument("--occ", default="0",
+                    help="comma-separated occupancy targets for stage 2 (0 = compiler's choice; 2 = two waves per SIMD)")
     args = ap.parse_args(argv)
     m, n, k, out = args.m, args.n, args.k, args.output_folder
+    split_ks = [int(x) for x in args.split_k.split(",") if x.strip()]
+    occs = [int(x) for x in args.occ.split(",") if x.strip()]
     os.makedirs(out, exist_ok=True)
     global POINTS_DIR
     POINTS_DIR = args.points_dir
@@ -314,7 +325,7 @@ def main(argv=None):
         pts = list(stage1)
         if args.all_shapes and args.space != "reference":
             for cfg, _ in stage1:
-                pts += [p for p in knob_points(cfg) if fits(p[0], m, n, k)]
+                pts += [p for p in knob_points(cfg, split_ks, occs) if fits(p[0], m, n, k)]
         res = build_points(out, pts, args.jobs)
         bad = sum(1 for v in res.values() if v)
         print(f"compiled {len(res) - bad} of {len(res)} candidates into {point_dir(out)}")
@@ -338,7 +349,7 @@ def main(argv=None):
         seen = set(by_key)
         for r in ranked:
             cfg = by_key[r["point"]][0]
-            for p in knob_points(cfg):
+            for p in knob_points(cfg, split_ks, occs):
                 kk = point_key(*p)
                 if kk not in seen and fits(p[0], m, n, k):
                     seen.add(kk)
@@ -354,7 +365,8 @@ def main(argv=None):
     print(f"Best: {best['gflops']:.1f} Gflops ({best['gflops'] / 1e3 / 157.3 * 100:.1f}% of the FP32 MFMA peak), "
           f"MT: {tuple(best['tile'])}, DK: {best['depth_k']}, MI: {tuple(best['mfma'])}, wg: {tuple(best['wave_group'])}, "
           f"wgm: {best['wgm']}, plr: {best['plr']}, gw: {best['gw']}, map_k_idx: {best['map_k_idx']}, "
-          f"vmem_stage: {best['vmem_stage']}, xcd: {best['xcd']} -> {out}/generated_gemm.co")
+          f"vmem_stage: {best['vmem_stage']}, xcd: {best['xcd']}, split_k: {best.get('split_k', 1)}, "
+          f"occ: {best.get('occ', 0)} -> {out}/generated_gemm.co")
     return 0
 
 

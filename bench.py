@@ -44,7 +44,11 @@ WORKLOADS = {
     "cfg2": (1024, 1024, 1024, 1, S.SGEMM_DIST_UNIFORM),
     "cfg4": (8192, 8192, 256, 3, S.SGEMM_DIST_NORMAL),
     "cfg5": (16384, 128, 4096, 4, S.SGEMM_DIST_UNIFORM),
+    # not a BASELINE.json config: few output tiles and a deep K, the case the
+    # split-K kernel exists for (32 tiles of 128 x 64 on 256 compute units)
+    "deepk": (512, 512, 16384, 5, S.SGEMM_DIST_UNIFORM),
 }
+HEADLINE_METRIC = "FP32 SGEMM TFLOP/s at 4096^3 NN; % of MI355X FP32 MFMA peak"
 
 
 def log(msg: str):
@@ -110,6 +114,8 @@ def main():
     ap.add_argument("--kernel", default=None, help="catalog instance (default: catalog.select)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--split-k", type=int, default=None,
+                    help="K ranges per output tile (0 = per problem; default: the instance's own setting)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -127,6 +133,10 @@ def main():
     A = S.fill_matrix(m, k, seed, 0, dist)
     B = S.fill_matrix(k, n, seed, 1, dist)
     kern = S.Kernel(co, toml)
+    if args.split_k is not None:
+        kern.set_split_k(args.split_k)
+    splits = kern.launch_splits(m, n, k)
+    log(f"K ranges per output tile: {splits}")
     dA, dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
     dD = S.DeviceBuffer(m * n * 4)
     dD.zero()
@@ -152,10 +162,12 @@ def main():
         f"{achieved:.2f} TFLOP/s; per-launch median {median_ms:.4f} ms")
 
     D = dD.download().reshape(n, m).T
+    # A, B read once and D written once; a split launch also writes and
+    # reads its partials (4 bytes per output per K range), not counted here
     alg_bytes = 4.0 * (m * k + k * n + m * n)
     traffic = read_traffic(name, args.workload)
     line = {
-        "metric": "FP32 SGEMM TFLOP/s at 4096^3 NN; % of MI355X FP32 MFMA peak",
+        "metric": HEADLINE_METRIC if args.workload == "cfg3" else f"FP32 SGEMM TFLOP/s at {m}x{n}x{k} NN",
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -173,6 +185,7 @@ def main():
             "dist": "uniform[-1,1)" if dist == S.SGEMM_DIST_UNIFORM else "normal(0,1)",
             "alpha": 1.0, "beta": 0.0,
             "kernel": name,
+            "split_k": splits,
             "pct_of_fp32_mfma_peak": round(100.0 * value / FP32_MFMA_PEAK_TFLOPS, 2),
             "device": info["name"],
             "peak_sclk_mhz": info["clock_khz"] / 1000.0,

@@ -35,7 +35,10 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 2
+#define SGEMM_SHIM_ABI_VERSION 3
+
+/* Most K ranges generated_gemm_splitk splits one output tile into. */
+#define SGEMM_MAX_SPLIT_K 16
 
 enum {
     SGEMM_OK = 0,
@@ -68,6 +71,9 @@ typedef struct sgemm_kernel_info {
     int workitems;        /* wave_group[0] * wave_group[1] * wavefront_size */
     int trans_a;          /* 1: A is stored k x m (lda >= k), op(A) = A^T */
     int trans_b;          /* 1: B is stored n x k (ldb >= n), op(B) = B^T */
+    int split_k;          /* K ranges per output tile for sgemm_launch: 0 = chosen per problem
+                             (sgemm_set_split_k), else a fixed count (toml key split_k, default 1) */
+    int split_k_max;      /* SGEMM_MAX_SPLIT_K if the code object has generated_gemm_splitk, else 1 */
 } sgemm_kernel_info;
 
 /* Message of the last failure on this thread ("" if none). */
@@ -81,7 +87,8 @@ int sgemm_abi_version(void);
  * Replaces nothing in the reference (it never queries the device). */
 int sgemm_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz, int* lds_per_block);
 
-/* Loads <co_path> (symbol "generated_gemm") and its <toml_path> config.
+/* Loads <co_path> (symbol "generated_gemm", and "generated_gemm_splitk" when
+ * present) and its <toml_path> config.
  * Replaces getAsmKernelConfig + prepareASMKernel (generator_runner.cpp:100-124, :69-73). */
 int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out);
 
@@ -100,6 +107,31 @@ int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info);
 int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd);
 
+/* Sets the number of K ranges (1..split_k_max) each output tile is split into
+ * by later launches; 1 launches generated_gemm.  0 chooses per problem: with
+ * T = ceil(m/MT0) * ceil(n/MT1) tiles and C compute units, no split when
+ * T >= C; else the s in 1..min(split_k_max, ceil(k/depth_k) / 4) with the
+ * fewest rounds of work-groups per unit of K work, ceil(T * s / C) / s (the
+ * smallest s among ties), so a problem with few tiles and a deep K still
+ * fills the GPU.
+ * With s > 1 ranges, sgemm_launch runs generated_gemm_splitk over a grid of
+ * (ceil(m/MT0), ceil(n/MT1), s') blocks, s' = min(s, ceil(k/depth_k)): every
+ * block multiplies one range of whole K tiles and the last block of a tile
+ * to finish sums the partials in range order, so results do not depend on
+ * timing.  The handle allocates the
+ * partials (sgemm_workspace_size bytes) on the first launch that needs more
+ * than it holds.  No counterpart in the reference, whose kernel has no K split
+ * (its knob set is generator.py:827-854). */
+int sgemm_set_split_k(sgemm_handle* h, int splits);
+
+/* Device bytes the handle's workspace needs for an m x n x k launch with its
+ * current split count (0 when the launch does not split). */
+int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes);
+
+/* K ranges an m x n x k launch with the handle's current setting uses
+ * (1: generated_gemm, no split). */
+int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits);
+
 /* Device memory (generator_runner.cpp:236-242, :291, :319-322). */
 int sgemm_malloc(void** dptr, size_t bytes);
 int sgemm_free(void* dptr);
@@ -110,7 +142,10 @@ int sgemm_memset(void* dptr, int value, size_t bytes);
 /* Enqueues one launch on the handle's stream; does not wait.
  * Replaces makeKernelArguments + launchASMKernel (generator_runner.cpp:126-190):
  * the same 80-byte kernarg buffer, passed through hipModuleLaunchKernel's
- * HIP_LAUNCH_PARAM_BUFFER_POINTER with a grid of (ceil(m/MT0), ceil(n/MT1)) blocks. */
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER with a grid of (ceil(m/MT0), ceil(n/MT1)) blocks.
+ * With a split count above 1 (sgemm_set_split_k) it launches the split kernel
+ * instead, with the handle's workspace; launches of one handle share that
+ * workspace, so they must run in order on the handle's stream. */
 int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
                  uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                  float alpha, float beta);

@@ -221,6 +221,9 @@ def parse_assembly(asm: str, kernel: str = "generated_gemm") -> "Program":
                 mods[mt] = 1
         ops = [parse_operand(x) for x in toks]
         insts.append(Instruction(mn, ops, mods, t, i + 1))
+    # the descriptor block of this kernel only (a code object may hold several)
+    m = re.search(r"\.amdhsa_kernel\s+" + re.escape(kernel) + r"\b(.*?)\.end_amdhsa_kernel", asm, re.S)
+    block = m.group(1) if m else asm
     desc = {}
     for key in ("amdhsa_group_segment_fixed_size", "amdhsa_user_sgpr_count", "amdhsa_user_sgpr_kernarg_segment_ptr",
                 "amdhsa_system_sgpr_workgroup_id_x", "amdhsa_system_sgpr_workgroup_id_y",
@@ -228,7 +231,7 @@ def parse_assembly(asm: str, kernel: str = "generated_gemm") -> "Program":
                 "amdhsa_user_sgpr_dispatch_id", "amdhsa_user_sgpr_private_segment_size",
                 "amdhsa_system_vgpr_workitem_id", "amdhsa_next_free_sgpr", "amdhsa_next_free_vgpr",
                 "amdhsa_accum_offset"):
-        m = re.search(r"\." + key + r"\s+(\d+)", asm)
+        m = re.search(r"\." + key + r"\s+(\d+)", block)
         if m:
             desc[key] = int(m.group(1))
     return Program(insts, labels, desc)
@@ -382,6 +385,15 @@ class GcnVirtualMachine:
         self.v[op.index][mask] = (val & np.uint64(MASK32)).astype(np.uint32)[mask]
         self.v[op.index + 1][mask] = (val >> np.uint64(32)).astype(np.uint32)[mask]
 
+    def regfile(self, op: Operand) -> np.ndarray:
+        """The vector register file a memory instruction's data operand names:
+        VGPRs, or AGPRs (gfx90a and later load and store them directly)."""
+        if op.kind == "v":
+            return self.v
+        if op.kind == "a":
+            return self.a
+        raise NotImplementedError(f"vector memory data operand {op}")
+
     def reg_block(self, op: Operand) -> np.ndarray:
         """(count, 64) view of a v/a register range."""
         f = self.v if op.kind == "v" else self.a if op.kind == "a" else None
@@ -476,17 +488,21 @@ def _acc_index(m: int) -> Tuple[np.ndarray, np.ndarray]:
 _ACC_INDEX = {32: _acc_index(32), 16: _acc_index(16)}
 
 
-def as_program(context) -> Program:
+def as_program(context, kernel: Optional[str] = None) -> Program:
+    """The parsed kernel of a Program, an assembly text or a generator context
+    (``kernel`` defaults to the context's kernel name, else generated_gemm)."""
     if isinstance(context, Program):
         return context
     if isinstance(context, str):
-        return parse_assembly(context)
+        return parse_assembly(context, kernel or "generated_gemm")
     if hasattr(context, "assembly"):
-        prog = getattr(context, "_vm_program", None)
-        if prog is None:
-            prog = parse_assembly(context.assembly(), getattr(context, "name", None) or "generated_gemm")
-            context._vm_program = prog
-        return prog
+        name = kernel or getattr(context, "name", None) or "generated_gemm"
+        cache = getattr(context, "_vm_programs", None)
+        if cache is None:
+            cache = context._vm_programs = {}
+        if name not in cache:
+            cache[name] = parse_assembly(context.assembly(), name)
+        return cache[name]
     raise TypeError(f"cannot run {type(context)}")
 
 
@@ -890,6 +906,34 @@ def _v_cndmask(vm, ins, prog):
     vm.wv32(ins.ops[0], np.where(sel, src1, src0).astype(np.uint32))
 
 
+@op("v_mbcnt_lo_u32_b32", "v_mbcnt_lo_u32_b32_e64")
+def _v_mbcnt_lo(vm, ins, prog):
+    """Per lane: popcount of mask bits 0..min(lane, 32)-1 plus src1."""
+    mask = vm.rv32(ins.ops[1]).astype(np.uint64)
+    lane = np.arange(WAVE, dtype=np.uint64)
+    below = np.where(lane >= 32, np.uint64(0xFFFFFFFF), (np.uint64(1) << lane) - np.uint64(1))
+    cnt = np.array([bin(int(x)).count("1") for x in (mask & below)], dtype=np.uint64)
+    vm.wv32(ins.ops[0], ((cnt + vm.rv32(ins.ops[2]).astype(np.uint64)) & np.uint64(MASK32)).astype(np.uint32))
+
+
+@op("v_mbcnt_hi_u32_b32", "v_mbcnt_hi_u32_b32_e64")
+def _v_mbcnt_hi(vm, ins, prog):
+    """Per lane: popcount of mask bits 0..lane-33 (lanes 32..63) plus src1."""
+    mask = vm.rv32(ins.ops[1]).astype(np.uint64)
+    lane = np.arange(WAVE, dtype=np.uint64)
+    below = np.where(lane < 32, np.uint64(0), (np.uint64(1) << np.maximum(lane, np.uint64(32)) - np.uint64(32))
+                     - np.uint64(1))
+    cnt = np.array([bin(int(x)).count("1") for x in (mask & below)], dtype=np.uint64)
+    vm.wv32(ins.ops[0], ((cnt + vm.rv32(ins.ops[2]).astype(np.uint64)) & np.uint64(MASK32)).astype(np.uint32))
+
+
+@op("s_bcnt1_i32_b64")
+def _s_bcnt1_i32_b64(vm, ins, prog):
+    r = bin(vm.rs64(ins.ops[1])).count("1")
+    vm.ws32(ins.ops[0], r)
+    vm.scc = int(r != 0)
+
+
 @op("v_readfirstlane_b32")
 def _v_readfirstlane(vm, ins, prog):
     src = vm.rv32(ins.ops[1])
@@ -1049,7 +1093,7 @@ def _global_load(nd):
 
         def land():
             for i in range(nd):
-                vm.v[dst.index + i][mask] = data[i][mask]
+                vm.regfile(dst)[dst.index + i][mask] = data[i][mask]
         vm.pending["vmcnt"].append(land)
     return _impl
 
@@ -1062,7 +1106,7 @@ def _global_store(nd):
         if not mask.any():
             return
         addr = _global_addr(vm, ins, vaddr, saddr)
-        data = np.stack([vm.v[src.index + i] for i in range(nd)])
+        data = np.stack([vm.regfile(src)[src.index + i] for i in range(nd)])
         vm.vmem.write_u32(addr[mask], data[:, mask], str(ins))
     return _impl
 
@@ -1070,6 +1114,91 @@ def _global_store(nd):
 for _nd, _sfx in ((1, "dword"), (2, "dwordx2"), (3, "dwordx3"), (4, "dwordx4")):
     _DISPATCH[f"global_load_{_sfx}"] = _global_load(_nd)
     _DISPATCH[f"global_store_{_sfx}"] = _global_store(_nd)
+
+
+@op("global_atomic_add")
+def _global_atomic_add(vm, ins, prog):
+    """32-bit atomic add, lanes in ascending order.  With sc0 (glc) the first
+    operand is the destination of the pre-add values, which land at vmcnt."""
+    ret = bool(ins.mods.get("sc0", 0) or ins.mods.get("glc", 0))
+    ops = ins.ops[1:] if ret else ins.ops
+    vaddr, src = ops[0], ops[1]
+    saddr = ops[2] if len(ops) > 2 else None
+    mask = vm.exec_mask()
+    addr = _global_addr(vm, ins, vaddr, saddr)
+    data = vm.rv32(src)
+    old = np.zeros(WAVE, dtype=np.uint32)
+    for lane in np.nonzero(mask)[0]:
+        a = addr[lane:lane + 1]
+        cur = vm.vmem.read_u32(a, 1, str(ins))[0, 0]
+        old[lane] = cur
+        vm.vmem.write_u32(a, np.array([[(int(cur) + int(data[lane])) & MASK32]], dtype=np.uint32), str(ins))
+    if ret:
+        dst = ins.ops[0]
+
+        def land():
+            vm.regfile(dst)[dst.index][mask] = old[mask]
+        vm.pending["vmcnt"].append(land)
+    else:
+        vm.pending["vmcnt"].append(lambda: None)
+
+
+def _buffer_addr(vm, ins, vaddr_op, srd_op, soff_op):
+    """Byte addresses and in-range mask of a raw (stride 0) MUBUF access:
+    base + (offen ? vaddr : 0) + soffset + offset, checked per access against
+    num_records (word 2 of the resource); out-of-range loads read 0 and
+    out-of-range stores are dropped, as on the hardware."""
+    if ins.mods.get("idxen", 0):
+        raise NotImplementedError(f"indexed buffer access {ins}")
+    w = [int(vm.s[srd_op.index + i]) for i in range(4)]
+    base = w[0] | ((w[1] & 0xFFFF) << 32)
+    if (w[1] >> 16) & 0x3FFF:
+        raise NotImplementedError(f"strided buffer resource in {ins}")
+    num_records = w[2]
+    off = vm.rv32(vaddr_op).astype(np.int64) if ins.mods.get("offen", 0) else np.zeros(WAVE, dtype=np.int64)
+    off = off + np.int64(vm.rs32(soff_op)) + np.int64(ins.mods.get("offset", 0))
+    return np.int64(base) + off, off, num_records
+
+
+def _buffer_load(nd):
+    def _impl(vm, ins, prog):
+        dst, vaddr, srd, soff = ins.ops[:4]
+        addr, off, num = _buffer_addr(vm, ins, vaddr, srd, soff)
+        mask = vm.exec_mask() & (off + 4 * nd <= num)
+        data = np.zeros((nd, WAVE), dtype=np.uint32)
+        if mask.any():
+            data[:, mask] = vm.vmem.read_u32(addr[mask], nd, str(ins))
+        emask = vm.exec_mask()
+
+        def land():
+            for i in range(nd):
+                vm.regfile(dst)[dst.index + i][emask] = data[i][emask]
+        vm.pending["vmcnt"].append(land)
+    return _impl
+
+
+def _buffer_store(nd):
+    def _impl(vm, ins, prog):
+        src, vaddr, srd, soff = ins.ops[:4]
+        addr, off, num = _buffer_addr(vm, ins, vaddr, srd, soff)
+        mask = vm.exec_mask() & (off + 4 * nd <= num)
+        if mask.any():
+            data = np.stack([vm.regfile(src)[src.index + i] for i in range(nd)])
+            vm.vmem.write_u32(addr[mask], data[:, mask], str(ins))
+        vm.pending["vmcnt"].append(lambda: None)
+    return _impl
+
+
+for _nd, _sfx in ((1, "dword"), (2, "dwordx2"), (3, "dwordx3"), (4, "dwordx4")):
+    _DISPATCH[f"buffer_load_{_sfx}"] = _buffer_load(_nd)
+    _DISPATCH[f"buffer_store_{_sfx}"] = _buffer_store(_nd)
+
+
+@op("buffer_wbl2", "buffer_inv")
+def _cache_maintenance(vm, ins, prog):
+    """L2 write-back / invalidate of the device-scope fences: the VM has one
+    coherent memory, so they only count as outstanding vector-memory work."""
+    vm.pending["vmcnt"].append(lambda: None)
 
 
 # LDS -------------------------------------------------------------------------
@@ -1084,7 +1213,7 @@ def _ds_read(nd):
 
         def land():
             for i in range(nd):
-                vm.v[dst.index + i][mask] = data[i][mask]
+                vm.regfile(dst)[dst.index + i][mask] = data[i][mask]
         vm.pending["lgkmcnt"].append(land)
     return _impl
 
@@ -1106,7 +1235,7 @@ def _ds_read2(dwords_each, scale):
 
         def land():
             for i in range(2 * dwords_each):
-                vm.v[dst.index + i][mask] = data[i][mask]
+                vm.regfile(dst)[dst.index + i][mask] = data[i][mask]
         vm.pending["lgkmcnt"].append(land)
     return _impl
 
@@ -1118,7 +1247,7 @@ def _ds_write(nd):
         if not mask.any():
             return
         addr = vm.rv32(addr_op).astype(np.int64) + ins.mods.get("offset", 0)
-        data = np.stack([vm.v[src.index + i] for i in range(nd)])
+        data = np.stack([vm.regfile(src)[src.index + i] for i in range(nd)])
         vm.lds.write_u32(addr[mask], data[:, mask], str(ins))
         vm.pending["lgkmcnt"].append(lambda: None)
     return _impl
@@ -1134,7 +1263,7 @@ def _ds_write2(dwords_each, scale):
         unit = 4 * dwords_each * scale
         for key, src in (("offset0", s0), ("offset1", s1)):
             a = base + ins.mods.get(key, 0) * unit
-            data = np.stack([vm.v[src.index + i] for i in range(dwords_each)])
+            data = np.stack([vm.regfile(src)[src.index + i] for i in range(dwords_each)])
             vm.lds.write_u32(a[mask], data[:, mask], str(ins))
         vm.pending["lgkmcnt"].append(lambda: None)
     return _impl
@@ -1154,62 +1283,74 @@ _DISPATCH["ds_write2st64_b64"] = _ds_write2(2, 64)
 
 
 # ------------------------------------------------------------ dispatching
-def run_kernel(program, grid: Tuple[int, int], workgroup_size: int, kernargs: bytes, vmem: Memory,
-               max_instructions: int = 50_000_000, on_workgroup: Optional[Callable] = None) -> int:
-    """Runs every work-group of a grid (x fastest), each with its waves
-    interleaved at barriers; returns the number of instructions executed."""
+def run_kernel(program, grid: Tuple[int, ...], workgroup_size: int, kernargs: bytes, vmem: Memory,
+               max_instructions: int = 50_000_000, on_workgroup: Optional[Callable] = None,
+               order: Optional[Sequence[Tuple[int, int, int]]] = None) -> int:
+    """Runs every work-group of a grid (x fastest, then y, then z), each with
+    its waves interleaved at barriers; returns the number of instructions
+    executed.  ``order`` lists the (x, y, z) work-groups in the order to run
+    them instead (each exactly once)."""
     prog = as_program(program)
     desc = prog.desc
     if not desc.get("amdhsa_user_sgpr_kernarg_segment_ptr", 0):
         raise NotImplementedError("kernel without a kernarg segment pointer")
     for key in ("amdhsa_user_sgpr_dispatch_ptr", "amdhsa_user_sgpr_queue_ptr", "amdhsa_user_sgpr_dispatch_id",
-                "amdhsa_system_sgpr_workgroup_id_z", "amdhsa_system_vgpr_workitem_id"):
+                "amdhsa_system_vgpr_workitem_id"):
         if desc.get(key, 0):
             raise NotImplementedError(f"kernel descriptor field {key} = {desc[key]}")
+    gx, gy = grid[0], grid[1]
+    gz = grid[2] if len(grid) > 2 else 1
+    every = [(x, y, z) for z in range(gz) for y in range(gy) for x in range(gx)]
+    if order is None:
+        order = every
+    elif sorted(order) != sorted(every):
+        raise ValueError("order must list every work-group of the grid exactly once")
     user = desc.get("amdhsa_user_sgpr_count", 2)
     lds_size = desc.get("amdhsa_group_segment_fixed_size", 0)
     nwaves = (workgroup_size + WAVE - 1) // WAVE
     total = 0
-    for wy in range(grid[1]):
-        for wx in range(grid[0]):
-            lds = Memory(max(lds_size, 4), "lds")
-            smem = Memory(max(len(kernargs), 8), "smem")
-            smem.write_bytes(0, kernargs)
-            waves = []
-            for w in range(nwaves):
-                vm = GcnVirtualMachine(nsgpr=max(desc.get("amdhsa_next_free_sgpr", 104) + 8, 104), nvgpr=512,
-                                       vmem_bytes=8)
-                vm.vmem, vm.smem, vm.lds = vmem, smem, lds
-                vm.s[0] = 0
-                vm.s[1] = 0
-                sid = user
-                if desc.get("amdhsa_system_sgpr_workgroup_id_x", 1):
-                    vm.s[sid] = wx
-                    sid += 1
-                if desc.get("amdhsa_system_sgpr_workgroup_id_y", 0):
-                    vm.s[sid] = wy
-                    sid += 1
-                tid = np.arange(WAVE, dtype=np.uint32) + w * WAVE
-                vm.v[0] = tid
-                active = tid < workgroup_size
-                vm.exec = GcnVirtualMachine._bits(active)
-                vm.reset_wave()
-                waves.append(vm)
-            budget = max_instructions
-            while not all(vm.done for vm in waves):
-                for vm in waves:
-                    if vm.done:
-                        continue
-                    try:
-                        vm.step(prog, budget)
-                    except BarrierReached:
-                        pass
-                live = [vm for vm in waves if not vm.done]
-                if live and len(live) != len(waves):
-                    raise RuntimeError("a wave ended while others wait at a barrier")
-            total += sum(vm.executed for vm in waves)
-            if on_workgroup:
-                on_workgroup(wx, wy, waves)
+    for (wx, wy, wz) in order:
+        lds = Memory(max(lds_size, 4), "lds")
+        smem = Memory(max(len(kernargs), 8), "smem")
+        smem.write_bytes(0, kernargs)
+        waves = []
+        for w in range(nwaves):
+            vm = GcnVirtualMachine(nsgpr=max(desc.get("amdhsa_next_free_sgpr", 104) + 8, 104), nvgpr=512,
+                                   vmem_bytes=8)
+            vm.vmem, vm.smem, vm.lds = vmem, smem, lds
+            vm.s[0] = 0
+            vm.s[1] = 0
+            sid = user
+            if desc.get("amdhsa_system_sgpr_workgroup_id_x", 1):
+                vm.s[sid] = wx
+                sid += 1
+            if desc.get("amdhsa_system_sgpr_workgroup_id_y", 0):
+                vm.s[sid] = wy
+                sid += 1
+            if desc.get("amdhsa_system_sgpr_workgroup_id_z", 0):
+                vm.s[sid] = wz
+                sid += 1
+            tid = np.arange(WAVE, dtype=np.uint32) + w * WAVE
+            vm.v[0] = tid
+            active = tid < workgroup_size
+            vm.exec = GcnVirtualMachine._bits(active)
+            vm.reset_wave()
+            waves.append(vm)
+        budget = max_instructions
+        while not all(vm.done for vm in waves):
+            for vm in waves:
+                if vm.done:
+                    continue
+                try:
+                    vm.step(prog, budget)
+                except BarrierReached:
+                    pass
+            live = [vm for vm in waves if not vm.done]
+            if live and len(live) != len(waves):
+                raise RuntimeError("a wave ended while others wait at a barrier")
+        total += sum(vm.executed for vm in waves)
+        if on_workgroup:
+            on_workgroup(wx, wy, waves)
     return total
 
 
@@ -1220,16 +1361,29 @@ def pack_kernargs(a: int, b: int, c: int, d: int, m: int, n: int, k: int, lda: i
     return raw + b"\0" * (80 - len(raw))
 
 
+def pack_splitk_kernargs(base: bytes, ws: int, tickets: int, splits: int) -> bytes:
+    """The split-K kernel's image: the 15 arguments (80 bytes), then ws at 80,
+    tickets at 88 and splits at 96, padded to 104 bytes."""
+    raw = base[:80] + struct.pack("<QQI", ws, tickets, splits)
+    return raw + b"\0" * (104 - len(raw))
+
+
 def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: np.ndarray,
               C: Optional[np.ndarray] = None, alpha: float = 1.0, beta: float = 0.0,
-              mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None) -> Tuple[np.ndarray, Dict]:
+              mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None,
+              splits: int = 0, order: Optional[Sequence[Tuple[int, int, int]]] = None) -> Tuple[np.ndarray, Dict]:
     """Runs a compiled SGEMM kernel on column-major A, B, C.
 
     Without ``mnk`` the problem is A (m x k) @ B (k x n) with tight leading
     dimensions.  With ``mnk = (m, n, k)`` the arrays are the full column-major
     storage: A is lda x (>= k), B is ldb x (>= n), C is ldc x (>= n), so
     lda = A.shape[0] etc.; D gets ``ldd`` rows (default m).  Returns D as the
-    full ldd x n storage when ``mnk`` is given, else m x n."""
+    full ldd x n storage when ``mnk`` is given, else m x n.
+
+    ``splits >= 1`` runs ``generated_gemm_splitk`` instead, over a grid of
+    ``splits`` K ranges, with its workspace and zeroed tickets; ``order`` is the
+    work-group order (see run_kernel).  The returned info holds the tickets
+    after the launch."""
     A = np.asfortranarray(A, dtype=np.float32)
     B = np.asfortranarray(B, dtype=np.float32)
     if mnk is None:
@@ -1242,8 +1396,12 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     Cm = np.zeros((m, n), dtype=np.float32, order="F") if C is None else np.asfortranarray(C, dtype=np.float32)
     ldc = Cm.shape[0]
     ldd = ldd or m
+    nwgx, nwgy = (m + tile[0] - 1) // tile[0], (n + tile[1] - 1) // tile[1]
     blobs = [A.ravel(order="F"), B.ravel(order="F"), Cm.ravel(order="F"),
              np.zeros(ldd * n, dtype=np.float32)]
+    if splits:
+        blobs.append(np.full(nwgx * nwgy * splits * tile[0] * tile[1], np.nan, dtype=np.float32))
+        blobs.append(np.zeros(nwgx * nwgy, dtype=np.uint32))
     # every buffer gets exactly its own bytes as an allocated region, with
     # unallocated gaps between them: any access past a buffer raises
     offs, pos = [], 4096
@@ -1251,13 +1409,23 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
         offs.append(pos)
         pos += (bl.nbytes + 4095) // 4096 * 4096 + 4096
     mem = Memory(pos, "vmem")
-    for o, bl, label in zip(offs, blobs, "ABCD"):
+    for o, bl, label in zip(offs, blobs, ["A", "B", "C", "D", "ws", "tickets"]):
         mem.write_bytes(o, bl.tobytes())
         mem.allocate_region(o, bl.nbytes, label)
-    nwgx, nwgy = (m + tile[0] - 1) // tile[0], (n + tile[1] - 1) // tile[1]
     ka = pack_kernargs(offs[0], offs[1], offs[2], offs[3], m, n, k, lda, ldb, ldc, ldd, alpha, beta, nwgx, nwgy)
-    count = run_kernel(program, (nwgx, nwgy), workitems, ka, mem)
+    info: Dict = {}
+    if splits:
+        ka = pack_splitk_kernargs(ka, offs[4], offs[5], splits)
+        grid: Tuple[int, ...] = (nwgx, nwgy, splits)
+        prog = as_program(program, "generated_gemm_splitk")
+    else:
+        grid = (nwgx, nwgy)
+        prog = as_program(program)
+    count = run_kernel(prog, grid, workitems, ka, mem, order=order)
     D = np.frombuffer(mem.read_bytes(offs[3], ldd * n * 4), dtype=np.float32).reshape(n, ldd).T.copy()
     if mnk is None:
         D = D[:m, :]
-    return D, {"instructions": count, "grid": (nwgx, nwgy), "d_offset": offs[3], "memory": mem}
+    if splits:
+        info["tickets"] = np.frombuffer(mem.read_bytes(offs[5], nwgx * nwgy * 4), dtype=np.uint32).copy()
+    info.update({"instructions": count, "grid": grid, "d_offset": offs[3], "memory": mem})
+    return D, info

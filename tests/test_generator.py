@@ -193,6 +193,57 @@ def test_every_catalog_instance_has_no_scratch(kernels):
         d = g.read_toml(catalog.paths(name)[1])
         assert d["scratch_bytes_per_lane"] == 0, name
         assert d["lds_bytes_compiled"] == d["lds_usage_bytes"], name
+        if d["split_k"] != 1:   # the split-K kernel too (its LDS adds the 4-byte ticket slot)
+            assert d["splitk_scratch_bytes_per_lane"] == 0, name
+            assert d["splitk_lds_bytes_compiled"] == d["lds_usage_bytes"] + 4, name
+
+
+def test_split_k_code_object_exports_both_kernels(kernels):
+    """With split_k != 1 the code object keeps generated_gemm (the reference
+    runner's symbol, same 80-byte arguments) and adds generated_gemm_splitk
+    with ws, tickets and splits at offsets 80, 88, 96 (104 bytes)."""
+    co, toml = catalog.paths("mt128x64_a16_wg2x2_dk32_s3")
+    meta = _note_metadata(co)
+    assert ".name:           generated_gemm\n" in meta and ".name:           generated_gemm_splitk\n" in meta
+    # explicit arguments end at 76 and 100 bytes; the launch buffers are padded to 80 and 104
+    sizes = sorted(int(l.split(":")[1]) for l in meta.splitlines() if ".kernarg_segment_size:" in l)
+    assert sizes == [76, 100]
+    offsets = [int(l.split(":")[1]) for l in meta.splitlines() if l.strip().lstrip("- ").startswith(".offset:")]
+    assert sorted(set(offsets) - set(range(0, 76, 4))) == [80, 88, 96]
+    assert g.read_toml(toml)["split_k"] == 0
+    plain = _note_metadata(catalog.paths("mt256x256_a32_wg2x2_dk16_s3")[0])
+    assert "generated_gemm_splitk" not in plain
+
+
+def test_split_k_knob_validation():
+    assert g.GemmOptimizations(1).split_k == 1
+    for bad in (-1, 17):
+        with pytest.raises(RuntimeError, match="split_k"):
+            g.GemmOptimizations(1, split_k=bad)
+    assert g.kernel_defines(cfg(), g.GemmOptimizations(1, split_k=0))["SG_SPLITK"] == 1
+    assert g.kernel_defines(cfg(), g.GemmOptimizations(1))["SG_SPLITK"] == 0
+
+
+def test_auto_split_known_answers():
+    """The per-problem split rule at the shapes it was calibrated on (MI355X,
+    256 CUs): the best measured split counts lie where tiles x splits just
+    fills whole rounds of the compute units."""
+    assert catalog.auto_split("mt128x64_a16_wg2x2_dk16_s2", 512, 512, 16384) == 8      # 32 tiles -> 256 groups
+    assert catalog.auto_split("mt64x64_a16_wg1x4_dk32_s3", 256, 256, 65536) == 16      # 16 tiles -> 256 groups
+    assert catalog.auto_split("mt128x64_a16_wg2x2_dk32_s3", 384, 384, 32768) == 14     # 18 tiles -> 252 groups
+    assert catalog.auto_split("mt64x64_a16_wg1x4_dk32_s3", 1024, 1024, 1024) == 1      # 256 tiles fill the GPU
+    assert catalog.auto_split("mt64x64_a16_wg1x4_dk32_s3", 64, 64, 64) == 1            # 2 K tiles: too shallow
+    assert catalog.auto_split("mt256x256_a32_wg2x2_dk16", 512, 512, 1 << 20) == 1      # no split kernel
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        m, n, k = (int(x) for x in rng.integers(1, 5000, size=3))
+        name = catalog.select(m, n, k)
+        s = catalog.auto_split(name, m, n, k)
+        cfgx, _ = catalog.SOLUTIONS[name]
+        tiles = -(-m // cfgx.tile_size[0]) * -(-n // cfgx.tile_size[1])
+        assert 1 <= s <= 16 and (s == 1 or s <= -(-k // cfgx.depth_k) // 4)
+        if tiles >= 256:
+            assert s == 1
 
 
 def test_compile_failure_returns_nonzero_and_writes_no_toml(tmp_path):

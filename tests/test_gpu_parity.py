@@ -44,7 +44,6 @@ def _small_shape(name, mult=(2, 3, 3)):
     return t0 * mult[0], t1 * mult[1], cfg.depth_k * mult[2]
 
 
-@pytest.mark.parametrize("name", list(catalog.SOLUTIONS))
 def _operands(name, m, n, k, seed, dist=S.SGEMM_DIST_UNIFORM):
     """(stored A, stored B, op(A), op(B)) for an instance's transposition."""
     cfg, _ = catalog.SOLUTIONS[name]
@@ -280,6 +279,109 @@ def test_baseline_config(kernels, cid, m, n, k, seed, dist):
     scale_r = np.abs(A64) @ np.abs(B64).sum(axis=1)
     assert np.max(np.abs(colsum - colsum_ref) / scale_c) <= oracle.tolerance(k) * 10
     assert np.max(np.abs(rowsum - rowsum_ref) / scale_r) <= oracle.tolerance(k) * 10
+
+
+# ----------------------------------------------------------------- split-K
+SPLIT_CASES = [
+    # (instance, m, n, k, splits); 0 = the per-problem choice of the host library
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 70, 45, 16 * 7 + 5, 3),
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 32, 64, 32, 4),        # ranges 2 and 3 are empty
+    ("mt32x32_a32_wg1x1_dk16_sk4_tt", 333, 95, 1000, 16),    # transposed operands, 16 ranges
+    ("mt128x64_a16_wg2x2_dk32_s3", 1000, 999, 3001, 5),      # edge tiles and a K remainder
+    ("mt128x64_a16_wg2x2_dk16_s2", 512, 512, 16384, 0),      # few tiles, deep K: 16 ranges
+    ("mt64x64_a16_wg1x4_dk32_s3", 256, 256, 65536, 0),       # 16 tiles: 16 ranges
+    ("mt64x64_a16_wg1x4_dk32_s3", 1024, 1024, 1024, 0),      # 256 tiles: no split
+]
+
+
+@pytest.mark.parametrize("name,m,n,k,splits", SPLIT_CASES)
+def test_split_k(kernels, name, m, n, k, splits):
+    """generated_gemm_splitk against the oracle, and bitwise equal over repeated
+    launches on one handle (the partials are summed in range order whatever
+    work-group finishes last, and every launch re-arms the tile tickets)."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    _say(f"split-K {name} {m}x{n}x{k} splits {splits}")
+    A, B, opA, opB = _operands(name, m, n, k, 21)
+    C = S.fill_matrix(m, n, 21, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (A, B, C))
+    dD = S.DeviceBuffer(4 * m * n)
+    with _kernel(name) as kern:
+        kern.set_split_k(splits)
+        ws = kern.workspace_size(m, n, k)
+        _say(f"  workspace {ws} bytes")
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=1.5)
+        kern.synchronize()
+        D = dD.download().reshape(n, m).T.copy()
+        for _ in range(2):
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=1.5)
+        kern.synchronize()
+        again = dD.download().reshape(n, m).T
+    assert np.array_equal(D, again), "split-K result changed between launches"
+    cols = _sample_columns(n, 48, 21) if m * n * k > 1 << 27 else np.arange(n)
+    ref = oracle.cpu_gemm_mt(opA, opB[:, cols], C[:, cols], 0.5, 1.5, threads=16)
+    _check(D[:, cols], ref, k, f"{name} splits {splits}")
+    if splits == 0 and m * n == 1024 * 1024:
+        assert ws == 0, "a problem whose tiles fill the GPU must not split"
+    elif splits != 1:
+        assert ws > 0
+
+
+def test_split_k_sums_partials_in_range_order(kernels):
+    """Partials 2^24, 1, -2^24: only the range-order sum ((2^24 + 1) - 2^24)
+    is exactly 0 in float32; every other association gives 1."""
+    m, n, k = 32, 32, 48
+    A = np.ones((m, k), dtype=np.float32)
+    B = np.zeros((k, n), dtype=np.float32)
+    B[0, :], B[16, :], B[32, :] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    with _kernel("mt32x32_a32_wg1x1_dk16_s3_sk4") as kern:
+        kern.set_split_k(3)
+        for _ in range(3):
+            D, _ = kern.run(A, B, None, m, n, k, alpha=1.0, beta=0.0, warmup=2, runs=3)
+            assert np.array_equal(D, np.zeros((m, n), dtype=np.float32))
+
+
+def test_split_and_plain_launches_interleave_on_one_handle(kernels):
+    name = "mt128x64_a16_wg2x2_dk16_s2"
+    m, n, k = 384, 320, 4096
+    A = S.fill_matrix(m, k, 22, 0)
+    B = S.fill_matrix(k, n, 22, 1)
+    ref = oracle.cpu_gemm_mt(A, B, None, 1.0, 0.0, threads=16)
+    with _kernel(name) as kern:
+        for splits in (7, 1, 0, 16, 2):
+            kern.set_split_k(splits)
+            D, _ = kern.run(A, B, None, m, n, k, alpha=1.0, beta=0.0)
+            _check(D, ref, k, f"{name} splits {splits}")
+
+
+def test_host_split_rule_matches_the_catalog(kernels):
+    """The library's per-problem split count (sgemm_launch_splits) is the rule
+    catalog.auto_split restates, on this device's compute-unit count."""
+    cus = S.device_info()["compute_units"]
+    rng = np.random.default_rng(5)
+    shapes = [(512, 512, 16384), (256, 256, 65536), (384, 384, 32768), (1024, 1024, 1024), (33, 65, 100000)]
+    shapes += [tuple(int(x) for x in rng.integers(1, 3000, size=3)) for _ in range(40)]
+    for name in ("mt128x64_a16_wg2x2_dk16_s2", "mt64x64_a16_wg1x4_dk32_s3", "mt64x64_a16_wg2x2_dk32_s3",
+                 "mt256x256_a32_wg2x2_dk16_s3"):
+        with _kernel(name) as kern:
+            for (m, n, k) in shapes:
+                assert kern.launch_splits(m, n, k) == catalog.auto_split(name, m, n, k, cus), (name, m, n, k)
+
+
+def test_split_k_errors(kernels):
+    with _kernel("mt32x32_a32_wg1x1_dk16_s3_sk4") as kern:
+        assert kern.split_k == 4 and kern.info.split_k_max == 16
+        with pytest.raises(S.SgemmError, match="outside 0..16"):
+            kern.set_split_k(17)
+        with pytest.raises(S.SgemmError, match="outside 0..16"):
+            kern.set_split_k(-1)
+        assert kern.split_k == 4
+    with _kernel("mt128x128_a32_wg2x2_dk16") as kern:   # no split kernel in this code object
+        assert kern.info.split_k_max == 1
+        with pytest.raises(S.SgemmError, match="generated_gemm_splitk") as e:
+            kern.set_split_k(2)
+        assert e.value.code == -3
+        kern.set_split_k(0)   # per-problem choice: never splits without the kernel
+        assert kern.workspace_size(64, 64, 1 << 20) == 0
 
 
 # ----------------------------------------------------------------- runner

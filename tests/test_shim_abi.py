@@ -34,8 +34,8 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 2
-    assert ctypes.sizeof(S.KernelInfo) == 4 * 17  # 17 ints, as in sgemm_kernel_info
+    assert lib.sgemm_abi_version() == 3
+    assert ctypes.sizeof(S.KernelInfo) == 4 * 19  # 19 ints, as in sgemm_kernel_info
 
 
 def test_no_device_is_an_error_code_not_a_crash(tmp_path):
@@ -64,6 +64,10 @@ def test_open_reports_missing_files_and_bad_configs(tmp_path):
     assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
     bad.write_text(open(toml).read().replace("mfma = [32, 32, 1, 2]", "mfma = [4, 4, 4, 4]"))
     assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+    for bad_split in ("17", "-1"):
+        bad.write_text(open(toml).read().replace("split_k = 1\n", f"split_k = {bad_split}\n"))
+        assert lib.sgemm_open(co.encode(), str(bad).encode(), ctypes.byref(h)) == -3
+        assert b"split_k" in lib.sgemm_last_error()
     assert lib.sgemm_open(b"/nonexistent.co", toml.encode(), ctypes.byref(h)) == -2
     assert lib.sgemm_open(None, toml.encode(), ctypes.byref(h)) == -1
 
@@ -74,6 +78,10 @@ def test_null_arguments_are_rejected():
     assert lib.sgemm_get_info(None, None) == -1
     assert lib.sgemm_fill(None, 10, 0, 0, 0) == -1
     assert lib.sgemm_fill(None, 0, 0, 0, 0) == 0
+    assert lib.sgemm_set_split_k(None, 2) == -1
+    size = ctypes.c_size_t()
+    assert lib.sgemm_workspace_size(None, 64, 64, 64, ctypes.byref(size)) == -1
+    assert lib.sgemm_launch_splits(None, 64, 64, 64, None) == -1
 
 
 def test_runner_usage_error_exit_code():

@@ -24,14 +24,16 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 _PROGRAMS = {}
 
 
-def program(name):
-    """Parsed gfx950 assembly of a catalog instance (hipcc -S of its source)."""
-    if name not in _PROGRAMS:
+def program(name, kernel="generated_gemm"):
+    """Parsed gfx950 assembly of a catalog instance's kernel (hipcc -S of its source)."""
+    if (name, kernel) not in _PROGRAMS:
         cfg, opt = catalog.SOLUTIONS[name]
-        ctx = g.GpuContext()
-        g.gemm(ctx, "generated_gemm", "gfx950", cfg, opt, g.default_arguments())
-        _PROGRAMS[name] = (V.parse_assembly(ctx.assembly()), cfg)
-    return _PROGRAMS[name]
+        if name not in _PROGRAMS:
+            ctx = g.GpuContext()
+            g.gemm(ctx, "generated_gemm", "gfx950", cfg, opt, g.default_arguments())
+            _PROGRAMS[name] = ctx.assembly()
+        _PROGRAMS[(name, kernel)] = (V.parse_assembly(_PROGRAMS[name], kernel), cfg)
+    return _PROGRAMS[(name, kernel)]
 
 
 def vm_sgemm(name, A, B, C=None, alpha=1.0, beta=0.0):
@@ -272,6 +274,113 @@ def test_transposed_layouts_in_vm(name, shape, pad):
     opA = A[:ra, :ca].T if cfg.trans_a else A[:m, :k]
     opB = B[:rb, :cb].T if cfg.trans_b else B[:k, :n]
     assert oracle.normwise_error(D[:m, :n], oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+
+
+# ------------------------------------------------------------- split-K
+SPLIT_CASES = [
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 70, 45, 16 * 7 + 5, 3),   # ragged M, N, K
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 32, 64, 16 * 2, 4),       # ranges 2 and 3 are empty
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 40, 33, 16 * 16, 16),     # the largest split count
+    ("mt64x64_a16_wg2x2_dk32_s3", 64, 70, 32 * 5, 5),           # a tuned instance, four waves
+    ("mt32x32_a32_wg1x1_dk16_sk4_tt", 33, 31, 16 * 6 + 1, 3),   # op(A) = A^T, op(B) = B^T
+]
+
+
+def _split_operands(cfg, m, n, k, seed):
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    A = oracle.fill_matrix(ra, ca, seed, 0)
+    B = oracle.fill_matrix(rb, cb, seed, 1)
+    C = oracle.fill_matrix(m, n, seed, 2)
+    opA = A.T if cfg.trans_a else A
+    opB = B.T if cfg.trans_b else B
+    return A, B, C, opA, opB
+
+
+@pytest.mark.parametrize("name,m,n,k,splits", SPLIT_CASES)
+def test_split_k_in_vm(name, m, n, k, splits):
+    """generated_gemm_splitk: every (tile, K range) work-group writes a partial,
+    the tile's last arrival sums them in range order and runs the epilogue.
+    The sum must not depend on which work-group arrives last (the VM runs the
+    grid in three different orders), and every ticket is re-armed to 0."""
+    prog, cfg = program(name, "generated_gemm_splitk")
+    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 6)
+    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m,
+                        splits=splits)
+    assert oracle.normwise_error(D, oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+    assert not info["tickets"].any()
+    groups = [(x, y, z) for z in range(splits) for y in range(info["grid"][1]) for x in range(info["grid"][0])]
+    rng = np.random.default_rng(0)
+    for order in (groups[::-1], [groups[i] for i in rng.permutation(len(groups))]):
+        D2, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m,
+                              splits=splits, order=order)
+        assert np.array_equal(D2, D) and not info2["tickets"].any()
+
+
+def test_split_k_with_one_range_equals_the_plain_kernel():
+    name = "mt32x32_a32_wg1x1_dk16_s3_sk4"
+    plain, cfg = program(name)
+    split, _ = program(name, "generated_gemm_splitk")
+    A, B, C, _, _ = _split_operands(cfg, 45, 37, 83, 7)
+    D1, _ = run_sgemm(plain, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5)
+    D2, _ = run_sgemm(split, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, splits=1)
+    assert np.array_equal(D1, D2)
+
+
+def test_split_k_sums_partials_in_range_order():
+    """Partials 2^24, 1 and -2^24 (one nonzero row of B per K range): in range
+    order (2^24 + 1) rounds to 2^24 and the sum is exactly 0; every other
+    association (for instance starting from the last arrival's own partial)
+    gives 1."""
+    prog, cfg = program("mt32x32_a32_wg1x1_dk16_s3_sk4", "generated_gemm_splitk")
+    m, n, k = 32, 32, 48
+    A = np.ones((m, k), dtype=np.float32)
+    B = np.zeros((k, n), dtype=np.float32)
+    B[0, :], B[16, :], B[32, :] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    for order in (None, [(0, 0, 2), (0, 0, 1), (0, 0, 0)], [(0, 0, 1), (0, 0, 2), (0, 0, 0)]):
+        D, _ = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, None, 1.0, 0.0, splits=3, order=order)
+        assert np.array_equal(D, np.zeros((m, n), dtype=np.float32)), order
+
+
+def test_vm_buffer_access_is_range_checked_like_the_hardware():
+    """MUBUF with a raw resource: loads past num_records read 0, stores past
+    it are dropped (per access)."""
+    vm = GcnVirtualMachine(104, 256, 64)
+    mem = V.Memory(8192, "vmem")
+    mem.allocate_region(4096, 1024, "buf")
+    mem.write_bytes(4096, np.arange(256, dtype=np.float32).tobytes())
+    vm.vmem = mem
+    vm.s[8], vm.s[9], vm.s[10], vm.s[11] = 4096, 0, 512, 0x20000   # 128 floats in range
+    vm.v[1] = (np.arange(64, dtype=np.uint32) * 16)                  # lane l: float4 at l*16 bytes
+    vm.v[10] = np.full(64, fbits(-1.0), dtype=np.uint32)
+    vm.run("generated_gemm:\n buffer_load_dwordx4 v[2:5], v1, s[8:11], 0 offen sc1\n s_waitcnt vmcnt(0)\n"
+           " buffer_store_dword v10, v1, s[8:11], 4 offen\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    got = np.stack([vm.v[2 + i].view(np.float32) for i in range(4)], axis=1)
+    want = np.zeros((64, 4), dtype=np.float32)
+    want[:32] = np.arange(128, dtype=np.float32).reshape(32, 4)
+    assert np.array_equal(got, want)
+    after = np.frombuffer(mem.read_bytes(4096, 1024), dtype=np.float32)
+    assert np.all(after[1:128:4] == -1.0) and np.array_equal(after[128:], np.arange(128, 256, dtype=np.float32))
+
+
+def test_vm_atomics_and_lane_counts():
+    vm = GcnVirtualMachine(104, 256, 64)
+    mem = V.Memory(8192, "vmem")
+    mem.allocate_region(4096, 64, "counter")
+    mem.write_bytes(4096, struct.pack("<I", 5))
+    vm.vmem = mem
+    vm.s[8], vm.s[9] = 4096, 0
+    vm.v[0] = np.zeros(64, dtype=np.uint32)
+    vm.v[1] = np.full(64, 2, dtype=np.uint32)
+    vm.s[20], vm.s[21] = 0xF0F0F0F0, 0x0000FFFF
+    vm.run("generated_gemm:\n global_atomic_add v2, v0, v1, s[8:9] sc0\n s_waitcnt vmcnt(0)\n"
+           " v_mbcnt_lo_u32_b32 v3, s20, 0\n v_mbcnt_hi_u32_b32 v3, s21, v3\n s_bcnt1_i32_b64 s22, s[20:21]\n"
+           " s_endpgm\n")
+    assert np.array_equal(vm.v[2], 5 + 2 * np.arange(64, dtype=np.uint32))   # lanes in order
+    assert struct.unpack("<I", mem.read_bytes(4096, 4))[0] == 5 + 2 * 64
+    mask = 0x0000FFFFF0F0F0F0
+    want = [bin(mask & ((1 << l) - 1)).count("1") for l in range(64)]
+    assert vm.v[3].tolist() == want and vm.s[22] == bin(mask).count("1")
 
 
 def test_an_undersized_buffer_is_caught():
