@@ -277,14 +277,21 @@ __device__ __forceinline__ void interleave_block() {
     }
 }
 
-// Maps the hardware work-group id to the logical (tile_x, tile_y).
-__device__ __forceinline__ void tile_coords(int bx, int by, int nwgx, int nwgy, int& tx, int& ty) {
-    int z = bx + by * nwgx;
-    const int total = nwgx * nwgy;
+// Work-group `lin` (of `total`, dispatched round-robin) runs on XCD
+// lin % SG_XCD; renumber so that each XCD owns one contiguous range of the
+// logical order (XCD x gets total / SG_XCD work-groups, one more for the first
+// total % SG_XCD XCDs).  A bijection on [0, total).
+__device__ __forceinline__ int xcd_order(int lin, int total) {
     if constexpr (SG_XCD > 1) {
-        // Work-group z runs on XCD z % SG_XCD; give each XCD a contiguous range.
-        if (total % SG_XCD == 0) z = (z % SG_XCD) * (total / SG_XCD) + z / SG_XCD;
+        const int x = lin % SG_XCD, q = total / SG_XCD, r = total % SG_XCD;
+        return x * q + (x < r ? x : r) + lin / SG_XCD;
     }
+    return lin;
+}
+
+// Maps a logical tile index to (tile_x, tile_y): groups SG_WGM tiles wide
+// along M, column by column inside a group.
+__device__ __forceinline__ void tile_coords(int z, int nwgx, int nwgy, int& tx, int& ty) {
     if constexpr (SG_WGM > 1) {
         const int span = SG_WGM * nwgy;
         const int group = z / span;
@@ -339,19 +346,26 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const int wm = wave % SG_WG0;
     const int wn = wave / SG_WG0;
 
+    // Logical tile: the XCD renumbering and grouping act on the 2-D tile grid;
+    // a split launch takes its K range from blockIdx.z.  (Both orderings of
+    // the whole (tile, range) grid tried -- range by range, and tile by tile --
+    // measured slower on MI355X.)
+    const int tiles = numWorkgroupX * numWorkgroupY;
+    const int split = SPLIT ? (int)blockIdx.z : 0;
     int tx, ty;
-    tile_coords(blockIdx.x, blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
+    tile_coords(xcd_order((int)blockIdx.x + numWorkgroupX * (int)blockIdx.y, tiles), numWorkgroupX, numWorkgroupY,
+                tx, ty);
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
 
-    // K range of this work-group: all of it, or split blockIdx.z of `splits`
+    // K range of this work-group: all of it, or range `split` of `splits`
     // ranges of whole K tiles (the last range takes the remainder; ranges past
     // the end are empty and contribute a zero partial).
     uint32_t k = k_total;
     if constexpr (SPLIT) {
         const uint32_t kt_all = (k_total + DK - 1) / DK;
         const uint32_t per = (kt_all + splits - 1) / splits;
-        const uint32_t t_first = min((uint32_t)blockIdx.z * per, kt_all);
+        const uint32_t t_first = min((uint32_t)split * per, kt_all);
         const uint32_t k_first = t_first * DK;
         const uint32_t k_end = min(k_first + per * DK, k_total);
         k = k_end > k_first ? k_end - k_first : 0u;
@@ -672,7 +686,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                     v.x = acc[i][j][4 * h]; v.y = acc[i][j][4 * h + 1];
                     v.z = acc[i][j][4 * h + 2]; v.w = acc[i][j][4 * h + 3];
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (ch * NT + tid) * 16,
-                                                           (int)(blockIdx.z * PART_BYTES), CPOL_SC1);
+                                                           (int)((uint32_t)split * PART_BYTES), CPOL_SC1);
                 }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __shared__ uint32_t arrived;

@@ -53,6 +53,7 @@ WORKLOADS = {
     "cfg3": (4096, 4096, 4096, 2, 0),
     "cfg4": (8192, 8192, 256, 3, 1),
     "cfg5": (16384, 128, 4096, 4, 0),
+    "deepk": (512, 512, 16384, 5, 0),   # few tiles, deep K: the split-K kernel
 }
 
 

@@ -95,6 +95,13 @@ int main(int argc, char** argv) {
         return -1;
     }
 
+    int splits = 1;
+    if ((r = sgemm_launch_splits(h, m, n, k, &splits)) != SGEMM_OK) {
+        sgemm_close(h);
+        return shim_error("sgemm_launch_splits", r);
+    }
+    std::cout << "K ranges per output tile: " << splits << (splits > 1 ? " (generated_gemm_splitk)" : "") << "\n";
+
     std::vector<float> A((size_t)m * k), B((size_t)k * n), C((size_t)m * n), D((size_t)m * n, 0.0f);
     if ((r = sgemm_fill(A.data(), A.size(), seed, 0, (int)dist)) != SGEMM_OK ||
         (r = sgemm_fill(B.data(), B.size(), seed, 1, (int)dist)) != SGEMM_OK ||

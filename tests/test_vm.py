@@ -201,6 +201,14 @@ def test_xcd_and_wgm_order_is_a_bijection_with_contiguous_xcd_ranges():
         zl = (z % 8) * 2 + z // 8
         width = 4
         assert (tx, ty) == (zl % width, zl // width)
+    # 15 tiles on 8 XCDs: XCD x owns 15 // 8 = 1 tile, plus one more for x < 7,
+    # starting at x * 1 + min(x, 7) in the logical order
+    owner = _tile_owner_map("mt64x64_a32_wg1x1_dk16", 3, 5)
+    assert sorted(owner.values()) == [(x, y) for x in range(3) for y in range(5)]
+    for (wx, wy), (tx, ty) in owner.items():
+        z = wx + 3 * wy
+        zl = (z % 8) * 1 + min(z % 8, 7) + z // 8
+        assert (tx, ty) == (zl % 3, zl // 3)
 
 
 # ------------------------------------------- the checker catches mistakes
