@@ -384,6 +384,57 @@ def test_split_k_errors(kernels):
         assert kern.workspace_size(64, 64, 1 << 20) == 0
 
 
+# ----------------------------------------------------------- random cases
+def _random_cases(count, seed):
+    """(instance, m, n, k, pads, alpha, beta, splits) drawn from every catalog instance."""
+    rng = np.random.default_rng(seed)
+    names = sorted(catalog.SOLUTIONS)
+    cases = []
+    for i in range(count):
+        name = names[int(rng.integers(len(names)))]
+        cfg, opt = catalog.SOLUTIONS[name]
+        t0, t1 = cfg.tile_size
+        m = int(rng.integers(1, 3 * t0 + 1))
+        n = int(rng.integers(1, 3 * t1 + 1))
+        k = int(rng.integers(0, 6 * cfg.depth_k + 1))
+        pads = tuple(int(x) for x in rng.choice([0, 0, 1, 3, 4], size=4))
+        alpha = float(rng.choice([1.0, -0.5, 2.0]))
+        beta = float(rng.choice([0.0, 1.0, -1.25]))
+        splits = int(rng.choice([0, 2, 3, 16])) if opt.split_k != 1 else 1
+        cases.append((name, m, n, k, pads, alpha, beta, splits))
+    return cases
+
+
+@pytest.mark.parametrize("name,m,n,k,pads,alpha,beta,splits", _random_cases(40, 2024))
+def test_random_shapes_layouts_and_splits(kernels, name, m, n, k, pads, alpha, beta, splits):
+    """Seeded random problems over every catalog instance: any m, n, k (k = 0
+    included), padded leading dimensions, alpha/beta, transposed operands and
+    split counts, against the oracle; rows past m of D stay untouched."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    _say(f"random {name} {m}x{n}x{k} pads {pads} alpha {alpha} beta {beta} splits {splits}")
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    lda, ldb, ldc, ldd = max(ra, 1) + pads[0], max(rb, 1) + pads[1], m + pads[2], m + pads[3]
+    Af = S.fill_matrix(lda, max(ca, 1), 31, 0)
+    Bf = S.fill_matrix(ldb, max(cb, 1), 31, 1)
+    Cf = S.fill_matrix(ldc, n, 31, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer.from_array(np.full((ldd, n), 9.5, dtype=np.float32))
+    with _kernel(name) as kern:
+        kern.set_split_k(splits)
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd)
+        kern.synchronize()
+    Dfull = dD.download().reshape(n, ldd).T
+    opA = np.asfortranarray(Af[:ra, :ca].T if cfg.trans_a else Af[:m, :k])
+    opB = np.asfortranarray(Bf[:rb, :cb].T if cfg.trans_b else Bf[:k, :n])
+    ref = oracle.cpu_gemm(opA, opB, Cf[:m, :n], alpha, beta)
+    if k == 0 or not np.any(ref):
+        assert np.array_equal(Dfull[:m, :], ref)
+    else:
+        _check(Dfull[:m, :], ref, k, name)
+    assert np.all(Dfull[m:, :] == 9.5), "rows past m of D were written"
+
+
 # ----------------------------------------------------------------- runner
 def _run(cmd, timeout=300):
     _say("+ " + " ".join(cmd))
