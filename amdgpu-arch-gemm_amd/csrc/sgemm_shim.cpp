@@ -534,7 +534,8 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
             h->tickets = nullptr;
             h->ticket_count = 0;
             HIP_TRY(hipMalloc((void**)&h->tickets, tiles * 4));
-            HIP_TRY(hipMemset(h->tickets, 0, tiles * 4));
+            // ordered before the launch below on the same stream
+            HIP_TRY(hipMemsetAsync(h->tickets, 0, tiles * 4, h->stream));
             h->ticket_count = tiles;
         }
     }

@@ -14,8 +14,10 @@ stdout line) and print the best.  Additions:
   {2x2, 4x1} x MFMA atom {32x32x2, 16x16x4} (stage 1), then the code-shape
   knobs depth_k {16,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
   x prefetch depth {1,2}
-  on the best ``--refine`` geometries (stage 2).  ``--space reference`` is the
-  reference's own 9-knob product.
+  on the best ``--refine`` geometries (stage 2), optionally crossed with
+  ``--split-k`` (split-K kernel; 0 = split count chosen per problem) and
+  ``--occ`` (waves per SIMD the registers are capped for).  ``--space
+  reference`` is the reference's own 9-knob product.
 * every result is appended to ``<out>/results.jsonl`` and a rerun skips
   points already there (resume);
 * each point runs in isolation: compile failures, runner failures and
@@ -91,7 +93,7 @@ def point_key(cfg: GemmSolutionConfig, opt: GemmOptimizations) -> str:
     return (f"a{cfg.mfma[0]}_wg{cfg.wave_group[0]}x{cfg.wave_group[1]}_wt{cfg.wave_tiling[0]}x{cfg.wave_tiling[1]}"
             f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}"
             + (f"_pd{opt.pd}" if opt.pd != 1 else "") + (f"_occ{opt.occ}" if opt.occ else "")
-            + (f"_sk{opt.split_k}" if opt.split_k > 1 else ""))
+            + (f"_sk{opt.split_k}" if opt.split_k != 1 else ""))
 
 
 def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1, occ=0,

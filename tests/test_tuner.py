@@ -1,0 +1,121 @@
+"""The gfx950 tuner (amdgpu-arch-gemm_amd/tuner/sgemm_tuner.py), without a GPU.
+
+The reference tuner (tuner/sgemm_tuner.py:41-128) enumerates knobs, compiles
+each point, runs the runner and prints the best; this one adds a gfx950 space,
+JSONL resume, per-point isolation and re-emission of the winner.  These tests
+drive its pieces with a fake benchmark so no GPU is needed.
+"""
+import json
+import os
+from itertools import product
+
+import pytest
+
+from generator import generator as g
+from tuner import sgemm_tuner as T
+
+
+def test_gfx950_stage1_space():
+    """Macro-tile {64,128,256}^2 x wave group {2x2, 4x1} x atom {32x32x2,
+    16x16x4}: every combination the generator accepts, and nothing else."""
+    pts = list(T.geometry_points(T.DEFAULT_KNOBS))
+    got = sorted((c.tile_size, c.wave_group, c.mfma) for c, _ in pts)
+    want = []
+    for (mt0, mt1), wg, mfma in product([(a, b) for a in (64, 128, 256) for b in (64, 128, 256)],
+                                        [(2, 2), (4, 1)], [(16, 16, 1, 4), (32, 32, 1, 2)]):
+        if mt0 % (mfma[0] * wg[0]) or mt1 % (mfma[1] * wg[1]):
+            continue
+        wt = (mt0 // (mfma[0] * wg[0]), mt1 // (mfma[1] * wg[1]))
+        try:
+            g.GemmSolutionConfig(g.DataType.FP32, g.DataType.FP32, g.DataType.FP32, g.DataType.FP32, mfma, wg, wt,
+                                 16, False, False, vmem_stage=2)
+        except RuntimeError:
+            continue
+        want.append(((mt0, mt1), wg, mfma))
+    assert got == sorted(want)
+    # the expressible part of the reference's own sweep of this space (33 points) minus what
+    # gfx950's limits reject (wave tiling above 8, LDS above 160 KiB)
+    assert 24 <= len(got) <= 33
+    assert ((256, 256), (2, 2), (32, 32, 1, 2)) in got   # the headline geometry
+
+
+def test_fits_skips_only_tiles_larger_than_the_problem():
+    cfg, _ = T.make_point((32, 32, 1, 2), (2, 2), (4, 4), 16, 2, 4, 3, 0, 0, 8)
+    assert T.fits(cfg, 256, 256, 16)
+    assert T.fits(cfg, 1000, 999, 1001)       # edge tiles are masked in the kernel
+    assert not T.fits(cfg, 255, 4096, 4096)   # the tile is larger than the problem
+    # 32 x 32 tile, 256 work-items, DK 16: 32*16*4 / 256 = 8 bytes of A per work-item, under the
+    # reference's one-16-byte-load filter (sgemm_tuner.py:102-105)
+    small, _ = T.make_point((16, 16, 1, 4), (2, 2), (1, 1), 16, 1, 1, 1, 0, 0, 0)
+    assert small.num_bytes_per_buffer_load == (8, 8)
+    assert not T.fits(small, 64, 64, 64)
+    one_wave, _ = T.make_point((16, 16, 1, 4), (1, 1), (1, 1), 16, 1, 1, 1, 0, 0, 0)
+    assert T.fits(one_wave, 64, 64, 64)        # 16 x 16 x 16 x 4 / 64 = 16 bytes
+
+
+def test_point_keys_distinguish_every_knob():
+    cfg, _ = T.make_point((16, 16, 1, 4), (2, 2), (4, 2), 16, 1, 1, 1, 0, 0, 0)
+    pts = list(T.knob_points(cfg, split_ks=(1, 0, 4), occs=(0, 2)))
+    keys = [T.point_key(*p) for p in pts]
+    assert len(keys) == len(set(keys))
+    opts = {(o.depth_k if hasattr(o, "depth_k") else c.depth_k, c.vmem_stage, o.wgm, o.xcd, o.plr, o.pd, o.split_k, o.occ)
+            for c, o in pts}
+    assert len(opts) == len(pts)
+    assert any(k.endswith("_sk4") for k in keys) and any("_occ2" in k for k in keys)
+
+
+def _fake_points(out, keys, spilling=()):
+    d = T.point_dir(out)
+    os.makedirs(d, exist_ok=True)
+    for k in keys:
+        open(os.path.join(d, f"{k}.co"), "wb").write(k.encode())
+        g.write_toml({"name": k, "scratch_bytes_per_lane": 64 if k in spilling else 0},
+                     os.path.join(d, f"{k}.toml"))
+
+
+def test_sweep_resumes_isolates_failures_and_emits_the_best(tmp_path, monkeypatch):
+    out = str(tmp_path)
+    monkeypatch.setattr(T, "POINTS_DIR", None)
+    pts = [T.make_point((32, 32, 1, 2), (2, 2), wt, 16, 2, 4, 3, 0, 0, 8) for wt in ((1, 1), (2, 2), (4, 4), (2, 1))]
+    keys = [T.point_key(*p) for p in pts]
+    _fake_points(out, keys[:3], spilling={keys[1]})
+    compiled = {keys[0]: 0, keys[1]: 0, keys[2]: 0, keys[3]: 1}   # the last failed to compile
+    calls = []
+
+    def bench(co, toml, timeout):
+        calls.append(os.path.basename(co))
+        if "wt1x1" in co:
+            raise RuntimeError("runner crashed")               # isolated, the sweep goes on
+        return 0, 1234.5
+
+    results = os.path.join(out, "results.jsonl")
+    recs = T.sweep(pts, out, 256, 256, 64, bench, 10.0, results, compiled)
+    status = {r["point"]: r["status"] for r in recs}
+    assert status[keys[0]].startswith("error") and status[keys[1]] == "spills"
+    assert status[keys[2]] == "ok" and status[keys[3]] == "compile_error"
+    assert len(calls) == 2
+    # resume: nothing is benchmarked again, the records come back from the JSONL file
+    recs2 = T.sweep(pts, out, 256, 256, 64, bench, 10.0, results, compiled)
+    assert len(calls) == 2 and [r["status"] for r in recs2] == [r["status"] for r in recs]
+    assert len(open(results).read().splitlines()) == 4
+    best = max((r for r in recs if r["status"] == "ok"), key=lambda r: r["gflops"])
+    T.emit_best(out, best)
+    assert open(os.path.join(out, "generated_gemm.co"), "rb").read() == keys[2].encode()
+    assert g.read_toml(os.path.join(out, "generated_gemm.toml"))["name"] == keys[2]
+
+
+def test_compile_only_builds_stage1_with_split_and_occupancy_knobs(tmp_path):
+    out = str(tmp_path)
+    rc = T.main(["--m", "64", "--n", "64", "--k", "64", "--bench", "unused", "--output-folder", out,
+                 "--compile-only", "--jobs", "8"])
+    assert rc == 0
+    built = sorted(f for f in os.listdir(os.path.join(out, "points")) if f.endswith(".co"))
+    assert built and all(f.startswith(("a16_", "a32_")) for f in built)
+    for f in built:
+        d = g.read_toml(os.path.join(out, "points", f[:-3] + ".toml"))
+        assert d["scratch_bytes_per_lane"] == 0 and d["split_k"] == 1
+    # the knob lists reach stage 2 (and the keys), checked without compiling
+    cfg, _ = T.make_point((16, 16, 1, 4), (2, 2), (2, 2), 16, 2, 4, 3, 0, 0, 8)
+    keys = {T.point_key(*p) for p in T.knob_points(cfg, split_ks=(1, 0), occs=(0, 2))}
+    assert any(k.endswith("_occ2_sk0") for k in keys) and any(k.endswith("_occ2") for k in keys)
+    assert sum(1 for k in keys if k.endswith("_sk0")) * 2 == len(keys)
