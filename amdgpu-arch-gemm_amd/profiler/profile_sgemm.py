@@ -1,7 +1,7 @@
 """rocprofv3 measurement of one SGEMM kernel instance on one workload.
 
     python amdgpu-arch-gemm_amd/profiler/profile_sgemm.py --kernel NAME \
-        --workload cfg3 --out gpurun_out/prof_cfg3 [--summary profiles/NAME_cfg3.md]
+        --workload cfg3 --out prof_out/cfg3 [--summary profiles/NAME_cfg3.md]
 
 This script never touches the GPU itself: every measurement is a child
 process -- rocprofv3 wrapping the GeneratorRunner executable (the product's
@@ -136,7 +136,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--kernel", required=True)
     ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
-    ap.add_argument("--out", required=True, help="raw rocprofv3 output folder (e.g. under gpurun_out/)")
+    ap.add_argument("--out", required=True, help="raw rocprofv3 output folder (large; keep it out of the repository)")
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
     ap.add_argument("--runs", type=int, default=20)
     ap.add_argument("--cus", type=int, default=256)
@@ -208,7 +208,7 @@ def main():
         "Command (from the repository root on the GPU box):",
         "",
         f"    python amdgpu-arch-gemm_amd/profiler/profile_sgemm.py --kernel {args.kernel} "
-        f"--workload {args.workload} --out gpurun_out/prof_{args.workload} --summary {os.path.relpath(summary, ROOT)}",
+        f"--workload {args.workload} --out {args.out} --summary {os.path.relpath(summary, ROOT)}",
         "",
         "which runs, each in its own process (`<runner>` = `"
         + " ".join(os.path.relpath(c, ROOT) if os.path.isabs(c) else c for c in runner) + "`):",

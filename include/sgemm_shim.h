@@ -125,11 +125,12 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
 int sgemm_set_split_k(sgemm_handle* h, int splits);
 
 /* Device bytes the handle's workspace needs for an m x n x k launch with its
- * current split count (0 when the launch does not split). */
+ * current split count (0 when the launch does not split).  No counterpart in
+ * the reference (its kernel needs no workspace). */
 int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes);
 
 /* K ranges an m x n x k launch with the handle's current setting uses
- * (1: generated_gemm, no split). */
+ * (1: generated_gemm, no split).  No counterpart in the reference. */
 int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits);
 
 /* Device memory (generator_runner.cpp:236-242, :291, :319-322). */
