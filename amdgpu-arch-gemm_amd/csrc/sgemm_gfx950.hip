@@ -213,7 +213,7 @@ template <int W> __device__ __forceinline__ void lds_read_row(const float* p, fl
     }
 }
 
-template <int W> __device__ __forceinline__ void global_store_row(float* p, const float (&v)[W]) {
+template <int W> __device__ __forceinline__ void store_row(float* p, const float (&v)[W]) {
     if constexpr (W == 1) {
         p[0] = v[0];
     } else if constexpr (W == 2) {
@@ -730,6 +730,56 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // ---- epilogue: D = alpha * acc + beta * C ----
     const int wrow = row0 + wm * (AT::M * WT0);
     const int wcol = col0 + wn * (AT::N * WT1);
+    // Whole tiles go through LDS: the accumulators of one MFMA column group
+    // (atom_n columns of the wave's SM-row sub-tile) are scattered into a
+    // column-major LDS chunk, then read back as float4 runs down each column,
+    // so one store instruction writes whole columns (SM * 4 bytes each, full
+    // 128-byte lines) instead of 16 bytes in each of atom_n columns.
+    constexpr int SM = AT::M * WT0;           // rows of a wave's sub-tile
+    constexpr int E_LD = SM + 4;              // LDS column stride (4-float pad: conflict-free scatter)
+    constexpr int E_CHUNK = AT::N * E_LD;     // floats of LDS per wave
+    constexpr int E_RUNS = SM / 4;            // float4 runs per column
+    constexpr int E_PER_LANE = AT::N * E_RUNS / 64;
+    static_assert(AT::N * E_RUNS % 64 == 0, "a column group is a whole number of float4s per lane");
+    if constexpr ((NT / 64) * E_CHUNK <= G::LDS_FLOATS) {
+        if (!slow_mn) {
+            // every wave's last K-loop access to LDS is behind this barrier
+            __syncthreads();
+            float* e = lds + wave * E_CHUNK;
+#pragma unroll
+            for (int jn = 0; jn < WT1; ++jn) {
+#pragma unroll
+                for (int q = 0; q < AT::ACC; ++q) {
+                    float v[WT0];
+#pragma unroll
+                    for (int i = 0; i < WT0; ++i) v[i] = alpha * acc[i][jn][q];
+                    store_row<WT0>(e + (lane % AT::N) * E_LD + AT::row(q, lane) * WT0, v);
+                }
+                // the wave's scattered writes are complete before any lane reads them back
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int p = 0; p < E_PER_LANE; ++p) {
+                    const int idx = p * 64 + lane;
+                    const int cc = idx / E_RUNS, r4 = (idx % E_RUNS) * 4;
+                    f32x4 v = *reinterpret_cast<const f32x4*>(e + cc * E_LD + r4);
+                    const size_t col = (size_t)(wcol + jn * AT::N + cc);
+                    if (beta != 0.0f) {
+                        const f32x4 cv = *reinterpret_cast<const f32x4*>(c + col * ldc + wrow + r4);
+                        v.x = __builtin_fmaf(beta, cv.x, v.x); v.y = __builtin_fmaf(beta, cv.y, v.y);
+                        v.z = __builtin_fmaf(beta, cv.z, v.z); v.w = __builtin_fmaf(beta, cv.w, v.w);
+                    }
+                    *reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4) = v;
+                }
+                // this group's reads are done before the next group overwrites the chunk
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int jn = 0; jn < WT1; ++jn) {
         const size_t colo = (size_t)(wcol + jn * AT::N + (lane % AT::N));
@@ -746,7 +796,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 #pragma unroll
                     for (int i = 0; i < WT0; ++i) v[i] = __builtin_fmaf(beta, cv[i], v[i]);
                 }
-                global_store_row<WT0>(d + colo * ldd + rr, v);
+                store_row<WT0>(d + colo * ldd + rr, v);
             } else if (colo < n) {
 #pragma unroll
                 for (int i = 0; i < WT0; ++i) {
