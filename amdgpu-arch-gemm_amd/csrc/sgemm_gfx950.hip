@@ -18,14 +18,18 @@
 // MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  Any m, n, k works: tiles
 // that lie wholly inside D with 16-byte aligned columns (every leading
 // dimension a multiple of 4) take the vector path, edge tiles and unaligned
-// problems load and store element by element with bounds checks, and a K
-// remainder is zero-filled in the last K tile.  The host side (shim, runner)
+// problems load and store element by element with bounds checks.  A K
+// remainder (k % 4 == 0) keeps the vector path by shifting the K origin so
+// that the first K tile is the partial one, its missing values loaded as
+// zeros; otherwise the last K tile is zero-filled on the element-wise path.
+// The host side (shim, runner)
 // checks that lda >= m, ldb >= k, ldc >= m, ldd >= m before every launch.
 //
 // Data path per K tile of depth DK:
 //   HBM --global_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
 //   LDS --ds_read_b{32,64,128}--> VGPR --v_mfma_f32_{32x32x2,16x16x4}_f32--> accumulators
-// and after the K loop accumulators --(alpha, beta)--> global_store_dwordx{1,2,4}.
+// and after the K loop accumulators --(alpha)--> LDS column chunk --(beta * C)-->
+// global_store_dwordx4 down whole columns of D.
 //
 // LDS layouts (floats):
 //   A tile: [DK][MT0 + PAD_A]  -- one k per row, m contiguous; written straight
@@ -246,6 +250,9 @@ template <int W> __device__ __forceinline__ void global_load_row(const float* p,
 // Tags selecting the vector (interior, aligned) or element-wise (edge) loads.
 struct FastPath { static constexpr bool slow = false; };
 struct SlowPath { static constexpr bool slow = true; };
+// Tags marking the load of a partial first K tile (shifted K origin) or any other.
+struct Head { static constexpr bool on = true; };
+struct NoHead { static constexpr bool on = false; };
 
 // Scheduling masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SCHED_MFMA = 0x008;
@@ -375,11 +382,19 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const int ktiles = (int)((k + DK - 1) / DK);
     // Uniform per work-group: the vector fast path needs a whole tile inside D
     // and 16-byte aligned rows of every operand; otherwise loads and stores go
-    // element by element with bounds checks.  A K remainder makes only the last
-    // K tile masked.
+    // element by element with bounds checks.
+    //
+    // A K remainder stays on the fast path when k % 4 == 0, there are at least
+    // two K tiles and the first K tile is not rotated: the K origin moves back
+    // by kshift, so K tile t covers k in [t*DK - kshift, (t+1)*DK - kshift).
+    // Only tile 0 is then partial; its first kshift values load as zeros
+    // (whole float4 chunks, masked), and every later tile -- including the one
+    // the branch-free refill repeats past the end -- is whole and in bounds.
+    // Otherwise the slow path zero-fills the last K tile.
     const bool aligned = ((lda | ldb | ldc | ldd) & 3u) == 0;
     const bool slow_mn = !aligned || row0 + MT0 > m || col0 + MT1 > n;
-    const int kt_partial = (k % DK) ? ktiles - 1 : -1;
+    const uint32_t kshift = (k % DK) ? DK - k % DK : 0u;
+    const bool slow_k = kshift != 0u && (SG_MAPK > 1 || (k & 3u) != 0u || ktiles < 2);
 
     // ---- global -> VGPR staging (element offsets inside a K tile, 64-bit bases) ----
     // Every thread moves float4 chunks.  A chunk runs along the operand's
@@ -429,23 +444,48 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     int kt_first = 0;
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
 
-    // gload(tag, t): global -> VGPR copy of K tile t.  With a SlowPath tag every
-    // element is loaded from a clamped (always valid) address and replaced by
-    // 0 when it lies outside A or B, so the code stays branch-free.
-    auto gload = [&](auto path, int t, int set) __attribute__((always_inline)) {
+    // gload(tag, t, set, head): global -> VGPR copy of K tile t.  On the fast
+    // path a Head tag (tile 0 of a shifted K origin) loads only the chunks at
+    // k >= kshift and zeros the rest.  With a SlowPath tag every element is
+    // loaded from a clamped (always valid) address and replaced by 0 when it
+    // lies outside A or B, so the code stays branch-free.
+    auto gload = [&](auto path, int t, int set, auto head) __attribute__((always_inline)) {
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
         if constexpr (!decltype(path)::slow) {
-            const float* pa = a_tile + (TA ? (size_t)kt * DK : (size_t)kt * DK * lda);
-            const float* pb = b_tile + (TB ? (size_t)kt * DK * ldb : (size_t)kt * DK);
+            const int64_t kb = (int64_t)kt * DK - (int64_t)kshift;
+            const float* pa = a_tile + (TA ? kb : kb * (int64_t)lda);
+            const float* pb = b_tile + (TB ? kb * (int64_t)ldb : kb);
 #pragma unroll
-            for (int i = 0; i < G::LA; ++i)
-                if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS)
-                    ra[set][i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+            for (int i = 0; i < G::LA; ++i) {
+                const int ch = tid + i * NT;
+                if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
+                    if constexpr (decltype(head)::on) {
+                        // k inside the tile: c1 (A), or 4 * c0 (A^T, float4 along k)
+                        const int kk = TA ? (ch % A_C0) * 4 : ch / A_C0;
+                        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+                        ra[set][i] = v;
+                    } else {
+                        ra[set][i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+                    }
+                }
+            }
 #pragma unroll
-            for (int i = 0; i < G::LB; ++i)
-                if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS)
-                    rb[set][i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+            for (int i = 0; i < G::LB; ++i) {
+                const int ch = tid + i * NT;
+                if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
+                    if constexpr (decltype(head)::on) {
+                        // k inside the tile: 4 * c0 (B, float4 along k), or c1 (B^T)
+                        const int kk = TB ? ch / B_C0 : (ch % B_C0) * 4;
+                        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+                        rb[set][i] = v;
+                    } else {
+                        rb[set][i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+                    }
+                }
+            }
         } else {
             const uint32_t k0 = (uint32_t)kt * DK;
 #pragma unroll
@@ -577,14 +617,15 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     #pragma unroll
         for (int s = 0; s < NBUF - 1; ++s) {
             if (s < ktiles) {
-                gload(path, s, 0);
+                if (s == 0 && kshift != 0u) gload(path, 0, 0, Head{});
+                else gload(path, s, 0, NoHead{});
                 swrite(s, 0);
             }
         }
         // tiles NBUF - 1 .. NBUF + PD - 2 go to the register sets
     #pragma unroll
         for (int j = 0; j < PD; ++j)
-            if (NBUF - 1 + j < ktiles) gload(path, NBUF - 1 + j, (NBUF - 1 + j) % PD);
+            if (NBUF - 1 + j < ktiles) gload(path, NBUF - 1 + j, (NBUF - 1 + j) % PD, NoHead{});
         __syncthreads();
 
         if constexpr (SG_PLR >= 2) {
@@ -620,7 +661,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                             mfma_frag(cur);
                             if (kb == 0) {
                                 swrite((u + NBUF - 1) % NBUF, set);
-                                gload(path, min(t + NBUF - 1 + PD, ktiles - 1), set);
+                                gload(path, min(t + NBUF - 1 + PD, ktiles - 1), set, NoHead{});
                             }
                             if constexpr (SG_PLR >= 3) {
                                 constexpr int NMFMA = KPL * WT0 * WT1;
@@ -645,14 +686,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                     if (t < ktiles) {
                         compute(u);
                         if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF, 0);
-                        if (t + NBUF < ktiles) gload(path, t + NBUF, 0);
+                        if (t + NBUF < ktiles) gload(path, t + NBUF, 0, NoHead{});
                         __syncthreads();
                     }
                 }
             }
         }
     };
-    if (slow_mn || kt_partial >= 0) kloop(SlowPath{});
+    if (slow_mn || slow_k) kloop(SlowPath{});
     else kloop(FastPath{});
 
     if constexpr (SPLIT) {

@@ -859,6 +859,7 @@ _vop_carry("v_addc_co_u32", lambda a, b, c: (a + b + c, (a + b + c) > MASK32))
 _vop_carry("v_sub_co_u32", lambda a, b, c: (a - b, b > a))
 _vop_carry("v_subrev_co_u32", lambda a, b, c: (b - a, a > b))
 _vop_carry("v_subb_co_u32", lambda a, b, c: (a - b - c, (b + c) > a))
+_vop_carry("v_subbrev_co_u32", lambda a, b, c: (b - a - c, (a + c) > b))
 _vop("v_mul_f32", lambda a, b: _u32(_f32(a) * _f32(b)))
 _vop("v_add_f32", lambda a, b: _u32(_f32(a) + _f32(b)))
 _vop("v_sub_f32", lambda a, b: _u32(_f32(a) - _f32(b)))

@@ -265,6 +265,33 @@ def test_edge_shapes_stay_inside_every_buffer(name, m, n, k, pad):
     assert np.all(D[m:, :] == 0), "rows past m of D were written"
 
 
+HEAD_CASES = [  # whole, aligned tiles with k % DK != 0 and k % 4 == 0 (instances without a K rotation)
+    ("mt32x32_a32_wg1x1_dk16", 64, 32, 20), ("mt64x64_a16_wg2x2_dk32_s3", 128, 64, 36),
+    ("mt64x64_a16_wg2x2_dk8", 128, 64, 12), ("mt16x16_a16_wg1x1_dk16_s3", 32, 16, 52),
+    ("mt32x32_a32_wg1x1_dk16_s2_pd2", 64, 32, 36),
+    ("mt64x64_a16_wg2x2_dk32_s3_tn", 64, 64, 36), ("mt32x32_a32_wg1x1_dk16_tt", 32, 64, 20),
+]
+
+
+@pytest.mark.parametrize("name,m,n,k", HEAD_CASES)
+def test_k_remainder_keeps_the_vector_path(name, m, n, k):
+    """A K remainder moves the K origin back so that the first K tile is the
+    partial one, loaded with its missing values as zeros: parity against f64
+    with every buffer guarded, and about as many instructions as the same
+    launch with K rounded up to whole tiles (the element-wise path would run
+    several times as many)."""
+    prog, cfg = program(name)
+    dk = cfg.depth_k
+    assert k % dk and k % 4 == 0 and k > dk
+    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 7)
+    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m)
+    assert oracle.normwise_error(D, oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+    kr = -(-k // dk) * dk
+    A2, B2, C2, _, _ = _split_operands(cfg, m, n, kr, 7)
+    _, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A2, B2, C2, 0.5, 1.5, mnk=(m, n, kr), ldd=m)
+    assert info["instructions"] <= 1.1 * info2["instructions"], (info["instructions"], info2["instructions"])
+
+
 @pytest.mark.parametrize("name", ["mt32x32_a32_wg1x1_dk16_tt", "mt16x16_a16_wg1x1_dk16_nt",
                                   "mt64x64_a16_wg2x2_dk32_s3_tn"])
 @pytest.mark.parametrize("shape,pad", [((None, None, None), 0), ((35, 59, 33), 1), ((5, 3, 1), 0)])
@@ -412,6 +439,27 @@ def test_scalar_alu_wraps_and_sets_scc():
     vm.run("generated_gemm:\n s_add_u32 s3, s1, s2\n s_addc_u32 s4, 0, 0\n s_mul_hi_u32 s5, s1, s1\n"
            " s_endpgm\n")
     assert vm.s[3] == 1 and vm.s[4] == 1 and vm.s[5] == 0xFFFFFFFE
+
+
+def test_vector_64bit_subtract_chains():
+    """x - y and y - x on 64-bit lanes through the borrow ops the compiler
+    chains (v_sub_co/v_subb_co and v_subrev_co/v_subbrev_co), against Python
+    integers modulo 2^64."""
+    rng = np.random.default_rng(11)
+    x = [int(v) for v in rng.integers(0, 2 ** 64, 64, dtype=np.uint64)]
+    y = [int(v) for v in rng.integers(0, 2 ** 64, 64, dtype=np.uint64)]
+    y[:4] = [x[0], x[1] + 1 & (2 ** 64 - 1), 0, 2 ** 64 - 1]  # equal, off by one, extremes
+    vm = GcnVirtualMachine(104, 256, 64)
+    for reg, vals in ((0, x), (2, y)):
+        vm.v[reg] = np.array([v & 0xFFFFFFFF for v in vals], dtype=np.uint32)
+        vm.v[reg + 1] = np.array([v >> 32 for v in vals], dtype=np.uint32)
+    vm.run("generated_gemm:\n v_sub_co_u32_e32 v4, vcc, v0, v2\n v_subb_co_u32_e32 v5, vcc, v1, v3, vcc\n"
+           " v_subrev_co_u32_e32 v6, vcc, v0, v2\n v_subbrev_co_u32_e32 v7, vcc, v1, v3, vcc\n s_endpgm\n")
+    got_xy = [int(lo) | int(hi) << 32 for lo, hi in zip(vm.v[4], vm.v[5])]
+    got_yx = [int(lo) | int(hi) << 32 for lo, hi in zip(vm.v[6], vm.v[7])]
+    assert got_xy == [(a - b) % 2 ** 64 for a, b in zip(x, y)]
+    assert got_yx == [(b - a) % 2 ** 64 for a, b in zip(x, y)]
+    assert vm.vcc == sum(1 << i for i, (a, b) in enumerate(zip(x, y)) if a > b)  # borrow of y - x
 
 
 def test_integer_division_sequence_of_the_compiler():
