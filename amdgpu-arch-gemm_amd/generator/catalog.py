@@ -39,6 +39,10 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     # problem's tiles cannot fill the GPU (not for 256 x 256 tiles, whose
     # 256 accumulators per lane leave no registers for the split epilogue)
     "mt256x256_a32_wg2x2_dk16_s3": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    # a 24-deep K tile: three 53 KB LDS buffers (159,744 B of the 160 KiB) and a
+    # third fewer barriers per launch than depth 16; 4096 = 170 * 24 + 16, so
+    # the first K tile is the partial one (shifted K origin)
+    "mt256x256_a32_wg2x2_dk24_s3": (_cfg(MFMA_32x32x2, (2, 2), (4, 4), 24, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     "mt64x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (2, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8, sk=0)),
     "mt128x64_a16_wg2x2_dk16_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=2), _opt(wgm=4, plr=1, xcd=8)),
     "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8, sk=0)),
@@ -102,7 +106,7 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 
 # shape class -> preferred instance (filled from tuner results; see select())
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
-    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk16_s3"),
+    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk24_s3"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
     ((8192, 8192, 256), "mt128x64_a16_wg2x2_dk16_s2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
@@ -127,10 +131,21 @@ def build_all(kernel_dir: str = KERNEL_DIR, names: Optional[List[str]] = None, j
     return names
 
 
+def vector_k(name: str, k: int) -> bool:
+    """True when every K tile of a k-deep problem takes the vector path: whole
+    K tiles, or a remainder with k % 4 == 0 and at least two K tiles on an
+    instance without a K rotation (the kernel then shifts the K origin so the
+    first tile is the partial one)."""
+    cfg, opt = SOLUTIONS[name]
+    dk = cfg.depth_k
+    return k % dk == 0 or (k % 4 == 0 and k > dk and opt.map_k_idx <= 1)
+
+
 def divides(name: str, m: int, n: int, k: int) -> bool:
+    """Whole tiles in M and N and a K the vector path covers."""
     cfg, _ = SOLUTIONS[name]
     t0, t1 = cfg.tile_size
-    return m % t0 == 0 and n % t1 == 0 and k % cfg.depth_k == 0
+    return m % t0 == 0 and n % t1 == 0 and vector_k(name, k)
 
 
 def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> int:
@@ -176,7 +191,7 @@ def select(m: int, n: int, k: int) -> str:
         fill = (m * n) / (tx * t0 * ty * t1)
         splits = auto_split(name, m, n, k)
         key = (min(tx * ty * splits, GFX950_COMPUTE_UNITS), splits == 1, round(fill, 1), t0 * t1,
-               k % cfg.depth_k == 0)
+               vector_k(name, k))
         if best is None or key > best[0]:
             best = (key, name)
     return best[1]

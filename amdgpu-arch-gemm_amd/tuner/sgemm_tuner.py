@@ -12,7 +12,7 @@ stdout line) and print the best.  Additions:
 
 * ``--space gfx950`` (default): macro-tile {64,128,256}^2 x wave-group
   {2x2, 4x1} x MFMA atom {32x32x2, 16x16x4} (stage 1), then the code-shape
-  knobs depth_k {16,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
+  knobs depth_k {16,24,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
   x prefetch depth {1,2}
   on the best ``--refine`` geometries (stage 2), optionally crossed with
   ``--split-k`` (split-K kernel; 0 = split count chosen per problem) and
@@ -75,7 +75,7 @@ GFX950_WAVE_GROUPS = [(2, 2), (4, 1)]
 # --space gfx950-wide: also 32-wide tiles and every wave group of the reference
 GFX950_WIDE_MACRO_TILES = [(a, b) for a in (32, 64, 128, 256) for b in (32, 64, 128, 256)]
 GFX950_WIDE_WAVE_GROUPS = SUPPORTED_WAVE_GROUPS + [(4, 1), (1, 4)]
-GFX950_DEPTH_K = [16, 32]
+GFX950_DEPTH_K = [16, 24, 32]
 GFX950_VMEM_STAGES = [1, 2]
 GFX950_WGM = [1, 4, 8]
 GFX950_XCD = [0, 8]

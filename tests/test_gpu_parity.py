@@ -163,6 +163,11 @@ EDGE_SHAPES = [
     # (instance, m, n, k, pad): edge tiles in M and N, K remainders, k < DK, odd leading dims
     ("mt256x256_a32_wg2x2_dk16_s3", 1000, 999, 1001, 0),
     ("mt256x256_a32_wg2x2_dk16_s3", 257, 255, 17, 1),
+    ("mt256x256_a32_wg2x2_dk24_s3", 1000, 999, 1001, 0),
+    # whole, aligned tiles with a K remainder: the vector path with a shifted K origin
+    ("mt256x256_a32_wg2x2_dk24_s3", 512, 768, 4100, 0),
+    ("mt256x256_a32_wg2x2_dk24_s3", 512, 512, 44, 4),
+    ("mt128x64_a16_wg2x2_dk32_s3", 16384, 128, 1000, 0),
     ("mt64x64_a16_wg2x2_dk32_s3", 1023, 1025, 1027, 0),
     ("mt64x64_a16_wg2x2_dk32_s3", 5, 3, 1, 1),
     ("mt128x64_a16_wg2x2_dk16_s3", 8190, 130, 250, 0),
