@@ -108,7 +108,7 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk24_s3"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
-    ((8192, 8192, 256), "mt128x64_a16_wg2x2_dk16_s2"),
+    ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
 ]
 

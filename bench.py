@@ -7,7 +7,9 @@ A step is one launch of the tuned gfx950 kernel on the BASELINE.json config
 beta = 0) with A, B and D resident in HBM.  W untimed launches, then K timed
 launches bracketed by device synchronisation; the host clock gives
 ms_per_step and `value` (TFLOP/s), HIP events on the kernel's stream give the
-per-launch kernel time used for the roofline fraction.
+per-launch kernel time used for the roofline fraction.  W defaults to at least
+10 launches and at least 0.25 s of them: the engine clock ramps up over
+milliseconds of load, which is all of a short workload's 10 launches.
 
 The CPU baseline is the reference's own cpuGemm (compiled from its source into
 oracle/_ref) -- or this project's C restatement of it when that was not built --
@@ -109,7 +111,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed launches before the timed ones (default: at least 10 and at least "
+                         "0.25 s of launches, so the engine clock has left its idle state)")
     ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--kernel", default=None, help="catalog instance (default: catalog.select)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -141,9 +145,21 @@ def main():
     dD = S.DeviceBuffer(m * n * 4)
     dD.zero()
 
-    for _ in range(args.warmup):
-        kern.launch(dA, dB, None, dD, m, n, k, 1.0, 0.0)
-    kern.synchronize()
+    if args.warmup is not None:
+        warmup = args.warmup
+        for _ in range(warmup):
+            kern.launch(dA, dB, None, dD, m, n, k, 1.0, 0.0)
+        kern.synchronize()
+    else:
+        # the engine clock ramps up over milliseconds of load: keep launching
+        # until 0.25 s have passed (and at least 10 launches)
+        warmup, t_w = 0, time.perf_counter()
+        while warmup < 10 or time.perf_counter() - t_w < 0.25:
+            for _ in range(10):
+                kern.launch(dA, dB, None, dD, m, n, k, 1.0, 0.0)
+            warmup += 10
+            kern.synchronize()
+    log(f"warmup: {warmup} launches")
 
     # timed region: exactly `steps` launches, device idle on both sides
     t0 = time.perf_counter()
@@ -172,7 +188,7 @@ def main():
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
