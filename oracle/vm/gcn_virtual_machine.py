@@ -686,6 +686,15 @@ def _s_and_saveexec(vm, ins, prog):
     vm.scc = int(vm.exec != 0)
 
 
+@op("s_or_saveexec_b64")
+def _s_or_saveexec(vm, ins, prog):
+    # the source is read before the destination (often the same pair) is written
+    old = vm.exec
+    vm.exec = (vm.rs64(ins.ops[1]) | old) & MASK64
+    vm.ws64(ins.ops[0], old)
+    vm.scc = int(vm.exec != 0)
+
+
 def _scmp(name, fn, signed=False):
     @op(name)
     def _impl(vm, ins, prog):
@@ -790,19 +799,32 @@ for _nd, _name in ((1, "s_load_dword"), (2, "s_load_dwordx2"), (4, "s_load_dword
 
 
 # vector ALU -------------------------------------------------------------
-def _vop(name, fn, nsrc=2):
+def _vop(name, fn, nsrc=2, clamped=None):
+    """VOP1/2/3 op without carry.  ``clamped`` (optional) computes the exact
+    result as int64 for the VOP3 ``clamp`` modifier, which saturates an
+    unsigned integer result to [0, 2^32 - 1]; any other op with ``clamp``, or
+    an op with another modifier, is not modelled and fails loudly."""
     def _impl(vm, ins, prog):
         srcs = [vm.rv32(o) for o in ins.ops[1:1 + nsrc]]
-        vm.wv32(ins.ops[0], fn(*srcs))
+        unknown = set(ins.mods) - {"clamp"}
+        if unknown:
+            raise NotImplementedError(f"modifiers {sorted(unknown)} of {ins}")
+        if "clamp" in ins.mods:
+            if clamped is None:
+                raise NotImplementedError(f"clamp modifier of {ins}")
+            vm.wv32(ins.ops[0], np.clip(clamped(*srcs), 0, MASK32).astype(np.uint32))
+        else:
+            vm.wv32(ins.ops[0], fn(*srcs))
     for suffix in ("", "_e32", "_e64"):
         _DISPATCH[name + suffix] = _impl
 
 
 _u64 = lambda x: x.astype(np.uint64)  # noqa: E731
+_i64 = lambda x: x.astype(np.int64)  # noqa: E731
 _vop("v_mov_b32", lambda a: a, 1)
-_vop("v_add_u32", lambda a, b: (_u64(a) + _u64(b)).astype(np.uint32))
-_vop("v_sub_u32", lambda a, b: (_u64(a) - _u64(b)).astype(np.uint32))
-_vop("v_subrev_u32", lambda a, b: (_u64(b) - _u64(a)).astype(np.uint32))
+_vop("v_add_u32", lambda a, b: (_u64(a) + _u64(b)).astype(np.uint32), clamped=lambda a, b: _i64(a) + _i64(b))
+_vop("v_sub_u32", lambda a, b: (_u64(a) - _u64(b)).astype(np.uint32), clamped=lambda a, b: _i64(a) - _i64(b))
+_vop("v_subrev_u32", lambda a, b: (_u64(b) - _u64(a)).astype(np.uint32), clamped=lambda a, b: _i64(b) - _i64(a))
 _vop("v_and_b32", lambda a, b: a & b)
 _vop("v_or_b32", lambda a, b: a | b)
 _vop("v_xor_b32", lambda a, b: a ^ b)

@@ -462,6 +462,29 @@ def test_vector_64bit_subtract_chains():
     assert vm.vcc == sum(1 << i for i, (a, b) in enumerate(zip(x, y)) if a > b)  # borrow of y - x
 
 
+def test_integer_clamp_saturates_and_saveexec_or():
+    """VOP3 clamp on unsigned add/sub saturates to [0, 2^32 - 1] (the
+    compiler uses it for max(a - b, 0)); without it the result wraps.
+    s_or_saveexec_b64 reads its source before writing the old EXEC there.
+    A modifier the VM does not model fails loudly."""
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.v[0] = np.array([5, 3, 0, 0xFFFFFFF0] * 16, dtype=np.uint32)
+    vm.v[1] = np.array([3, 5, 1, 0x20] * 16, dtype=np.uint32)
+    vm.exec = 0x00000000FFFF0000
+    vm.s[4], vm.s[5] = 0x0000FFFF, 0x0
+    vm.run("generated_gemm:\n v_sub_u32_e64 v2, v0, v1 clamp\n v_sub_u32_e64 v3, v0, v1\n"
+           " v_add_u32_e64 v4, v0, v1 clamp\n v_subrev_u32_e64 v5, v0, v1 clamp\n"
+           " s_or_saveexec_b64 s[4:5], s[4:5]\n s_endpgm\n")
+    lanes = range(16, 32)  # lanes live under the starting EXEC
+    assert [int(vm.v[2][i]) for i in lanes] == [2, 0, 0, 0xFFFFFFD0] * 4
+    assert [int(vm.v[3][i]) for i in lanes] == [2, 0xFFFFFFFE, 0xFFFFFFFF, 0xFFFFFFD0] * 4
+    assert [int(vm.v[4][i]) for i in lanes] == [8, 8, 1, 0xFFFFFFFF] * 4
+    assert [int(vm.v[5][i]) for i in lanes] == [0, 2, 1, 0] * 4
+    assert vm.exec == 0x00000000FFFFFFFF and (vm.s[4], vm.s[5]) == (0xFFFF0000, 0)
+    with pytest.raises(NotImplementedError):
+        GcnVirtualMachine(104, 256, 64).run("generated_gemm:\n v_add_u32_e64 v2, v0, v1 mul:2\n s_endpgm\n")
+
+
 def test_integer_division_sequence_of_the_compiler():
     # the kernel's tile order divides by runtime values with v_rcp_iflag_f32 and
     # correction steps: check the emitted sequence over many numerators
