@@ -330,7 +330,9 @@ int sgemm_device_info(char* name, size_t name_len, int* compute_units, int* cloc
     hipDeviceProp_t p;
     HIP_TRY(hipGetDeviceProperties(&p, 0));
     if (name && name_len) {
-        snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+        // some drivers report an empty marketing name: fall back to the ISA name alone
+        if (p.name[0]) snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+        else snprintf(name, name_len, "%s, %d CUs", p.gcnArchName, p.multiProcessorCount);
     }
     if (compute_units) *compute_units = p.multiProcessorCount;
     if (clock_khz) *clock_khz = p.clockRate;
