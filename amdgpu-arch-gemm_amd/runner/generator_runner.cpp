@@ -111,6 +111,7 @@ int main(int argc, char** argv) {
     }
 
     std::vector<float> ref;
+    std::vector<double> ref64;
     if (validate) {
         ref.assign((size_t)m * n, 0.0f);
         // The stored A is k x m and B is n x k for transposed kernels; the CPU
@@ -136,6 +137,8 @@ int main(int argc, char** argv) {
         const auto t1 = std::chrono::steady_clock::now();
         std::cout << "cpuGemm func: " << std::chrono::duration<double, std::milli>(t1 - t0).count() << " ms ("
                   << threads << " threads of " << std::thread::hardware_concurrency() << ")\n";
+        ref64.assign((size_t)m * n, 0.0);
+        runner_gemm_f64(pa, pb, C.data(), ref64.data(), alpha, beta, m, n, k, threads);
     }
 
     double ms = 0.0;
@@ -165,6 +168,9 @@ int main(int argc, char** argv) {
         std::cout << "max |D - D_ref| = " << max_err << " at index " << worst << " (gpu " << D[worst] << ", cpu "
                   << ref[worst] << ")\n"
                   << "normwise relative error = " << rel << " (tolerance 1e-5*sqrt(K) = " << tol << ")\n"
+                  << "float64 reference: normwise error of the GPU result "
+                  << runner_normwise_error(D.data(), ref64.data(), D.size()) << ", of cpuGemm "
+                  << runner_normwise_error(ref.data(), ref64.data(), ref.size()) << "\n"
                   << "# of mismatches: " << (pass ? 0 : 1) << "/1 (normwise)\n"
                   << "validation: " << (pass ? "PASS" : "FAIL") << "\n";
         status = pass ? 0 : -1;

@@ -458,6 +458,13 @@ def test_generator_runner_validates(kernels):
     lines = out.split("\n")
     assert lines[-3].startswith("Gflops: ")  # what sgemm_tuner.py:115 parses
     assert float(lines[-3].split(":")[-1]) > 0
+    # both the GPU result and the float cpuGemm are measured against a float64 GEMM
+    f64 = [ln for ln in lines if ln.startswith("float64 reference:")]
+    assert len(f64) == 1, out
+    gpu_err = float(f64[0].split("GPU result ")[1].split(",")[0])
+    cpu_err = float(f64[0].split("of cpuGemm ")[1])
+    tol = 1e-5 * 1024 ** 0.5
+    assert 0 < gpu_err <= tol and 0 < cpu_err <= tol, f64[0]
 
 
 def test_generator_runner_odd_shape_validates(kernels):
