@@ -423,6 +423,11 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
     const uint64_t wgy = ((uint64_t)n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n;
     if (wgx > 0x7fffffffull || wgy > 65535ull || wgx * wgy > 0x7fffffffull)
         return fail(SGEMM_E_SHAPE, "grid %llux%llu too large", (unsigned long long)wgx, (unsigned long long)wgy);
+    // row, column and k indices inside the kernel are 32-bit signed: the tile
+    // grid padded to whole tiles, and k plus one K tile, stay below 2^31
+    if (wgx * (uint32_t)i.tile_m > 0x7fffffffull || wgy * (uint32_t)i.tile_n > 0x7fffffffull ||
+        (uint64_t)k + (uint32_t)i.depth_k > 0x7fffffffull)
+        return fail(SGEMM_E_SHAPE, "m=%u n=%u k=%u: padded to whole tiles they must stay below 2^31", m, n, k);
     // per-thread offsets inside one K tile are 32-bit: lda * depth_k and
     // ldb * tile_n must stay below 2^32 elements
     const uint64_t a_span = (uint64_t)lda * (uint32_t)(i.trans_a ? i.tile_m : i.depth_k);

@@ -157,6 +157,12 @@ def test_bad_leading_dimension_is_an_error_not_a_launch(kernels):
             kern.launch(d, d, None, d, 256, 256, 16, alpha=1.0, beta=0.0, lda=255)
         with pytest.raises(S.SgemmError, match="leading dimensions too small"):
             kern.launch(d, d, None, d, 256, 256, 16, alpha=1.0, beta=0.0, ldb=15)
+        # 32-bit signed row / column / k indices in the kernel: the host rejects
+        # shapes whose padded tile grid reaches 2^31, before any launch
+        big = (1 << 31) - 100
+        for m, n, k in ((big, 1, 1), (1, big, 1), (1, 1, big)):
+            msg = kern.check_shape(m, n, k, lda=max(m, k), ldb=max(k, n), ldc=m, ldd=m)
+            assert msg and ("below 2^31" in msg or "too large" in msg), (m, n, k, msg)
 
 
 EDGE_SHAPES = [
