@@ -39,7 +39,7 @@ import shutil
 import subprocess
 import sys
 import time
-from concurrent.futures import ThreadPoolExecutor
+from concurrent.futures import ThreadPoolExecutor, as_completed
 from itertools import product
 from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
@@ -179,9 +179,17 @@ def build_point(out: str, p: Point) -> Tuple[str, int]:
 
 
 def build_points(out: str, points: List[Point], jobs: int) -> Dict[str, int]:
+    """Compiles the candidates in parallel; prints a progress line every 16."""
     os.makedirs(point_dir(out), exist_ok=True)
+    res: Dict[str, int] = {}
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        return dict(ex.map(lambda p: build_point(out, p), points))
+        futures = [ex.submit(build_point, out, p) for p in points]
+        for i, f in enumerate(as_completed(futures), 1):
+            key, rc = f.result()
+            res[key] = rc
+            if i % 16 == 0 or i == len(futures):
+                print(f"compiled {i}/{len(futures)} candidates", flush=True)
+    return res
 
 
 def spills(out: str, key: str) -> bool:
