@@ -26,7 +26,7 @@
 // checks that lda >= m, ldb >= k, ldc >= m, ldd >= m before every launch.
 //
 // Data path per K tile of depth DK:
-//   HBM --global_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
+//   HBM --buffer_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
 //   LDS --ds_read_b{32,64,128}--> VGPR --v_mfma_f32_{32x32x2,16x16x4}_f32--> accumulators
 // and after the K loop accumulators --(alpha)--> LDS column chunk --(beta * C)-->
 // global_store_dwordx4 down whole columns of D.
@@ -396,7 +396,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const uint32_t kshift = (k % DK) ? DK - k % DK : 0u;
     const bool slow_k = kshift != 0u && (SG_MAPK > 1 || (k & 3u) != 0u || ktiles < 2);
 
-    // ---- global -> VGPR staging (element offsets inside a K tile, 64-bit bases) ----
+    // ---- global -> VGPR staging (byte offsets inside a K tile) ----
     // Every thread moves float4 chunks.  A chunk runs along the operand's
     // contiguous dimension: m for A (NN) or k for A^T, k for B (NN) or n for
     // B^T.  Chunks along the LDS row direction are written with one
@@ -409,17 +409,17 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // element (row, kk) of op(A) is a[row + kk*lda] (NN) or a[kk + row*lda] (T)
     const float* a_tile = TA ? a + (size_t)row0 * lda : a + row0;
     const float* b_tile = TB ? b + col0 : b + (size_t)col0 * ldb;
-    uint32_t a_off[G::LA], b_off[G::LB];
+    uint32_t a_off[G::LA], b_off[G::LB];  // bytes from the K tile's first element
     int a_lds[G::LA], b_lds[G::LB];
 #pragma unroll
     for (int i = 0; i < G::LA; ++i) {
         const int ch = tid + i * NT;
         const int c0 = ch % A_C0, c1 = ch / A_C0;
         if constexpr (!TA) {  // c0: m / 4, c1: k
-            a_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * lda;
+            a_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * lda) * 4u;
             a_lds[i] = c1 * G::A_LD + c0 * 4;
         } else {              // c0: k / 4, c1: m
-            a_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * lda;
+            a_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * lda) * 4u;
             a_lds[i] = (c0 * 4) * G::A_LD + c1;
         }
     }
@@ -428,13 +428,19 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         const int ch = tid + i * NT;
         const int c0 = ch % B_C0, c1 = ch / B_C0;
         if constexpr (!TB) {  // c0: k / 4, c1: n
-            b_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * ldb;
+            b_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * ldb) * 4u;
             b_lds[i] = G::A_STAGE + c1 * G::B_LD + c0 * 4;
         } else {              // c0: n / 4, c1: k
-            b_off[i] = (uint32_t)(c0 * 4) + (uint32_t)c1 * ldb;
+            b_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * ldb) * 4u;
             b_lds[i] = G::A_STAGE + (c0 * 4) * G::B_LD + c1;
         }
     }
+    // Bytes one K tile of each operand spans from its first element: DK
+    // columns of A (or MT0 rows of A^T) and MT1 columns of B (or DK rows of
+    // B^T).  The host keeps them below 2^31, so the byte offsets above fit
+    // 32 bits; they are the buffer descriptors' num_records.
+    const uint32_t a_bytes = ((TA ? (uint32_t)(MT0 - 1) : (uint32_t)(DK - 1)) * lda + (uint32_t)(TA ? DK : MT0)) * 4u;
+    const uint32_t b_bytes = ((TB ? (uint32_t)(DK - 1) : (uint32_t)(MT1 - 1)) * ldb + (uint32_t)(TB ? MT1 : DK)) * 4u;
     // PD register staging sets: with the early-refill schedules a K tile's
     // global loads are issued PD tiles before its LDS writes.
     constexpr int PD = (SG_PLR >= 2) ? SG_PD : 1;
@@ -445,8 +451,12 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
 
     // gload(tag, t, set, head): global -> VGPR copy of K tile t.  On the fast
-    // path a Head tag (tile 0 of a shifted K origin) loads only the chunks at
-    // k >= kshift and zeros the rest.  With a SlowPath tag every element is
+    // path every chunk is one buffer_load_dwordx4: a wave-uniform descriptor
+    // per operand and K tile (scalar arithmetic only; num_records is the K
+    // tile's footprint) and the chunk's 32-bit byte offset -- no 64-bit vector
+    // address per load.  A Head tag (tile 0 of a shifted K origin) loads only
+    // the chunks at k >= kshift, with flat loads, and zeros the rest.  With a
+    // SlowPath tag every element is
     // loaded from a clamped (always valid) address and replaced by 0 when it
     // lies outside A or B, so the code stays branch-free.
     auto gload = [&](auto path, int t, int set, auto head) __attribute__((always_inline)) {
@@ -456,6 +466,12 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             const int64_t kb = (int64_t)kt * DK - (int64_t)kshift;
             const float* pa = a_tile + (TA ? kb : kb * (int64_t)lda);
             const float* pb = b_tile + (TB ? kb * (int64_t)ldb : kb);
+            const __amdgpu_buffer_rsrc_t rsa =
+                __builtin_amdgcn_make_buffer_rsrc((void*)pa, (short)0, (int)a_bytes, BUFFER_RSRC_WORD3);
+            const __amdgpu_buffer_rsrc_t rsb =
+                __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, (int)b_bytes, BUFFER_RSRC_WORD3);
+            const char* ca = reinterpret_cast<const char*>(pa);
+            const char* cb = reinterpret_cast<const char*>(pb);
 #pragma unroll
             for (int i = 0; i < G::LA; ++i) {
                 const int ch = tid + i * NT;
@@ -464,10 +480,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         // k inside the tile: c1 (A), or 4 * c0 (A^T, float4 along k)
                         const int kk = TA ? (ch % A_C0) * 4 : ch / A_C0;
                         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(ca + a_off[i]);
                         ra[set][i] = v;
                     } else {
-                        ra[set][i] = *reinterpret_cast<const f32x4*>(pa + a_off[i]);
+                        ra[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)a_off[i], 0, 0));
                     }
                 }
             }
@@ -479,10 +495,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         // k inside the tile: 4 * c0 (B, float4 along k), or c1 (B^T)
                         const int kk = TB ? ch / B_C0 : (ch % B_C0) * 4;
                         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(cb + b_off[i]);
                         rb[set][i] = v;
                     } else {
-                        rb[set][i] = *reinterpret_cast<const f32x4*>(pb + b_off[i]);
+                        rb[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)b_off[i], 0, 0));
                     }
                 }
             }

@@ -428,12 +428,15 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
     if (wgx * (uint32_t)i.tile_m > 0x7fffffffull || wgy * (uint32_t)i.tile_n > 0x7fffffffull ||
         (uint64_t)k + (uint32_t)i.depth_k > 0x7fffffffull)
         return fail(SGEMM_E_SHAPE, "m=%u n=%u k=%u: padded to whole tiles they must stay below 2^31", m, n, k);
-    // per-thread offsets inside one K tile are 32-bit: lda * depth_k and
-    // ldb * tile_n must stay below 2^32 elements
-    const uint64_t a_span = (uint64_t)lda * (uint32_t)(i.trans_a ? i.tile_m : i.depth_k);
-    const uint64_t b_span = (uint64_t)ldb * (uint32_t)(i.trans_b ? i.depth_k : i.tile_n);
-    if (a_span >= (1ull << 32) || b_span >= (1ull << 32))
-        return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets: lda=%u ldb=%u", lda, ldb);
+    // the kernel addresses one K tile of each operand through a buffer
+    // descriptor with 32-bit byte offsets: lda * depth_k (tile_m for A^T) and
+    // ldb * tile_n (depth_k for B^T) floats must stay below 2^31 bytes
+    const uint64_t a_span = (uint64_t)lda * (uint32_t)(i.trans_a ? i.tile_m : i.depth_k) * 4u;
+    const uint64_t b_span = (uint64_t)ldb * (uint32_t)(i.trans_b ? i.depth_k : i.tile_n) * 4u;
+    if (a_span >= (1ull << 31) || b_span >= (1ull << 31))
+        return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets (a K tile spans %llu / %llu "
+                    "bytes of A / B, limit 2^31): lda=%u ldb=%u", (unsigned long long)a_span,
+                    (unsigned long long)b_span, lda, ldb);
     return SGEMM_OK;
 }
 

@@ -1096,12 +1096,18 @@ _DISPATCH["v_mfma_f32_16x16x4_f32"] = _DISPATCH["v_mfma_f32_16x16x4f32"] = _mfma
 
 # global memory -------------------------------------------------------------
 def _global_addr(vm, ins, vaddr_op, saddr_op):
-    off = _sext(ins.mods.get("offset", 0), 32)
+    """Per-lane 64-bit address: vaddr (64-bit), or saddr (64-bit SGPR pair) plus
+    the zero-extended 32-bit vaddr, plus the signed instruction offset, all
+    modulo 2^64 as in the hardware.  A base outside the memory (a K tile's base
+    before the matrix, say) is fine as long as the active lanes' sums land
+    inside; the memory's range check judges those."""
+    off = np.uint64(_sext(ins.mods.get("offset", 0), 32) & MASK64)
     if saddr_op is None or saddr_op.kind == "off":
-        addr = vm.rv64(vaddr_op).astype(np.int64)
+        addr = vm.rv64(vaddr_op).astype(np.uint64)
     else:
-        addr = np.int64(vm.rs64(saddr_op)) + vm.rv32(vaddr_op).astype(np.int64)
-    return addr + off
+        addr = np.uint64(vm.rs64(saddr_op) & MASK64) + vm.rv32(vaddr_op).astype(np.uint64)
+    with np.errstate(over="ignore"):
+        return (addr + off).astype(np.uint64)
 
 
 def _global_load(nd):

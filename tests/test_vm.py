@@ -485,6 +485,24 @@ def test_integer_clamp_saturates_and_saveexec_or():
         GcnVirtualMachine(104, 256, 64).run("generated_gemm:\n v_add_u32_e64 v2, v0, v1 mul:2\n s_endpgm\n")
 
 
+def test_global_address_wraps_like_the_hardware():
+    """saddr + zero-extended vaddr is taken modulo 2^64: a base below the memory
+    (a K tile's base before the matrix) with offsets that land inside reads
+    the right bytes; a lane whose sum stays outside is an error."""
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.vmem = V.Memory(1024, "vmem")
+    vm.vmem.write_bytes(0, np.arange(256, dtype=np.uint32).tobytes())
+    base = (1 << 64) - 64
+    vm.s[0], vm.s[1] = base & 0xFFFFFFFF, base >> 32
+    vm.v[0] = np.array([64 + 16 * (i % 8) for i in range(64)], dtype=np.uint32)  # lands at bytes 0..112
+    vm.run("generated_gemm:\n global_load_dwordx4 v[4:7], v0, s[0:1]\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    assert [int(vm.v[4][i]) for i in range(8)] == [4 * (i % 8) for i in range(8)]
+    assert [int(vm.v[7][i]) for i in range(8)] == [4 * (i % 8) + 3 for i in range(8)]
+    vm.v[0] = np.full(64, 48, dtype=np.uint32)  # base + 48 is still 16 bytes below the memory
+    with pytest.raises(MemoryError):
+        vm.run("generated_gemm:\n global_load_dwordx4 v[4:7], v0, s[0:1]\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+
+
 def test_integer_division_sequence_of_the_compiler():
     # the kernel's tile order divides by runtime values with v_rcp_iflag_f32 and
     # correction steps: check the emitted sequence over many numerators
