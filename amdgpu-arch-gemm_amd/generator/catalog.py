@@ -110,7 +110,12 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
     ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
+    # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
+    ((512, 512, 16384), "mt128x64_a16_wg2x2_dk16_s2"),
 ]
+# among launches that split K, the instance measured best for them (interleaved
+# runs at 512 x 512 x 16384: 114.5 TFLOP/s against 94.5 for the depth-32 one)
+SPLIT_INSTANCE = "mt128x64_a16_wg2x2_dk16_s2"
 
 
 def paths(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
@@ -176,8 +181,9 @@ def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_CO
 def select(m: int, n: int, k: int) -> str:
     """Instance for an (m, n, k) problem: the tuner's choice for a BASELINE
     shape, else the tuned instance that best fills the GPU -- the most
-    work-groups (tiles times K splits) up to one per CU first, then no split,
-    then the least padding at the edges, then the largest tile."""
+    work-groups (tiles times K splits) up to one per CU first, then no split
+    (and among split launches SPLIT_INSTANCE), then the least padding at the
+    edges, then the largest tile."""
     if m <= 0 or n <= 0:
         raise RuntimeError(f"empty problem {m}x{n}x{k}")
     for shape, name in PREFERRED:
@@ -190,8 +196,8 @@ def select(m: int, n: int, k: int) -> str:
         tx, ty = -(-m // t0), -(-n // t1)
         fill = (m * n) / (tx * t0 * ty * t1)
         splits = auto_split(name, m, n, k)
-        key = (min(tx * ty * splits, GFX950_COMPUTE_UNITS), splits == 1, round(fill, 1), t0 * t1,
-               vector_k(name, k))
+        key = (min(tx * ty * splits, GFX950_COMPUTE_UNITS), splits == 1, splits > 1 and name == SPLIT_INSTANCE,
+               round(fill, 1), t0 * t1, vector_k(name, k))
         if best is None or key > best[0]:
             best = (key, name)
     return best[1]
