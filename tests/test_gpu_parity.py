@@ -136,6 +136,35 @@ def test_leading_dimensions_and_offsets(kernels):
     assert np.all(Dfull[m:, :] == 7.25), "rows past m of D were written"
 
 
+def test_leading_dimension_at_the_buffer_offset_limit(kernels):
+    """K tiles load through buffer descriptors with 32-bit byte offsets: a
+    leading dimension whose K-tile footprint is just under 2^31 bytes still
+    computes the right D (the last column of each tile sits ~2 GiB past its
+    first), and one more row is rejected by the host before any launch."""
+    name = "mt256x256_a32_wg2x2_dk16_s3"   # depth 16: a tile spans 16 columns of A
+    cfg, _ = catalog.SOLUTIONS[name]
+    dk = cfg.depth_k
+    m, n, k = 256, 256, 2 * dk
+    lda = (1 << 31) // (4 * dk) - 64       # lda * dk * 4 = 2^31 - 4096 bytes
+    _say(f"large lda {lda} ({lda * k * 4 / 2**30:.2f} GiB of A)")
+    A = S.fill_matrix(m, k, 21, 0)
+    B = S.fill_matrix(k, n, 21, 1)
+    with _kernel(name) as kern:
+        assert kern.check_shape(m, n, k, lda=lda + 64) is not None   # footprint 2^31 bytes: rejected
+        dA = S.DeviceBuffer(4 * lda * k)
+        dA.zero()
+        lib = S.load_library()
+        for j in range(k):  # column j of A at float offset j * lda
+            col = np.ascontiguousarray(A[:, j])
+            S._check("sgemm_memcpy_h2d", lib.sgemm_memcpy_h2d(dA.ptr + 4 * j * lda, col.ctypes.data, col.nbytes))
+        dB, dD = S.DeviceBuffer.from_array(B), S.DeviceBuffer(m * n * 4)
+        kern.launch(dA, dB, None, dD, m, n, k, alpha=1.0, beta=0.0, lda=lda)
+        kern.synchronize()
+    D = dD.download().reshape(n, m).T
+    _check(D, oracle.cpu_gemm(A, B), k, name)
+    dA.close()
+
+
 def test_k_zero_is_beta_c(kernels):
     name = "mt64x64_a32_wg2x2_dk16"
     m, n = 128, 64
