@@ -827,7 +827,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         v.x = __builtin_fmaf(beta, cv.x, v.x); v.y = __builtin_fmaf(beta, cv.y, v.y);
                         v.z = __builtin_fmaf(beta, cv.z, v.z); v.w = __builtin_fmaf(beta, cv.w, v.w);
                     }
-                    *reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4) = v;
+                    // streaming (nt) store: D is not read again by this launch
+                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4));
                 }
                 // this group's reads are done before the next group overwrites the chunk
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
