@@ -17,8 +17,10 @@
 // numWorkgroupY = ceil(n / MT1) with MT0 = atom_m * WG0 * WT0 and
 // MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  Any m, n, k works: tiles
 // that lie wholly inside D with 16-byte aligned columns (every leading
-// dimension a multiple of 4) take the vector path, edge tiles and unaligned
-// problems load and store element by element with bounds checks.  A K
+// dimension a multiple of 4) take the vector path; so do edge tiles when m is
+// a multiple of 4 (and n, for a transposed B), with their loads past the edge
+// redirected inside the tile and their stores predicated.  Other edge tiles
+// and unaligned problems load and store element by element.  A K
 // remainder (k % 4 == 0) keeps the vector path by shifting the K origin so
 // that the first K tile is the partial one, its missing values loaded as
 // zeros; otherwise the last K tile is zero-filled on the element-wise path.
@@ -391,8 +393,16 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // (whole float4 chunks, masked), and every later tile -- including the one
     // the branch-free refill repeats past the end -- is whole and in bounds.
     // Otherwise the slow path zero-fills the last K tile.
+    //
+    // An edge tile (one reaching past m or n) stays on the fast path as well
+    // when no float4 chunk straddles the edge: m % 4 == 0, and n % 4 == 0 for
+    // B^T (whose chunks run along n).  Its chunks wholly past the edge load
+    // a chunk of the tile's first row (A) or column (B) instead -- always in
+    // bounds -- and what they bring only reaches rows or columns of D past the
+    // edge, which the epilogue does not store.
     const bool aligned = ((lda | ldb | ldc | ldd) & 3u) == 0;
-    const bool slow_mn = !aligned || row0 + MT0 > m || col0 + MT1 > n;
+    const bool edge = row0 + MT0 > m || col0 + MT1 > n;
+    const bool slow_mn = !aligned || (edge && ((m & 3u) != 0u || (TB && (n & 3u) != 0u)));
     const uint32_t kshift = (k % DK) ? DK - k % DK : 0u;
     const bool slow_k = kshift != 0u && (SG_MAPK > 1 || (k & 3u) != 0u || ktiles < 2);
 
@@ -415,11 +425,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     for (int i = 0; i < G::LA; ++i) {
         const int ch = tid + i * NT;
         const int c0 = ch % A_C0, c1 = ch / A_C0;
+        // a chunk of rows wholly past m reads the tile's first row instead
         if constexpr (!TA) {  // c0: m / 4, c1: k
-            a_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * lda) * 4u;
+            const uint32_t r = row0 + (uint32_t)(c0 * 4) < m ? (uint32_t)(c0 * 4) : 0u;
+            a_off[i] = (r + (uint32_t)c1 * lda) * 4u;
             a_lds[i] = c1 * G::A_LD + c0 * 4;
         } else {              // c0: k / 4, c1: m
-            a_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * lda) * 4u;
+            const uint32_t r = row0 + (uint32_t)c1 < m ? (uint32_t)c1 : 0u;
+            a_off[i] = ((uint32_t)(c0 * 4) + r * lda) * 4u;
             a_lds[i] = (c0 * 4) * G::A_LD + c1;
         }
     }
@@ -427,11 +440,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     for (int i = 0; i < G::LB; ++i) {
         const int ch = tid + i * NT;
         const int c0 = ch % B_C0, c1 = ch / B_C0;
+        // a chunk of columns wholly past n reads the tile's first column instead
         if constexpr (!TB) {  // c0: k / 4, c1: n
-            b_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * ldb) * 4u;
+            const uint32_t cc = col0 + (uint32_t)c1 < n ? (uint32_t)c1 : 0u;
+            b_off[i] = ((uint32_t)(c0 * 4) + cc * ldb) * 4u;
             b_lds[i] = G::A_STAGE + c1 * G::B_LD + c0 * 4;
         } else {              // c0: n / 4, c1: k
-            b_off[i] = ((uint32_t)(c0 * 4) + (uint32_t)c1 * ldb) * 4u;
+            const uint32_t cc = col0 + (uint32_t)(c0 * 4) < n ? (uint32_t)(c0 * 4) : 0u;
+            b_off[i] = (cc + (uint32_t)c1 * ldb) * 4u;
             b_lds[i] = G::A_STAGE + (c0 * 4) * G::B_LD + c1;
         }
     }
@@ -822,13 +838,17 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                     const int cc = idx / E_RUNS, r4 = (idx % E_RUNS) * 4;
                     f32x4 v = *reinterpret_cast<const f32x4*>(e + cc * E_LD + r4);
                     const size_t col = (size_t)(wcol + jn * AT::N + cc);
-                    if (beta != 0.0f) {
-                        const f32x4 cv = *reinterpret_cast<const f32x4*>(c + col * ldc + wrow + r4);
-                        v.x = __builtin_fmaf(beta, cv.x, v.x); v.y = __builtin_fmaf(beta, cv.y, v.y);
-                        v.z = __builtin_fmaf(beta, cv.z, v.z); v.w = __builtin_fmaf(beta, cv.w, v.w);
+                    // an edge tile stores only inside D (m % 4 == 0: a float4 run
+                    // is wholly inside or wholly past m)
+                    if (!edge || (col < n && (uint32_t)(wrow + r4) < m)) {
+                        if (beta != 0.0f) {
+                            const f32x4 cv = *reinterpret_cast<const f32x4*>(c + col * ldc + wrow + r4);
+                            v.x = __builtin_fmaf(beta, cv.x, v.x); v.y = __builtin_fmaf(beta, cv.y, v.y);
+                            v.z = __builtin_fmaf(beta, cv.z, v.z); v.w = __builtin_fmaf(beta, cv.w, v.w);
+                        }
+                        // streaming (nt) store: D is not read again by this launch
+                        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4));
                     }
-                    // streaming (nt) store: D is not read again by this launch
-                    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4));
                 }
                 // this group's reads are done before the next group overwrites the chunk
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

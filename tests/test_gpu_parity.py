@@ -203,6 +203,10 @@ EDGE_SHAPES = [
     ("mt256x256_a32_wg2x2_dk24_s3", 512, 768, 4100, 0),
     ("mt256x256_a32_wg2x2_dk24_s3", 512, 512, 44, 4),
     ("mt128x64_a16_wg2x2_dk32_s3", 16384, 128, 1000, 0),
+    # edge tiles with aligned columns and m % 4 == 0: the vector path, loads redirected, stores predicated
+    ("mt256x256_a32_wg2x2_dk24_s3", 4000, 3000, 2000, 0),
+    ("mt256x256_a32_wg2x2_dk24_s3", 1000, 700, 508, 4),
+    ("mt64x64_a16_wg1x4_dk32_s3", 1000, 1000, 1000, 0),
     ("mt64x64_a16_wg2x2_dk32_s3", 1023, 1025, 1027, 0),
     ("mt64x64_a16_wg2x2_dk32_s3", 5, 3, 1, 1),
     ("mt128x64_a16_wg2x2_dk16_s3", 8190, 130, 250, 0),
@@ -239,6 +243,8 @@ TRANS_CASES = [
     ("mt256x256_a32_wg2x2_dk16_s3_tn", 1024, 768, 512, 0),
     ("mt256x256_a32_wg2x2_dk16_s3_nt", 1000, 700, 333, 1),
     ("mt256x256_a32_wg2x2_dk16_s3_tt", 512, 512, 1024, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_tt", 1000, 700, 512, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_tn", 900, 500, 300, 4),
     ("mt64x64_a16_wg2x2_dk32_s3_tn", 300, 200, 100, 3),
     ("mt32x32_a32_wg1x1_dk16_tt", 35, 59, 33, 1),
     ("mt16x16_a16_wg1x1_dk16_nt", 19, 27, 33, 0),
