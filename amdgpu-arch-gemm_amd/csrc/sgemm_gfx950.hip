@@ -15,23 +15,23 @@
 // SG_WG0 * SG_WG1 * 64 work-items; all LDS is static (the runner passes 0 B of
 // dynamic LDS, generator_runner.cpp:189).  numWorkgroupX = ceil(m / MT0),
 // numWorkgroupY = ceil(n / MT1) with MT0 = atom_m * WG0 * WT0 and
-// MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  Any m, n, k works: tiles
-// that lie wholly inside D with 16-byte aligned columns (every leading
-// dimension a multiple of 4) take the vector path; so do edge tiles when m is
-// a multiple of 4 (and n, for a transposed B), with their loads past the edge
-// redirected inside the tile and their stores predicated.  Other edge tiles
-// and unaligned problems load and store element by element.  A K
-// remainder (k % 4 == 0) keeps the vector path by shifting the K origin so
-// that the first K tile is the partial one, its missing values loaded as
-// zeros; otherwise the last K tile is zero-filled on the element-wise path.
-// The host side (shim, runner)
+// MT1 = atom_n * WG1 * WT1 (generator.py:898-903).  Any m, n, k, any leading
+// dimensions and any 4-byte aligned pointers take the vector path: buffer
+// loads and stores of float4 chunks need dword alignment only, and their
+// range check is per dword.  Chunks wholly past m or n load a chunk inside
+// the tile instead; a chunk straddling the end of an operand reads 0 past it;
+// the epilogue stores only elements inside D.  A K remainder shifts the K
+// origin so that the first K tile is the partial one, its missing values
+// loaded as zeros (element by element for chunks along k that straddle it).
+// Only a K remainder with a single K tile, or with a rotated first K tile
+// (SG_MAPK > 1), takes the element-wise path.  The host side (shim, runner)
 // checks that lda >= m, ldb >= k, ldc >= m, ldd >= m before every launch.
 //
 // Data path per K tile of depth DK:
 //   HBM --buffer_load_dwordx4--> VGPR --ds_write_b128--> LDS (NBUF buffers)
 //   LDS --ds_read_b{32,64,128}--> VGPR --v_mfma_f32_{32x32x2,16x16x4}_f32--> accumulators
 // and after the K loop accumulators --(alpha)--> LDS column chunk --(beta * C)-->
-// global_store_dwordx4 down whole columns of D.
+// buffer_store_dwordx4 down whole columns of D.
 //
 // LDS layouts (floats):
 //   A tile: [DK][MT0 + PAD_A]  -- one k per row, m contiguous; written straight
@@ -138,6 +138,7 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // Cache-policy operand of the buffer intrinsics on gfx94x/gfx950: bit 0 sc0,
 // bit 1 nt, bit 4 sc1; sc1 alone is device scope (coherent across XCDs).
 constexpr int CPOL_SC1 = 0x10;
+constexpr int CPOL_NT = 0x2;
 
 template <int N> struct Vec;
 template <> struct Vec<1> { typedef float type; };
@@ -249,7 +250,7 @@ template <int W> __device__ __forceinline__ void global_load_row(const float* p,
     }
 }
 
-// Tags selecting the vector (interior, aligned) or element-wise (edge) loads.
+// Tags selecting the vector (float4 chunk) or element-wise K loop.
 struct FastPath { static constexpr bool slow = false; };
 struct SlowPath { static constexpr bool slow = true; };
 // Tags marking the load of a partial first K tile (shifted K origin) or any other.
@@ -351,7 +352,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform (a scalar register): the epilogue's buffer descriptors
+    // derived from it then need no per-lane waterfall loop
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % SG_WG0;
     const int wn = wave / SG_WG0;
 
@@ -366,6 +369,15 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 tx, ty);
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
+
+    // Bytes from each operand's first element to just past the last one the
+    // caller guarantees (column-major with its leading dimension): the loads'
+    // buffer descriptors never reach past them.
+    auto extent = [](uint32_t cols, uint32_t ld, uint32_t rows) -> uint64_t {
+        return (cols && rows) ? ((uint64_t)(cols - 1) * ld + rows) * 4u : 0u;
+    };
+    const char* const a_lim = reinterpret_cast<const char*>(a) + (TA ? extent(m, lda, k_total) : extent(k_total, lda, m));
+    const char* const b_lim = reinterpret_cast<const char*>(b) + (TB ? extent(k_total, ldb, n) : extent(n, ldb, k_total));
 
     // K range of this work-group: all of it, or range `split` of `splits`
     // ranges of whole K tiles (the last range takes the remainder; ranges past
@@ -382,29 +394,27 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         b += TB ? (size_t)k_first * ldb : (size_t)k_first;
     }
     const int ktiles = (int)((k + DK - 1) / DK);
-    // Uniform per work-group: the vector fast path needs a whole tile inside D
-    // and 16-byte aligned rows of every operand; otherwise loads and stores go
-    // element by element with bounds checks.
+    // Uniform per work-group: every tile takes the vector path (float4 chunks
+    // through buffer loads, dword alignment is enough) except for the K
+    // remainders it cannot take below; those load and store element by
+    // element with bounds checks.
     //
-    // A K remainder stays on the fast path when k % 4 == 0, there are at least
-    // two K tiles and the first K tile is not rotated: the K origin moves back
-    // by kshift, so K tile t covers k in [t*DK - kshift, (t+1)*DK - kshift).
-    // Only tile 0 is then partial; its first kshift values load as zeros
-    // (whole float4 chunks, masked), and every later tile -- including the one
-    // the branch-free refill repeats past the end -- is whole and in bounds.
-    // Otherwise the slow path zero-fills the last K tile.
+    // K remainder: the K origin moves back by kshift, so K tile t covers k in
+    // [t*DK - kshift, (t+1)*DK - kshift).  Only tile 0 is then partial; its
+    // first kshift values load as zeros, and every later tile -- including the
+    // one the branch-free refill repeats past the end -- is whole and in
+    // bounds.  This needs at least two K tiles and no rotation of the first.
     //
-    // An edge tile (one reaching past m or n) stays on the fast path as well
-    // when no float4 chunk straddles the edge: m % 4 == 0, and n % 4 == 0 for
-    // B^T (whose chunks run along n).  Its chunks wholly past the edge load
-    // a chunk of the tile's first row (A) or column (B) instead -- always in
-    // bounds -- and what they bring only reaches rows or columns of D past the
-    // edge, which the epilogue does not store.
-    const bool aligned = ((lda | ldb | ldc | ldd) & 3u) == 0;
+    // Edges in M and N: values of A past row m and of B past column n only
+    // reach rows and columns of D past the edge, which the epilogue does not
+    // store.  So a chunk wholly past the edge loads a chunk of the tile's first
+    // row (A) or column (B) instead, always in bounds, and a chunk straddling
+    // the edge loads as it is: its dwords past the operand's last element are
+    // outside the buffer descriptor's range and read as 0 (the range check is
+    // per dword), the others are in memory.
     const bool edge = row0 + MT0 > m || col0 + MT1 > n;
-    const bool slow_mn = !aligned || (edge && ((m & 3u) != 0u || (TB && (n & 3u) != 0u)));
     const uint32_t kshift = (k % DK) ? DK - k % DK : 0u;
-    const bool slow_k = kshift != 0u && (SG_MAPK > 1 || (k & 3u) != 0u || ktiles < 2);
+    const bool slow = kshift != 0u && (SG_MAPK > 1 || ktiles < 2);
 
     // ---- global -> VGPR staging (byte offsets inside a K tile) ----
     // Every thread moves float4 chunks.  A chunk runs along the operand's
@@ -457,6 +467,23 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // 32 bits; they are the buffer descriptors' num_records.
     const uint32_t a_bytes = ((TA ? (uint32_t)(MT0 - 1) : (uint32_t)(DK - 1)) * lda + (uint32_t)(TA ? DK : MT0)) * 4u;
     const uint32_t b_bytes = ((TB ? (uint32_t)(DK - 1) : (uint32_t)(MT1 - 1)) * ldb + (uint32_t)(TB ? MT1 : DK)) * 4u;
+    // Which loads can reach past an operand's last element: chunks wholly
+    // past m or n are redirected, and every K tile but the first lies inside
+    // [0, k), so only a chunk straddling m (A) or n (B^T) in the operand's
+    // last column (row) reads past it, by at most 3 dwords -- at a column
+    // (row) within 3 of the last, inside the last K tile since DK >= 4 and
+    // that tile is whole.  So only the last K tile's descriptors are cut at
+    // the operand's end; a cut never removes an element inside the operand.
+    auto cut = [](const char* lim, const float* base, uint32_t bytes) -> int {
+        const int64_t left = lim - reinterpret_cast<const char*>(base);
+        return (int)(left < 0 ? 0 : (left < (int64_t)bytes ? left : (int64_t)bytes));
+    };
+    int a_rec_last = 0, b_rec_last = 0;
+    if (ktiles > 0) {
+        const int64_t kb = (int64_t)(ktiles - 1) * DK - (int64_t)kshift;
+        a_rec_last = cut(a_lim, a_tile + (TA ? kb : kb * (int64_t)lda), a_bytes);
+        b_rec_last = cut(b_lim, b_tile + (TB ? kb * (int64_t)ldb : kb), b_bytes);
+    }
     // PD register staging sets: with the early-refill schedules a K tile's
     // global loads are issued PD tiles before its LDS writes.
     constexpr int PD = (SG_PLR >= 2) ? SG_PD : 1;
@@ -470,8 +497,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // path every chunk is one buffer_load_dwordx4: a wave-uniform descriptor
     // per operand and K tile (scalar arithmetic only; num_records is the K
     // tile's footprint) and the chunk's 32-bit byte offset -- no 64-bit vector
-    // address per load.  A Head tag (tile 0 of a shifted K origin) loads only
-    // the chunks at k >= kshift, with flat loads, and zeros the rest.  With a
+    // address per load.  A Head tag (tile 0 of a shifted K origin) keeps only
+    // the values at k >= kshift and zeros the rest.  With a
     // SlowPath tag every element is
     // loaded from a clamped (always valid) address and replaced by 0 when it
     // lies outside A or B, so the code stays branch-free.
@@ -479,25 +506,57 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
         if constexpr (!decltype(path)::slow) {
-            const int64_t kb = (int64_t)kt * DK - (int64_t)kshift;
+            // descriptors start at the K tile's first k, or for a Head tile at
+            // its first k inside the operand (tile k = kshift): no base ever
+            // lies before the matrix
+            const int64_t kb = (int64_t)kt * DK - (int64_t)kshift + (decltype(head)::on ? (int64_t)kshift : 0);
             const float* pa = a_tile + (TA ? kb : kb * (int64_t)lda);
             const float* pb = b_tile + (TB ? kb * (int64_t)ldb : kb);
-            const __amdgpu_buffer_rsrc_t rsa =
-                __builtin_amdgcn_make_buffer_rsrc((void*)pa, (short)0, (int)a_bytes, BUFFER_RSRC_WORD3);
-            const __amdgpu_buffer_rsrc_t rsb =
-                __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, (int)b_bytes, BUFFER_RSRC_WORD3);
-            const char* ca = reinterpret_cast<const char*>(pa);
-            const char* cb = reinterpret_cast<const char*>(pb);
+            // num_records: the K tile's footprint, cut at the operand's last
+            // element in the last K tile (32-bit scalar select, no 64-bit compare)
+            const bool last = kt == ktiles - 1;
+            const int a_rec = last ? a_rec_last : (int)a_bytes;
+            const int b_rec = last ? b_rec_last : (int)b_bytes;
+            const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)pa, (short)0, a_rec, BUFFER_RSRC_WORD3);
+            const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, b_rec, BUFFER_RSRC_WORD3);
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            // A Head chunk keeps the values at k >= kshift (inside the tile) and
+            // zeros the rest; a value below kshift loads the one at k = kshift of
+            // its row or column instead, so every load stays in bounds.  The
+            // descriptor starts kshift k steps (k_bytes each) into the tile:
+            // offsets move back by that much.  Chunks along k (A^T, B; k_bytes
+            // = 4) straddle kshift unless it is a multiple of 4: then they load
+            // element by element.
+            auto head_load = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t off, int kk, bool along_k,
+                                 uint32_t k_bytes) __attribute__((always_inline)) -> f32x4 {
+                if (!along_k || (kshift & 3u) == 0u) {
+                    const bool live = kk >= (int)kshift;
+                    const uint32_t o = off - (live ? kshift : (uint32_t)kk) * k_bytes;
+                    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, 0));
+                    return live ? v : z;
+                }
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // the element's k clamped up to kshift, as a byte step from
+                    // the descriptor's first k; written as one max so that no
+                    // constant splits off into the instruction's offset field
+                    // (the register part alone could be negative)
+                    const int ke = max(kk + e, (int)kshift);
+                    const uint32_t o = off + (uint32_t)(ke - kk - (int)kshift) * 4u;
+                    const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)o, 0, 0));
+                    v[e] = kk + e >= (int)kshift ? x : 0.0f;
+                }
+                return v;
+            };
 #pragma unroll
             for (int i = 0; i < G::LA; ++i) {
                 const int ch = tid + i * NT;
                 if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
                     if constexpr (decltype(head)::on) {
-                        // k inside the tile: c1 (A), or 4 * c0 (A^T, float4 along k)
+                        // k inside the tile of the chunk's first element: c1 (A), 4 * c0 (A^T)
                         const int kk = TA ? (ch % A_C0) * 4 : ch / A_C0;
-                        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(ca + a_off[i]);
-                        ra[set][i] = v;
+                        ra[set][i] = head_load(rsa, a_off[i], kk, TA, TA ? 4u : lda * 4u);
                     } else {
                         ra[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)a_off[i], 0, 0));
                     }
@@ -508,11 +567,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 const int ch = tid + i * NT;
                 if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
                     if constexpr (decltype(head)::on) {
-                        // k inside the tile: 4 * c0 (B, float4 along k), or c1 (B^T)
+                        // k inside the tile of the chunk's first element: 4 * c0 (B), c1 (B^T)
                         const int kk = TB ? ch / B_C0 : (ch % B_C0) * 4;
-                        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                        if (kk >= (int)kshift) v = *reinterpret_cast<const f32x4*>(cb + b_off[i]);
-                        rb[set][i] = v;
+                        rb[set][i] = head_load(rsb, b_off[i], kk, !TB, TB ? ldb * 4u : 4u);
                     } else {
                         rb[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)b_off[i], 0, 0));
                     }
@@ -725,7 +782,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             }
         }
     };
-    if (slow_mn || slow_k) kloop(SlowPath{});
+    if (slow) kloop(SlowPath{});
     else kloop(FastPath{});
 
     if constexpr (SPLIT) {
@@ -815,10 +872,24 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     constexpr int E_PER_LANE = AT::N * E_RUNS / 64;
     static_assert(AT::N * E_RUNS % 64 == 0, "a column group is a whole number of float4s per lane");
     if constexpr ((NT / 64) * E_CHUNK <= G::LDS_FLOATS) {
-        if (!slow_mn) {
+        {
             // every wave's last K-loop access to LDS is behind this barrier
             __syncthreads();
             float* e = lds + wave * E_CHUNK;
+            // Buffer descriptors over the wave's sub-tile of D and of C (SN
+            // columns of SM rows from (wrow, wcol)), cut at the matrix's last
+            // element; dword alignment is enough, so any ldc / ldd works.
+            constexpr int SN = AT::N * WT1;
+            auto sub_rsrc = [&](const float* base, uint32_t ld) __attribute__((always_inline)) {
+                const uintptr_t first = reinterpret_cast<uintptr_t>(base) + ((uint64_t)wcol * ld + (uint32_t)wrow) * 4u;
+                const uintptr_t last = reinterpret_cast<uintptr_t>(base) + ((uint64_t)(n - 1) * ld + m) * 4u;
+                const uint64_t foot = ((uint64_t)(SN - 1) * ld + SM) * 4u;
+                const uint64_t left = last > first ? (uint64_t)(last - first) : 0u;
+                return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(first), (short)0,
+                                                         (int)(left < foot ? left : foot), BUFFER_RSRC_WORD3);
+            };
+            const __amdgpu_buffer_rsrc_t rsd = sub_rsrc(d, ldd);
+            const __amdgpu_buffer_rsrc_t rsc = sub_rsrc(beta != 0.0f ? c : d, beta != 0.0f ? ldc : ldd);
 #pragma unroll
             for (int jn = 0; jn < WT1; ++jn) {
 #pragma unroll
@@ -832,22 +903,69 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-                for (int p = 0; p < E_PER_LANE; ++p) {
+                // Lane run p: column cc, rows r4..r4+3 of the group, in batches
+                // of EB runs: the batch's LDS reads, then its C loads (a run
+                // reaching past C's last element reads 0 there, the others
+                // stay inside C's allocation), then its stores.
+                constexpr int EB = E_PER_LANE < 4 ? E_PER_LANE : 4;
+                static_assert(E_PER_LANE % EB == 0, "whole batches of runs");
+                auto run_off = [&](int p, uint32_t ld) __attribute__((always_inline)) {
                     const int idx = p * 64 + lane;
-                    const int cc = idx / E_RUNS, r4 = (idx % E_RUNS) * 4;
-                    f32x4 v = *reinterpret_cast<const f32x4*>(e + cc * E_LD + r4);
-                    const size_t col = (size_t)(wcol + jn * AT::N + cc);
-                    // an edge tile stores only inside D (m % 4 == 0: a float4 run
-                    // is wholly inside or wholly past m)
-                    if (!edge || (col < n && (uint32_t)(wrow + r4) < m)) {
-                        if (beta != 0.0f) {
-                            const f32x4 cv = *reinterpret_cast<const f32x4*>(c + col * ldc + wrow + r4);
-                            v.x = __builtin_fmaf(beta, cv.x, v.x); v.y = __builtin_fmaf(beta, cv.y, v.y);
-                            v.z = __builtin_fmaf(beta, cv.z, v.z); v.w = __builtin_fmaf(beta, cv.w, v.w);
+                    return ((uint32_t)(jn * AT::N + idx / E_RUNS) * ld + (uint32_t)((idx % E_RUNS) * 4)) * 4u;
+                };
+#pragma unroll
+                for (int p0 = 0; p0 < E_PER_LANE; p0 += EB) {
+                    f32x4 v[EB];
+#pragma unroll
+                    for (int b = 0; b < EB; ++b) {
+                        const int idx = (p0 + b) * 64 + lane;
+                        v[b] = *reinterpret_cast<const f32x4*>(e + (idx / E_RUNS) * E_LD + (idx % E_RUNS) * 4);
+                    }
+                    if (beta != 0.0f) {
+                        f32x4 cv[EB];
+#pragma unroll
+                        for (int b = 0; b < EB; ++b)
+                            cv[b] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, (int)run_off(p0 + b, ldc), 0, 0));
+#pragma unroll
+                        for (int b = 0; b < EB; ++b) {
+                            v[b].x = __builtin_fmaf(beta, cv[b].x, v[b].x); v[b].y = __builtin_fmaf(beta, cv[b].y, v[b].y);
+                            v[b].z = __builtin_fmaf(beta, cv[b].z, v[b].z); v[b].w = __builtin_fmaf(beta, cv[b].w, v[b].w);
                         }
-                        // streaming (nt) store: D is not read again by this launch
-                        __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d + col * ldd + wrow + r4));
+                    }
+                    // streaming (nt) stores: D is not read again by this launch
+                    if (!edge) {
+#pragma unroll
+                        for (int b = 0; b < EB; ++b)
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[b]), rsd,
+                                                                   (int)run_off(p0 + b, ldd), 0, CPOL_NT);
+                    } else {
+                        // only elements inside D are stored: a run reaching past m
+                        // (possible when m % 4 != 0) is stored element by element
+#pragma unroll
+                        for (int b = 0; b < EB; ++b) {
+                            const int idx = (p0 + b) * 64 + lane;
+                            const uint32_t row = (uint32_t)wrow + (uint32_t)((idx % E_RUNS) * 4);
+                            const uint32_t col = (uint32_t)wcol + (uint32_t)(jn * AT::N + idx / E_RUNS);
+                            const uint32_t off = run_off(p0 + b, ldd);
+                            if (col < n && row < m) {
+                                if (row + 4u <= m) {
+                                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[b]), rsd, (int)off,
+                                                                           0, CPOL_NT);
+                                } else {
+#pragma unroll
+                                    for (int q = 0; q < 3; ++q) {
+                                        // the element is copied out first: hipcc's
+                                        // bit_cast of a vector element with a loop
+                                        // index read element 0 for every q
+                                        const float x = v[b][q];
+                                        if (row + (uint32_t)q < m)
+                                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rsd,
+                                                                                  (int)(off + 4u * q), 0, CPOL_NT);
+                                    }
+                                }
+                            }
+                        }
                     }
                 }
                 // this group's reads are done before the next group overwrites the chunk
@@ -858,6 +976,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             return;
         }
     }
+    // Direct stores (when the LDS chunk does not fit): vector stores for an
+    // interior tile with 16-byte aligned columns of C and D, else element by
+    // element with bounds checks.
+    const bool d_vec = !edge && ((ldc | ldd) & 3u) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(c) | reinterpret_cast<uintptr_t>(d)) & 15u) == 0;
 #pragma unroll
     for (int jn = 0; jn < WT1; ++jn) {
         const size_t colo = (size_t)(wcol + jn * AT::N + (lane % AT::N));
@@ -867,7 +990,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             float v[WT0];
 #pragma unroll
             for (int i = 0; i < WT0; ++i) v[i] = alpha * acc[i][jn][q];
-            if (!slow_mn) {
+            if (d_vec) {
                 if (beta != 0.0f) {
                     float cv[WT0];
                     global_load_row<WT0>(c + colo * ldc + rr, cv);

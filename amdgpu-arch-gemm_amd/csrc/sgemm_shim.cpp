@@ -437,6 +437,12 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
         return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets (a K tile spans %llu / %llu "
                     "bytes of A / B, limit 2^31): lda=%u ldb=%u", (unsigned long long)a_span,
                     (unsigned long long)b_span, lda, ldb);
+    // and one tile of C and of D the same way: ldc * tile_n and ldd * tile_n
+    // floats below 2^31 bytes
+    const uint64_t cd_span = (uint64_t)(ldc > ldd ? ldc : ldd) * (uint32_t)i.tile_n * 4u;
+    if (cd_span >= (1ull << 31))
+        return fail(SGEMM_E_SHAPE, "leading dimensions too large for 32-bit tile offsets (a tile of C / D spans %llu "
+                    "bytes, limit 2^31): ldc=%u ldd=%u", (unsigned long long)cd_span, ldc, ldd);
     return SGEMM_OK;
 }
 
@@ -508,8 +514,9 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
     if (m == 0 || n == 0) return SGEMM_OK;
     if (!dD || (k && (!dA || !dB)) || (beta != 0.0f && !dC))
         return fail(SGEMM_E_INVALID, "sgemm_launch: null device pointer");
-    if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 15u)
-        return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 16-byte aligned");
+    // buffer loads and stores need dword alignment only
+    if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 3u)
+        return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 4-byte aligned");
     const sgemm_kernel_info& i = h->info;
     KernArgs ka;
     memset(&ka, 0, sizeof(ka));

@@ -138,12 +138,12 @@ def build_all(kernel_dir: str = KERNEL_DIR, names: Optional[List[str]] = None, j
 
 def vector_k(name: str, k: int) -> bool:
     """True when every K tile of a k-deep problem takes the vector path: whole
-    K tiles, or a remainder with k % 4 == 0 and at least two K tiles on an
-    instance without a K rotation (the kernel then shifts the K origin so the
-    first tile is the partial one)."""
+    K tiles, or a remainder with at least two K tiles on an instance without a
+    K rotation (the kernel then shifts the K origin so the first tile is the
+    partial one)."""
     cfg, opt = SOLUTIONS[name]
     dk = cfg.depth_k
-    return k % dk == 0 or (k % 4 == 0 and k > dk and opt.map_k_idx <= 1)
+    return k % dk == 0 or (k > dk and opt.map_k_idx <= 1)
 
 
 def divides(name: str, m: int, n: int, k: int) -> bool:

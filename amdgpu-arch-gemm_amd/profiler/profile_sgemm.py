@@ -55,6 +55,9 @@ WORKLOADS = {
     "cfg5": (16384, 128, 4096, 4, 0),
     "deepk": (512, 512, 16384, 5, 0),   # few tiles, deep K: the split-K kernel
 }
+# runner warm-up launches per workload: about 0.1 s of each, long enough for
+# the engine clock to leave its idle state (5 launches of a 20 us kernel are not)
+WARMUP = {"cfg2": 4000, "cfg3": 120, "cfg4": 400, "cfg5": 800, "deepk": 1200}
 
 
 def log(msg):
@@ -139,13 +142,17 @@ def main():
     ap.add_argument("--out", required=True, help="raw rocprofv3 output folder (large; keep it out of the repository)")
     ap.add_argument("--summary", default=None, help="markdown summary path (default: <out>/summary.md)")
     ap.add_argument("--runs", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed runner launches first (default: about 0.1 s of the workload, so the "
+                         "engine clock has ramped up before the dispatches the medians describe)")
     ap.add_argument("--cus", type=int, default=256)
     args = ap.parse_args()
 
     m, n, k, seed, dist = WORKLOADS[args.workload]
     co, toml = catalog.paths(args.kernel)
     os.makedirs(args.out, exist_ok=True)
-    runner = [RUNNER, co, toml, str(m), str(n), str(k), "5", str(args.runs), "0", str(seed), str(dist), "1", "0"]
+    warmup = args.warmup if args.warmup is not None else WARMUP[args.workload]
+    runner = [RUNNER, co, toml, str(m), str(n), str(k), str(warmup), str(args.runs), "0", str(seed), str(dist), "1", "0"]
     probe = [PROBE, str(PROBE_BYTES), "3"]
     cmds = {}
 

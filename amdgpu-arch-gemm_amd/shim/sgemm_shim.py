@@ -165,6 +165,11 @@ class DeviceBuffer:
     def zero(self):
         _check("sgemm_memset", load_library().sgemm_memset(self.ptr, 0, self.nbytes))
 
+    def view(self, offset: int, nbytes: int) -> "DeviceView":
+        """The bytes [offset, offset + nbytes) of this allocation, usable
+        wherever a DeviceBuffer is (a launch needs 4-byte aligned pointers)."""
+        return DeviceView(self, offset, nbytes)
+
     def close(self):
         if self.ptr:
             load_library().sgemm_free(self.ptr)
@@ -175,6 +180,21 @@ class DeviceBuffer:
             self.close()
         except Exception:
             pass
+
+
+class DeviceView(DeviceBuffer):
+    """A byte range of a DeviceBuffer; it owns nothing and keeps its owner alive."""
+
+    def __init__(self, owner: DeviceBuffer, offset: int, nbytes: int):
+        offset, nbytes = int(offset), int(nbytes)
+        if offset < 0 or nbytes < 0 or offset + nbytes > owner.nbytes:
+            raise ValueError(f"view [{offset}, {offset + nbytes}) outside a {owner.nbytes}-byte buffer")
+        self.owner = owner
+        self.nbytes = nbytes
+        self.ptr = owner.ptr + offset
+
+    def close(self):
+        self.ptr = None
 
 
 class Kernel:

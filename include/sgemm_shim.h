@@ -102,8 +102,9 @@ int sgemm_get_info(const sgemm_handle* h, sgemm_kernel_info* info);
  * message otherwise.  Any m, n, k is accepted (edge tiles and a K remainder are
  * masked in the kernel); the leading dimensions must cover the stored
  * matrices (lda >= m, or k with trans_a; ldb >= k, or n with trans_b;
- * ldc, ldd >= m), and one tile's span of A and of B must stay below 2^32
- * elements. */
+ * ldc, ldd >= m), and one tile's span of each matrix must stay below 2^31
+ * bytes (lda * depth_k, or lda * tile_m with trans_a; ldb * tile_n, or
+ * ldb * depth_k with trans_b; ldc * tile_n and ldd * tile_n, times 4). */
 int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd);
 
@@ -146,7 +147,8 @@ int sgemm_memset(void* dptr, int value, size_t bytes);
  * HIP_LAUNCH_PARAM_BUFFER_POINTER with a grid of (ceil(m/MT0), ceil(n/MT1)) blocks.
  * With a split count above 1 (sgemm_set_split_k) it launches the split kernel
  * instead, with the handle's workspace; launches of one handle share that
- * workspace, so they must run in order on the handle's stream. */
+ * workspace, so they must run in order on the handle's stream.  Device
+ * pointers need 4-byte alignment only (SGEMM_E_INVALID otherwise). */
 int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
                  uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                  float alpha, float beta);

@@ -686,6 +686,15 @@ def _s_and_saveexec(vm, ins, prog):
     vm.scc = int(vm.exec != 0)
 
 
+@op("s_andn2_saveexec_b64")
+def _s_andn2_saveexec(vm, ins, prog):
+    # EXEC = S0 & ~EXEC (the else-branch mask); the old EXEC goes to D
+    old = vm.exec
+    vm.exec = vm.rs64(ins.ops[1]) & ~old & MASK64
+    vm.ws64(ins.ops[0], old)
+    vm.scc = int(vm.exec != 0)
+
+
 @op("s_or_saveexec_b64")
 def _s_or_saveexec(vm, ins, prog):
     # the source is read before the destination (often the same pair) is written
@@ -1173,10 +1182,11 @@ def _global_atomic_add(vm, ins, prog):
 
 
 def _buffer_addr(vm, ins, vaddr_op, srd_op, soff_op):
-    """Byte addresses and in-range mask of a raw (stride 0) MUBUF access:
-    base + (offen ? vaddr : 0) + soffset + offset, checked per access against
-    num_records (word 2 of the resource); out-of-range loads read 0 and
-    out-of-range stores are dropped, as on the hardware."""
+    """Byte addresses and offsets of a raw (stride 0) MUBUF access:
+    base + (offen ? vaddr : 0) + soffset + offset.  The range check against
+    num_records (word 2 of the resource) is per dword, as measured on gfx950:
+    a multi-dword load returns its in-range dwords and 0 for the others, a
+    store writes only its in-range dwords."""
     if ins.mods.get("idxen", 0):
         raise NotImplementedError(f"indexed buffer access {ins}")
     w = [int(vm.s[srd_op.index + i]) for i in range(4)]
@@ -1186,6 +1196,11 @@ def _buffer_addr(vm, ins, vaddr_op, srd_op, soff_op):
     num_records = w[2]
     off = vm.rv32(vaddr_op).astype(np.int64) if ins.mods.get("offen", 0) else np.zeros(WAVE, dtype=np.int64)
     off = off + np.int64(vm.rs32(soff_op)) + np.int64(ins.mods.get("offset", 0))
+    # A sum past 32 bits (a "negative" register offset plus the instruction's
+    # offset field) is not modelled: which of the wrapped and the unwrapped
+    # offset the range check sees is not part of this machine's contract.
+    if (off[vm.exec_mask()] >= (1 << 32)).any():
+        raise NotImplementedError(f"{ins}: buffer offset sum past 32 bits")
     return np.int64(base) + off, off, num_records
 
 
@@ -1193,10 +1208,11 @@ def _buffer_load(nd):
     def _impl(vm, ins, prog):
         dst, vaddr, srd, soff = ins.ops[:4]
         addr, off, num = _buffer_addr(vm, ins, vaddr, srd, soff)
-        mask = vm.exec_mask() & (off + 4 * nd <= num)
         data = np.zeros((nd, WAVE), dtype=np.uint32)
-        if mask.any():
-            data[:, mask] = vm.vmem.read_u32(addr[mask], nd, str(ins))
+        for i in range(nd):  # per-dword range check
+            mask = vm.exec_mask() & (off + 4 * (i + 1) <= num)
+            if mask.any():
+                data[i, mask] = vm.vmem.read_u32(addr[mask] + 4 * i, 1, str(ins))[0]
         emask = vm.exec_mask()
 
         def land():
@@ -1210,10 +1226,10 @@ def _buffer_store(nd):
     def _impl(vm, ins, prog):
         src, vaddr, srd, soff = ins.ops[:4]
         addr, off, num = _buffer_addr(vm, ins, vaddr, srd, soff)
-        mask = vm.exec_mask() & (off + 4 * nd <= num)
-        if mask.any():
-            data = np.stack([vm.regfile(src)[src.index + i] for i in range(nd)])
-            vm.vmem.write_u32(addr[mask], data[:, mask], str(ins))
+        for i in range(nd):  # per-dword range check
+            mask = vm.exec_mask() & (off + 4 * (i + 1) <= num)
+            if mask.any():
+                vm.vmem.write_u32(addr[mask] + 4 * i, vm.regfile(src)[src.index + i][mask][None, :], str(ins))
         vm.pending["vmcnt"].append(lambda: None)
     return _impl
 
@@ -1400,7 +1416,8 @@ def pack_splitk_kernargs(base: bytes, ws: int, tickets: int, splits: int) -> byt
 def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: np.ndarray,
               C: Optional[np.ndarray] = None, alpha: float = 1.0, beta: float = 0.0,
               mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None,
-              splits: int = 0, order: Optional[Sequence[Tuple[int, int, int]]] = None) -> Tuple[np.ndarray, Dict]:
+              splits: int = 0, order: Optional[Sequence[Tuple[int, int, int]]] = None,
+              misalign: int = 0) -> Tuple[np.ndarray, Dict]:
     """Runs a compiled SGEMM kernel on column-major A, B, C.
 
     Without ``mnk`` the problem is A (m x k) @ B (k x n) with tight leading
@@ -1412,7 +1429,10 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     ``splits >= 1`` runs ``generated_gemm_splitk`` instead, over a grid of
     ``splits`` K ranges, with its workspace and zeroed tickets; ``order`` is the
     work-group order (see run_kernel).  The returned info holds the tickets
-    after the launch."""
+    after the launch.  ``misalign`` (a multiple of 4 below 16) moves the start
+    of every buffer that many bytes past a 4 KiB boundary."""
+    if misalign % 4 or not 0 <= misalign < 16:
+        raise ValueError("misalign must be 0, 4, 8 or 12 bytes")
     A = np.asfortranarray(A, dtype=np.float32)
     B = np.asfortranarray(B, dtype=np.float32)
     if mnk is None:
@@ -1435,8 +1455,8 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     # unallocated gaps between them: any access past a buffer raises
     offs, pos = [], 4096
     for bl in blobs:
-        offs.append(pos)
-        pos += (bl.nbytes + 4095) // 4096 * 4096 + 4096
+        offs.append(pos + misalign)
+        pos += (bl.nbytes + misalign + 4095) // 4096 * 4096 + 4096
     mem = Memory(pos, "vmem")
     for o, bl, label in zip(offs, blobs, ["A", "B", "C", "D", "ws", "tickets"]):
         mem.write_bytes(o, bl.tobytes())

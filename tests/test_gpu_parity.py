@@ -238,6 +238,63 @@ def test_arbitrary_shapes(kernels, name, m, n, k, pad):
     assert np.all(Dfull[m:, :] == -3.5), "rows past m of D were written"
 
 
+UNALIGNED_CASES = [
+    # (instance, m, n, k, pad, shift, splits): odd leading dimensions and
+    # pointers `shift` floats past a 16-byte boundary (dword aligned only)
+    ("mt256x256_a32_wg2x2_dk24_s3", 1001, 999, 1003, 1, 1, 0),
+    ("mt256x256_a32_wg2x2_dk24_s3", 4095, 1024, 4097, 0, 3, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_tn", 777, 555, 333, 3, 2, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_nt", 515, 301, 262, 1, 1, 0),
+    ("mt256x256_a32_wg2x2_dk16_s3_tt", 513, 300, 257, 1, 3, 0),
+    ("mt256x128_a32_wg2x2_dk16", 1000, 500, 300, 0, 1, 0),      # the epilogue without an LDS stage
+    ("mt256x128_a32_wg2x2_dk16", 1024, 512, 256, 4, 0, 0),
+    ("mt64x64_a16_wg1x4_dk32_s3", 4095, 257, 2049, 0, 1, 0),
+    ("mt128x64_a16_wg2x2_dk16_s2", 511, 509, 16383, 1, 2, 0),   # split-K chosen by the host
+    ("mt128x64_a16_wg2x2_dk16_s2", 130, 66, 1001, 3, 1, 5),
+]
+
+
+def _shifted(arr, shift):
+    """A device copy of column-major `arr` starting `shift` floats into its
+    allocation; returns (allocation, view with .ptr)."""
+    flat = np.ascontiguousarray(np.asarray(arr, dtype=np.float32).ravel(order="F"))
+    buf = S.DeviceBuffer(flat.nbytes + 16)
+    view = buf.view(4 * shift, flat.nbytes)
+    view.upload(flat)
+    return buf, view
+
+
+@pytest.mark.parametrize("name,m,n,k,pad,shift,splits", UNALIGNED_CASES)
+def test_unaligned_pointers_and_leading_dimensions(kernels, name, m, n, k, pad, shift, splits):
+    """Buffer loads and stores need dword alignment only: any leading
+    dimension and any 4-byte aligned pointer take the same kernels, checked
+    against the oracle; rows past m of D stay untouched."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    _say(f"unaligned {name} {m}x{n}x{k} pad {pad} shift {shift} splits {splits}")
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    lda, ldb, ldc, ldd = ra + pad, rb + 2 * pad, m + pad, m + 3 * pad
+    Af = S.fill_matrix(lda, ca, 12, 0)
+    Bf = S.fill_matrix(ldb, cb, 12, 1)
+    Cf = S.fill_matrix(ldc, n, 12, 2)
+    (ba, va), (bb, vb), (bc, vc) = (_shifted(x, shift) for x in (Af, Bf, Cf))
+    bd, vd = _shifted(np.full((ldd, n), 2.75, dtype=np.float32), shift)
+    with _kernel(name) as kern:
+        kern.set_split_k(splits)
+        kern.launch(va, vb, vc, vd, m, n, k, alpha=0.75, beta=-1.5, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd)
+        kern.synchronize()
+    Dfull = vd.download().reshape(n, ldd).T
+    cols = _sample_columns(n, 48, 5)
+    opA = np.asfortranarray(Af[:ra, :ca].T if cfg.trans_a else Af[:m, :k])
+    opB = np.asfortranarray(Bf[:rb, :cb].T if cfg.trans_b else Bf[:k, :n])
+    ref = oracle.cpu_gemm_mt(opA, np.asfortranarray(opB[:, cols]), np.asfortranarray(Cf[:m, cols]), 0.75, -1.5,
+                             threads=16)
+    _check(Dfull[:m, cols], ref, k, name)
+    assert np.all(Dfull[m:, :] == 2.75), "rows past m of D were written"
+    for b in (ba, bb, bc, bd):
+        b.close()
+
+
 TRANS_CASES = [
     # (instance, m, n, k, pad)
     ("mt256x256_a32_wg2x2_dk16_s3_tn", 1024, 768, 512, 0),

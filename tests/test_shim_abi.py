@@ -120,3 +120,18 @@ def test_runner_cpu_reference_matches_oracle():
         subprocess.run([exe], cwd=tmp, check=True)
         D = np.fromfile(os.path.join(tmp, "out.bin"), dtype=np.float32).reshape(n, m).T
     assert np.array_equal(D, oracle.cpu_gemm(A, B, C, 0.5, -2.0))
+
+
+def test_device_view_bounds_and_ownership():
+    """A view is a byte range of its owner: pointer arithmetic only, checked
+    against the owner's size, and closing it never frees the owner's memory."""
+    import types
+    owner = types.SimpleNamespace(ptr=1 << 20, nbytes=64)
+    v = S.DeviceView(owner, 4, 60)
+    assert v.ptr == (1 << 20) + 4 and v.nbytes == 60 and v.owner is owner
+    v.close()
+    assert v.ptr is None and owner.ptr == 1 << 20
+    for off, nb in ((-4, 8), (8, 57), (64, 4)):
+        with pytest.raises(ValueError):
+            S.DeviceView(owner, off, nb)
+    assert S.DeviceView(owner, 64, 0).nbytes == 0

@@ -250,6 +250,7 @@ EDGE_CASES = [  # (instance, m, n, k): partial tiles in M and N, K remainders, k
     ("mt64x64_a16_wg2x2_dk32_s3", 67, 123, 65), ("mt64x64_a16_wg2x2_dk32_s3", 128, 64, 29),
     ("mt128x64_a32_wg4x1_dk8_s3", 131, 123, 17), ("mt16x16_a16_wg1x1_dk16_s3_plr3", 15, 17, 48),
     ("mt64x64_a32_wg1x1_dk16", 63, 65, 48),
+    ("mt256x128_a32_wg2x2_dk16", 250, 100, 40),  # the epilogue without an LDS stage
 ]
 
 
@@ -258,46 +259,59 @@ EDGE_CASES = [  # (instance, m, n, k): partial tiles in M and N, K remainders, k
 def test_edge_shapes_stay_inside_every_buffer(name, m, n, k, pad):
     """Arbitrary shapes: each of A, B, C, D is its own guarded region in the VM,
     so any read or write outside the matrices raises MemoryError.  pad = 1 makes
-    every leading dimension odd (the element-wise path for all tiles)."""
+    every leading dimension odd and every buffer start 4 bytes past a 16-byte
+    boundary."""
     prog, cfg = program(name)
     lda, ldb, ldc, ldd = m + pad, k + pad, m + 2 * pad, m + 3 * pad
     A = oracle.fill_matrix(lda, k, 3, 0)
     B = oracle.fill_matrix(ldb, n, 3, 1)
     C = oracle.fill_matrix(ldc, n, 3, 2)
-    D, _ = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=ldd)
+    D, _ = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=ldd,
+                     misalign=4 * pad)
     ref = oracle.gemm_f64(A[:m, :k], B[:k, :n], C[:m, :n], 0.5, 1.5)
     assert oracle.normwise_error(D[:m, :n], ref) <= oracle.tolerance(k)
     assert np.all(D[m:, :] == 0), "rows past m of D were written"
 
 
-EDGE_VECTOR_CASES = [  # (instance, m, n, k): edge tiles in M and N with m % 4 == 0 (n % 4 == 0 for B^T)
-    ("mt64x64_a16_wg2x2_dk32_s3", 100, 70, 64), ("mt32x32_a32_wg1x1_dk16", 36, 40, 48),
-    ("mt64x64_a16_wg2x2_dk32_s3_tn", 100, 70, 64), ("mt32x32_a32_wg1x1_dk16_tt", 36, 44, 48),
-    ("mt16x16_a16_wg1x1_dk16_nt", 20, 36, 32),
-    ("mt64x64_a16_wg2x2_dk32_s3", 100, 70, 100),   # and a K remainder (shifted K origin)
+VECTOR_CASES = [  # (instance, m, n, k, pad, misalign): every shape takes the vector path
+    ("mt64x64_a16_wg2x2_dk32_s3", 100, 70, 64, 0, 0), ("mt32x32_a32_wg1x1_dk16", 36, 40, 48, 0, 0),
+    ("mt64x64_a16_wg2x2_dk32_s3_tn", 100, 70, 64, 0, 0), ("mt32x32_a32_wg1x1_dk16_tt", 36, 44, 48, 0, 0),
+    ("mt16x16_a16_wg1x1_dk16_nt", 20, 36, 32, 0, 0),
+    ("mt64x64_a16_wg2x2_dk32_s3", 100, 70, 100, 0, 0),   # and a K remainder (shifted K origin)
+    # unaligned: m % 4 != 0, odd leading dimensions, dword-aligned pointers
+    ("mt64x64_a16_wg2x2_dk32_s3", 99, 70, 64, 1, 4), ("mt32x32_a32_wg1x1_dk16", 35, 59, 66, 1, 8),
+    ("mt64x64_a16_wg2x2_dk32_s3_tn", 101, 70, 67, 3, 12), ("mt32x32_a32_wg1x1_dk16_tt", 37, 45, 50, 1, 4),
+    ("mt16x16_a16_wg1x1_dk16_nt", 21, 37, 35, 2, 4), ("mt64x64_a16_wg2x2_dk32_s3", 64, 64, 97, 1, 0),
 ]
 
 
-@pytest.mark.parametrize("name,m,n,k", EDGE_VECTOR_CASES)
-def test_aligned_edge_tiles_keep_the_vector_path(name, m, n, k):
-    """Edge tiles with 16-byte aligned columns and m % 4 == 0 stay on the
-    vector path: chunks past the edge load a chunk of the tile's first row or
-    column, the epilogue's stores are predicated.  Every buffer is guarded,
-    rows past m of D (ldd > m) must stay untouched, and the launch runs about
-    as many instructions as the same grid of whole tiles."""
+@pytest.mark.parametrize("name,m,n,k,pad,misalign", VECTOR_CASES)
+def test_any_shape_keeps_the_vector_path(name, m, n, k, pad, misalign):
+    """Every shape takes the vector path: chunks wholly past the edge load a
+    chunk of the tile's first row or column, a chunk straddling the end of an
+    operand reads 0 past it (per-dword buffer range check), a K remainder moves
+    the K origin back (elementwise loads in the first K tile when it straddles
+    a chunk along k), and the epilogue stores only elements inside D.  Every
+    buffer is guarded, rows past m of D (ldd > m) must stay untouched, and the
+    launch runs about as many instructions as the same grid of whole tiles."""
     prog, cfg = program(name)
     t0, t1 = cfg.tile_size
-    assert m % t0 or n % t1
-    ldd = m + 4
-    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 9)
-    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=ldd)
-    assert oracle.normwise_error(D[:m, :n], oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+    ldd = m + 4 + pad
+    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 9, pad)
+    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=ldd,
+                        misalign=misalign)
+    assert oracle.normwise_error(D[:m, :n], oracle.gemm_f64(opA, opB, C[:m, :n], 0.5, 1.5)) <= oracle.tolerance(k)
     assert np.all(D[m:, :] == 0), "rows past m of D were written"
     mw, nw = -(-m // t0) * t0, -(-n // t1) * t1
-    A2, B2, C2, _, _ = _split_operands(cfg, mw, nw, k, 9)
-    _, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A2, B2, C2, 0.5, 1.5, mnk=(mw, nw, k), ldd=mw)
+    kw = -(-k // cfg.depth_k) * cfg.depth_k
+    A2, B2, C2, _, _ = _split_operands(cfg, mw, nw, kw, 9)
+    _, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A2, B2, C2, 0.5, 1.5, mnk=(mw, nw, kw), ldd=mw)
     assert info["grid"] == info2["grid"]
-    assert info["instructions"] <= 1.1 * info2["instructions"], (info["instructions"], info2["instructions"])
+    # (edge tiles run the epilogue with bounds checks, and a K remainder that
+    # straddles a chunk along k costs one element-wise first K tile: up to
+    # 25% more at these few K tiles; the element-wise path for the whole
+    # launch runs two to three times as many)
+    assert info["instructions"] <= 1.3 * info2["instructions"], (info["instructions"], info2["instructions"])
 
 
 HEAD_CASES = [  # whole, aligned tiles with k % DK != 0 and k % 4 == 0 (instances without a K rotation)
@@ -324,7 +338,8 @@ def test_k_remainder_keeps_the_vector_path(name, m, n, k):
     kr = -(-k // dk) * dk
     A2, B2, C2, _, _ = _split_operands(cfg, m, n, kr, 7)
     _, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A2, B2, C2, 0.5, 1.5, mnk=(m, n, kr), ldd=m)
-    assert info["instructions"] <= 1.1 * info2["instructions"], (info["instructions"], info2["instructions"])
+    # (the first K tile's selects cost up to 15% at two or three K tiles)
+    assert info["instructions"] <= 1.15 * info2["instructions"], (info["instructions"], info2["instructions"])
 
 
 @pytest.mark.parametrize("name", ["mt32x32_a32_wg1x1_dk16_tt", "mt16x16_a16_wg1x1_dk16_nt",
@@ -356,14 +371,16 @@ SPLIT_CASES = [
 ]
 
 
-def _split_operands(cfg, m, n, k, seed):
+def _split_operands(cfg, m, n, k, seed, pad=0):
+    """Stored A, B, C (each with ``pad`` extra rows: leading dimensions past the
+    matrix) and op(A), op(B) as m x k and k x n."""
     ra, ca = (k, m) if cfg.trans_a else (m, k)
     rb, cb = (n, k) if cfg.trans_b else (k, n)
-    A = oracle.fill_matrix(ra, ca, seed, 0)
-    B = oracle.fill_matrix(rb, cb, seed, 1)
-    C = oracle.fill_matrix(m, n, seed, 2)
-    opA = A.T if cfg.trans_a else A
-    opB = B.T if cfg.trans_b else B
+    A = oracle.fill_matrix(ra + pad, ca, seed, 0)
+    B = oracle.fill_matrix(rb + pad, cb, seed, 1)
+    C = oracle.fill_matrix(m + pad, n, seed, 2)
+    opA = A[:ra].T if cfg.trans_a else A[:ra]
+    opB = B[:rb].T if cfg.trans_b else B[:rb]
     return A, B, C, opA, opB
 
 
@@ -433,6 +450,35 @@ def test_vm_buffer_access_is_range_checked_like_the_hardware():
     assert np.all(after[1:128:4] == -1.0) and np.array_equal(after[128:], np.arange(128, 256, dtype=np.float32))
 
 
+def test_vm_buffer_range_check_is_per_dword():
+    """The range check is per dword, as measured on an MI355X with a probe
+    kernel (dwords 1000 + i, num_records = 20 bytes, lane l loading a dwordx4 at
+    byte 4*l): a load straddling num_records keeps its in-range dwords and
+    reads 0 for the rest; dword-aligned (not 16-byte aligned) dwordx4 loads
+    read the dwords at their address.  Stores follow the same per-dword rule
+    here (the kernels never issue a store that straddles its range)."""
+    measured = [[1000, 1001, 1002, 1003], [1001, 1002, 1003, 1004], [1002, 1003, 1004, 0], [1003, 1004, 0, 0],
+                [1004, 0, 0, 0], [0, 0, 0, 0], [0, 0, 0, 0], [0, 0, 0, 0]]
+    vm = GcnVirtualMachine(104, 256, 64)
+    mem = V.Memory(1024, "vmem")
+    mem.write_bytes(0, (1000 + np.arange(256, dtype=np.uint32)).tobytes())
+    vm.vmem = mem
+    vm.s[8], vm.s[9], vm.s[10], vm.s[11] = 0, 0, 20, 0x20000
+    vm.v[1] = np.arange(64, dtype=np.uint32) * 4
+    vm.exec = 0xFF
+    vm.run("generated_gemm:\n buffer_load_dwordx4 v[2:5], v1, s[8:11], 0 offen\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    got = [[int(vm.v[2 + i][lane]) for i in range(4)] for lane in range(8)]
+    assert got == measured
+    # a store straddling num_records: lane 0 stores 4 dwords at byte 12, only the first two land
+    vm.v[6], vm.v[7], vm.v[8], vm.v[9] = (np.full(64, x, dtype=np.uint32) for x in (7, 8, 9, 10))
+    vm.v[1] = np.full(64, 12, dtype=np.uint32)
+    vm.s[10] = 20
+    vm.exec = 0x1
+    vm.run("generated_gemm:\n buffer_store_dwordx4 v[6:9], v1, s[8:11], 0 offen\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    after = np.frombuffer(mem.read_bytes(0, 32), dtype=np.uint32).tolist()
+    assert after == [1000, 1001, 1002, 7, 8, 1005, 1006, 1007]
+
+
 def test_vm_atomics_and_lane_counts():
     vm = GcnVirtualMachine(104, 256, 64)
     mem = V.Memory(8192, "vmem")
@@ -500,8 +546,8 @@ def test_vector_64bit_subtract_chains():
 def test_integer_clamp_saturates_and_saveexec_or():
     """VOP3 clamp on unsigned add/sub saturates to [0, 2^32 - 1] (the
     compiler uses it for max(a - b, 0)); without it the result wraps.
-    s_or_saveexec_b64 reads its source before writing the old EXEC there.
-    A modifier the VM does not model fails loudly."""
+    s_or_saveexec_b64 reads its source before writing the old EXEC there;
+    s_andn2_saveexec_b64 keeps the source lanes EXEC had off.  A modifier the VM does not model fails loudly."""
     vm = GcnVirtualMachine(104, 256, 64)
     vm.v[0] = np.array([5, 3, 0, 0xFFFFFFF0] * 16, dtype=np.uint32)
     vm.v[1] = np.array([3, 5, 1, 0x20] * 16, dtype=np.uint32)
@@ -516,6 +562,10 @@ def test_integer_clamp_saturates_and_saveexec_or():
     assert [int(vm.v[4][i]) for i in lanes] == [8, 8, 1, 0xFFFFFFFF] * 4
     assert [int(vm.v[5][i]) for i in lanes] == [0, 2, 1, 0] * 4
     assert vm.exec == 0x00000000FFFFFFFF and (vm.s[4], vm.s[5]) == (0xFFFF0000, 0)
+    # s_andn2_saveexec_b64: EXEC = S0 & ~EXEC, the old EXEC saved
+    vm.s[6], vm.s[7] = 0x00FF00FF, 0x1
+    vm.run("generated_gemm:\n s_andn2_saveexec_b64 s[8:9], s[6:7]\n s_endpgm\n")
+    assert vm.exec == 0x0000000100000000 and (vm.s[8], vm.s[9]) == (0xFFFFFFFF, 0) and vm.scc == 1
     with pytest.raises(NotImplementedError):
         GcnVirtualMachine(104, 256, 64).run("generated_gemm:\n v_add_u32_e64 v2, v0, v1 mul:2\n s_endpgm\n")
 
