@@ -111,11 +111,13 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
     # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
-    ((512, 512, 16384), "mt128x64_a16_wg2x2_dk16_s2"),
+    ((512, 512, 16384), "mt64x64_a16_wg1x4_dk32_s3"),
 ]
 # among launches that split K, the instance measured best for them (interleaved
-# runs at 512 x 512 x 16384: 114.5 TFLOP/s against 94.5 for the depth-32 one)
-SPLIT_INSTANCE = "mt128x64_a16_wg2x2_dk16_s2"
+# runs, host-chosen split counts: 125.6 / 127.5 / 114.8 TFLOP/s at 512^2 x 16384,
+# 1024 x 512 x 8192 and 256^2 x 65536, against 109.0 / 110.5 / 59.0 for
+# mt128x64_a16_wg2x2_dk16_s2 and 121.9 / 125.8 / 68.1 for the depth-32 128 x 64)
+SPLIT_INSTANCE = "mt64x64_a16_wg1x4_dk32_s3"
 
 
 def paths(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
