@@ -113,11 +113,23 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
     ((512, 512, 16384), "mt64x64_a16_wg1x4_dk32_s3"),
 ]
-# among launches that split K, the instance measured best for them (interleaved
-# runs, host-chosen split counts: 125.6 / 127.5 / 114.8 TFLOP/s at 512^2 x 16384,
-# 1024 x 512 x 8192 and 256^2 x 65536, against 109.0 / 110.5 / 59.0 for
-# mt128x64_a16_wg2x2_dk16_s2 and 121.9 / 125.8 / 68.1 for the depth-32 128 x 64)
-SPLIT_INSTANCE = "mt64x64_a16_wg1x4_dk32_s3"
+# Instances select() chooses among for other shapes, with the fraction of the
+# FP32 MFMA peak each reaches in its K loop on large problems (MI355X,
+# interleaved runs over 15 shapes from 768^3 to 8192^3).  The 64 x 64 one also
+# carries the split-K kernel: against mt128x64_a16_wg2x2_dk16_s2 it measured
+# 125.6 / 127.5 / 114.8 TFLOP/s at 512^2 x 16384, 1024 x 512 x 8192 and
+# 256^2 x 65536 (host-chosen split counts), against 109.0 / 110.5 / 59.0.
+CANDIDATES: Dict[str, float] = {
+    "mt256x256_a32_wg2x2_dk24_s3": 0.959,
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": 0.970,
+    "mt128x64_a16_wg2x2_dk32_s3": 0.967,
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": 0.966,
+    "mt64x64_a16_wg1x4_dk32_s3": 0.926,
+}
+# peak FP32 MFMA rate of one CU (157.3 TFLOP/s / 256) and the share of HBM
+# write bandwidth one CU's epilogue gets when all store at once (fitted)
+_CU_FLOPS = 157.3e12 / GFX950_COMPUTE_UNITS
+_CU_WRITE_BYTES_PER_S = 25e9
 
 
 def paths(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
@@ -180,26 +192,44 @@ def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_CO
     return max(1, min(s, ktiles))
 
 
+def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
+    """Time model behind select(): the CU with the most work-groups sets the
+    time (rounds of tiles x K splits over the CUs, each work-group a K loop at
+    the instance's MFMA efficiency plus its epilogue's stores), and a split
+    launch adds its partials' writes and the last work-group's reads.  Two
+    work-groups per CU (occ=2) hide half of each epilogue behind the other's
+    K loop.  Wave quantisation is the point: 3000^3 in 256 x 128 tiles is 288
+    work-groups, two rounds on 32 CUs, at half the speed of 64 x 64 tiles."""
+    cfg, opt = SOLUTIONS[name]
+    t0, t1 = cfg.tile_size
+    dk = cfg.depth_k
+    tiles = -(-m // t0) * -(-n // t1)
+    splits = auto_split(name, m, n, k, compute_units)
+    ktiles = -(-max(k, 1) // dk)
+    k_range = -(-ktiles // splits) * dk
+    rounds = -(-(tiles * splits) // compute_units)
+    occ = max(opt.occ, 1)
+    tile_bytes = t0 * t1 * 4
+    loop = 2.0 * t0 * t1 * k_range / (_CU_FLOPS * CANDIDATES.get(name, 0.9))
+    epilogue = tile_bytes / _CU_WRITE_BYTES_PER_S
+    reduce = 2.0 * splits * tile_bytes / _CU_WRITE_BYTES_PER_S if splits > 1 else 0.0
+    return rounds * (loop + epilogue / occ) + epilogue * (1.0 - 1.0 / occ) + reduce
+
+
 def select(m: int, n: int, k: int) -> str:
     """Instance for an (m, n, k) problem: the tuner's choice for a BASELINE
-    shape, else the tuned instance that best fills the GPU -- the most
-    work-groups (tiles times K splits) up to one per CU first, then no split
-    (and among split launches SPLIT_INSTANCE), then the least padding at the
-    edges, then the largest tile."""
+    shape, else the candidate with the least predicted time
+    (predicted_seconds; the larger tile among near ties)."""
     if m <= 0 or n <= 0:
         raise RuntimeError(f"empty problem {m}x{n}x{k}")
     for shape, name in PREFERRED:
         if shape == (m, n, k):
             return name
     best = None
-    for name in dict.fromkeys(nm for _, nm in PREFERRED):
+    for name in CANDIDATES:
         cfg, _ = SOLUTIONS[name]
         t0, t1 = cfg.tile_size
-        tx, ty = -(-m // t0), -(-n // t1)
-        fill = (m * n) / (tx * t0 * ty * t1)
-        splits = auto_split(name, m, n, k)
-        key = (min(tx * ty * splits, GFX950_COMPUTE_UNITS), splits == 1, splits > 1 and name == SPLIT_INSTANCE,
-               round(fill, 1), t0 * t1, vector_k(name, k))
-        if best is None or key > best[0]:
+        key = (predicted_seconds(name, m, n, k), -t0 * t1)
+        if best is None or key < best[0]:
             best = (key, name)
     return best[1]

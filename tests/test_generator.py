@@ -265,8 +265,42 @@ def test_cli_writes_co_and_toml(tmp_path):
 def test_select_prefers_tuned_and_divisible():
     for shape, name in catalog.PREFERRED:
         assert catalog.select(*shape) == name
-    # shapes outside the table: a tuned instance that fills the GPU and pads least
+    # shapes outside the table: a candidate of the time model
     assert catalog.divides(catalog.select(8192, 8192, 8192), 8192, 8192, 8192)
-    assert catalog.select(100, 70, 33) in dict(catalog.PREFERRED).values()
+    assert catalog.select(100, 70, 33) in catalog.CANDIDATES
     with pytest.raises(RuntimeError):
         catalog.select(0, 16, 16)
+
+
+# (shape, fastest candidate measured on MI355X in interleaved runs): the first
+# four are among the 15 shapes the efficiencies were fitted on, the others were
+# measured afterwards to check the model
+MEASURED_BEST = [
+    ((3000, 3000, 3000), "mt64x64_a16_wg1x4_dk32_s3"),           # 134.9 TFLOP/s; 256x128: 81
+    ((6144, 6144, 6144), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 151.3; 256x256: 110
+    ((8192, 8192, 8192), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.6
+    ((1536, 1536, 1536), "mt64x64_a16_wg1x4_dk32_s3"),           # 102.1; 128x64: 78
+    ((2500, 2500, 2500), "mt64x64_a16_wg1x4_dk32_s3"),           # 122.8 (not fitted on)
+    ((7000, 7000, 1000), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 139.3 (not fitted on)
+    ((4095, 4095, 4095), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.4 (not fitted on)
+    ((1792, 1792, 1792), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 109.3 (not fitted on)
+]
+
+
+@pytest.mark.parametrize("shape,name", MEASURED_BEST)
+def test_select_picks_the_measured_best(shape, name):
+    assert catalog.select(*shape) == name
+
+
+def test_time_model_counts_rounds_of_work_groups():
+    """Wave quantisation: one more tile than the CUs hold costs a whole extra
+    round, and splitting K fills a GPU that few tiles leave idle."""
+    nm = "mt256x256_a32_wg2x2_dk24_s3"
+    t_full = catalog.predicted_seconds(nm, 4096, 4096, 4104)          # 256 tiles: one round
+    t_over = catalog.predicted_seconds(nm, 4096 + 256, 4096, 4104)    # 272 tiles: two rounds
+    assert 1.9 < t_over / t_full < 2.1
+    sp = "mt64x64_a16_wg1x4_dk32_s3"
+    assert catalog.auto_split(sp, 512, 512, 16384) == 4
+    # 4 ranges of 4096 on 256 CUs against one range of 16384 on 64 CUs
+    assert catalog.predicted_seconds(sp, 512, 512, 16384) < 0.3 * (
+        2.0 * 64 * 64 * 16384 / (157.3e12 / 256 * catalog.CANDIDATES[sp]))
