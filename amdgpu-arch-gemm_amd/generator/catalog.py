@@ -106,7 +106,11 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 
 # shape class -> preferred instance (filled from tuner results; see select())
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
-    ((4096, 4096, 4096), "mt256x256_a32_wg2x2_dk24_s3"),
+    # two 256 x 128 work-groups per CU: each hides the other's prologue and
+    # epilogue (interleaved runs at 4096^3: 152.0 / 151.9 TFLOP/s against
+    # 150.9 / 151.0 for the 256 x 256 depth-24 instance, which held this row
+    # before)
+    ((4096, 4096, 4096), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
     ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
