@@ -251,6 +251,7 @@ EDGE_CASES = [  # (instance, m, n, k): partial tiles in M and N, K remainders, k
     ("mt128x64_a32_wg4x1_dk8_s3", 131, 123, 17), ("mt16x16_a16_wg1x1_dk16_s3_plr3", 15, 17, 48),
     ("mt64x64_a32_wg1x1_dk16", 63, 65, 48),
     ("mt256x128_a32_wg2x2_dk16", 250, 100, 40),  # the epilogue without an LDS stage
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", 300, 200, 37),  # the 4096^3 instance
 ]
 
 
@@ -282,6 +283,7 @@ VECTOR_CASES = [  # (instance, m, n, k, pad, misalign): every shape takes the ve
     ("mt64x64_a16_wg2x2_dk32_s3", 99, 70, 64, 1, 4), ("mt32x32_a32_wg1x1_dk16", 35, 59, 66, 1, 8),
     ("mt64x64_a16_wg2x2_dk32_s3_tn", 101, 70, 67, 3, 12), ("mt32x32_a32_wg1x1_dk16_tt", 37, 45, 50, 1, 4),
     ("mt16x16_a16_wg1x1_dk16_nt", 21, 37, 35, 2, 4), ("mt64x64_a16_wg2x2_dk32_s3", 64, 64, 97, 1, 0),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", 256, 128, 100, 0, 0),   # the 4096^3 instance, K remainder
 ]
 
 
