@@ -489,7 +489,7 @@ def test_split_k_errors(kernels):
 
 # ----------------------------------------------------------- random cases
 def _random_cases(count, seed):
-    """(instance, m, n, k, pads, alpha, beta, splits) drawn from every catalog instance."""
+    """(instance, m, n, k, pads, alpha, beta, splits, shift) drawn from every catalog instance."""
     rng = np.random.default_rng(seed)
     names = sorted(catalog.SOLUTIONS)
     cases = []
@@ -504,25 +504,27 @@ def _random_cases(count, seed):
         alpha = float(rng.choice([1.0, -0.5, 2.0]))
         beta = float(rng.choice([0.0, 1.0, -1.25]))
         splits = int(rng.choice([0, 2, 3, 16])) if opt.split_k != 1 else 1
-        cases.append((name, m, n, k, pads, alpha, beta, splits))
+        shift = int(rng.integers(0, 4))
+        cases.append((name, m, n, k, pads, alpha, beta, splits, shift))
     return cases
 
 
-@pytest.mark.parametrize("name,m,n,k,pads,alpha,beta,splits", _random_cases(40, 2024))
-def test_random_shapes_layouts_and_splits(kernels, name, m, n, k, pads, alpha, beta, splits):
+@pytest.mark.parametrize("name,m,n,k,pads,alpha,beta,splits,shift", _random_cases(40, 2024))
+def test_random_shapes_layouts_and_splits(kernels, name, m, n, k, pads, alpha, beta, splits, shift):
     """Seeded random problems over every catalog instance: any m, n, k (k = 0
-    included), padded leading dimensions, alpha/beta, transposed operands and
-    split counts, against the oracle; rows past m of D stay untouched."""
+    included), padded leading dimensions, alpha/beta, transposed operands,
+    split counts and pointers `shift` floats past a 16-byte boundary, against
+    the oracle; rows past m of D stay untouched."""
     cfg, _ = catalog.SOLUTIONS[name]
-    _say(f"random {name} {m}x{n}x{k} pads {pads} alpha {alpha} beta {beta} splits {splits}")
+    _say(f"random {name} {m}x{n}x{k} pads {pads} alpha {alpha} beta {beta} splits {splits} shift {shift}")
     ra, ca = (k, m) if cfg.trans_a else (m, k)
     rb, cb = (n, k) if cfg.trans_b else (k, n)
     lda, ldb, ldc, ldd = max(ra, 1) + pads[0], max(rb, 1) + pads[1], m + pads[2], m + pads[3]
     Af = S.fill_matrix(lda, max(ca, 1), 31, 0)
     Bf = S.fill_matrix(ldb, max(cb, 1), 31, 1)
     Cf = S.fill_matrix(ldc, n, 31, 2)
-    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
-    dD = S.DeviceBuffer.from_array(np.full((ldd, n), 9.5, dtype=np.float32))
+    (ba, dA), (bb, dB), (bc, dC) = (_shifted(x, shift) for x in (Af, Bf, Cf))
+    bd, dD = _shifted(np.full((ldd, n), 9.5, dtype=np.float32), shift)
     with _kernel(name) as kern:
         kern.set_split_k(splits)
         kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd)
