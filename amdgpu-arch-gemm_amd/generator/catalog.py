@@ -55,6 +55,11 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
                                         _opt(wgm=4, plr=3, xcd=8, occ=2, sk=0)),
     "mt256x128_a32_wg2x2_dk16_s3_occ2": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16, stages=2),
                                          _opt(wgm=4, plr=3, xcd=8, occ=2)),
+    # the same with the refill's memory instructions not interleaved one by one
+    # (plr=2): ahead at K = 256 (135.4 / 135.3 TFLOP/s against 132.0 / 132.9 at
+    # 8192 x 8192 x 256), behind at K = 512 and at 4096^3
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16, stages=2),
+                                              _opt(wgm=4, plr=2, xcd=8, occ=2)),
     "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
     "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
@@ -112,7 +117,7 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     # before)
     ((4096, 4096, 4096), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
-    ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
+    ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),
     ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3"),
     # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
     ((512, 512, 16384), "mt64x64_a16_wg1x4_dk32_s3"),
