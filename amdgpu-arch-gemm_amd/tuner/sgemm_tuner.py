@@ -15,8 +15,9 @@ stdout line) and print the best.  Additions:
   knobs depth_k {16,24,32} x vmem_stage {1,2} x wgm {1,4,8} x xcd {0,8} x plr {1,2,3}
   x prefetch depth {1,2}
   on the best ``--refine`` geometries (stage 2), optionally crossed with
-  ``--split-k`` (split-K kernel; 0 = split count chosen per problem) and
-  ``--occ`` (waves per SIMD the registers are capped for).  ``--space
+  ``--split-k`` (split-K kernel; 0 = split count chosen per problem);
+  ``--occ`` (waves per SIMD the registers are capped for, default 0 and 2)
+  applies to both stages.  ``--space
   reference`` is the reference's own 9-knob product.
 * every result is appended to ``<out>/results.jsonl`` and a rerun skips
   points already there (resume);
@@ -120,15 +121,19 @@ def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
     return cfg.num_bytes_per_buffer_load == (16, 16)
 
 
-def geometry_points(knobs: Dict, wide: bool = False) -> Iterable[Point]:
+def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,)) -> Iterable[Point]:
+    """Stage-1 candidates: every macro-tile x wave-group x atom geometry at the
+    default code-shape knobs, once per occupancy target in ``occs`` (a
+    geometry that only pays with two work-groups per CU -- the 4096^3 winner,
+    256 x 128 -- must reach stage 2 at that occupancy)."""
     tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
     groups = GFX950_WIDE_WAVE_GROUPS if wide else GFX950_WAVE_GROUPS
-    for (mt0, mt1), wg, mfma in product(tiles, groups, SUPPORTED_MFMAS):
+    for (mt0, mt1), wg, mfma, occ in product(tiles, groups, SUPPORTED_MFMAS, occs):
         if mt0 % (mfma[0] * wg[0]) or mt1 % (mfma[1] * wg[1]):
             continue
         wt = (mt0 // (mfma[0] * wg[0]), mt1 // (mfma[1] * wg[1]))
         p = make_point(mfma, wg, wt, knobs["depth_k"], knobs["vmem_stage"], knobs["wgm"], knobs["plr"], knobs["gw"],
-                       knobs["map_k_idx"], knobs["xcd"])
+                       knobs["map_k_idx"], knobs["xcd"], occ=occ)
         if p:
             yield p
 
@@ -314,7 +319,7 @@ def main(argv=None):
                     help="with --compile-only: build the stage-2 candidates of every geometry")
     ap.add_argument("--split-k", default="1",
                     help="comma-separated split-K values for stage 2 (0 = chosen per problem; default 1: no split)")
-    ap.add_argument("--occ", default="0",
+    ap.add_argument("--occ", default="0,2",
                     help="comma-separated occupancy targets for stage 2 (0 = compiler's choice; 2 = two waves per SIMD)")
     args = ap.parse_args(argv)
     m, n, k, out = args.m, args.n, args.k, args.output_folder
@@ -328,7 +333,7 @@ def main(argv=None):
     if args.space == "reference":
         stage1 = [p for p in reference_points() if fits(p[0], m, n, k)]
     else:
-        stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide")
+        stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide", occs=occs)
                   if fits(p[0], m, n, k)]
 
     if args.compile_only:

@@ -39,6 +39,18 @@ def test_gfx950_stage1_space():
     assert ((256, 256), (2, 2), (32, 32, 1, 2)) in got   # the headline geometry
 
 
+def test_stage1_tries_each_geometry_at_each_occupancy():
+    """With occs (0, 2) every geometry is a stage-1 candidate twice, so that
+    one that only pays with two work-groups per CU (the 4096^3 winner,
+    256 x 128) can reach stage 2; the CLI searches both by default."""
+    one = [T.point_key(*p) for p in T.geometry_points(T.DEFAULT_KNOBS)]
+    two = [T.point_key(*p) for p in T.geometry_points(T.DEFAULT_KNOBS, occs=(0, 2))]
+    assert set(one) < set(two)
+    assert sorted(k for k in two if not k.endswith("_occ2")) == sorted(one)
+    assert "a32_wg2x2_wt4x2_dk16_s2_wgm4_plr3_gw0_mk0_x8_occ2" in two
+
+
+
 def test_fits_skips_only_tiles_larger_than_the_problem():
     cfg, _ = T.make_point((32, 32, 1, 2), (2, 2), (4, 4), 16, 2, 4, 3, 0, 0, 8)
     assert T.fits(cfg, 256, 256, 16)
