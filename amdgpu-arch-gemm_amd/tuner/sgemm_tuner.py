@@ -17,7 +17,7 @@ stdout line) and print the best.  Additions:
   on the best ``--refine`` geometries (stage 2), optionally crossed with
   ``--split-k`` (split-K kernel; 0 = split count chosen per problem);
   ``--occ`` (waves per SIMD the registers are capped for, default 0 and 2)
-  applies to both stages.  ``--space
+  applies to both stages, and stage 1 tries depth_k 16 and 32.  ``--space
   reference`` is the reference's own 9-knob product.
 * every result is appended to ``<out>/results.jsonl`` and a rerun skips
   points already there (resume);
@@ -83,6 +83,8 @@ GFX950_XCD = [0, 8]
 GFX950_PLR = [1, 2, 3]
 GFX950_PD = [1, 2]
 DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=2, wgm=4, xcd=8, plr=3, gw=0, map_k_idx=0)
+# K depths every geometry is tried at in stage 1
+STAGE1_DEPTHS = (16, 32)
 ARCH = "gfx950"
 VERBOSE = False
 
@@ -121,18 +123,21 @@ def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
     return cfg.num_bytes_per_buffer_load == (16, 16)
 
 
-def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,)) -> Iterable[Point]:
+def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
+                    depths: Sequence[int] = (16,)) -> Iterable[Point]:
     """Stage-1 candidates: every macro-tile x wave-group x atom geometry at the
-    default code-shape knobs, once per occupancy target in ``occs`` (a
-    geometry that only pays with two work-groups per CU -- the 4096^3 winner,
-    256 x 128 -- must reach stage 2 at that occupancy)."""
+    default code-shape knobs, once per occupancy target in ``occs`` and K
+    depth in ``depths``: a geometry that only pays with two work-groups per
+    CU (the 4096^3 winner, 256 x 128) or with a deeper K tile (16x16x4 atoms:
+    128 x 64 runs 30% faster at depth 32 than at 16) must reach stage 2 at
+    that setting."""
     tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
     groups = GFX950_WIDE_WAVE_GROUPS if wide else GFX950_WAVE_GROUPS
-    for (mt0, mt1), wg, mfma, occ in product(tiles, groups, SUPPORTED_MFMAS, occs):
+    for (mt0, mt1), wg, mfma, occ, dk in product(tiles, groups, SUPPORTED_MFMAS, occs, depths):
         if mt0 % (mfma[0] * wg[0]) or mt1 % (mfma[1] * wg[1]):
             continue
         wt = (mt0 // (mfma[0] * wg[0]), mt1 // (mfma[1] * wg[1]))
-        p = make_point(mfma, wg, wt, knobs["depth_k"], knobs["vmem_stage"], knobs["wgm"], knobs["plr"], knobs["gw"],
+        p = make_point(mfma, wg, wt, dk, knobs["vmem_stage"], knobs["wgm"], knobs["plr"], knobs["gw"],
                        knobs["map_k_idx"], knobs["xcd"], occ=occ)
         if p:
             yield p
@@ -333,8 +338,8 @@ def main(argv=None):
     if args.space == "reference":
         stage1 = [p for p in reference_points() if fits(p[0], m, n, k)]
     else:
-        stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide", occs=occs)
-                  if fits(p[0], m, n, k)]
+        stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide", occs=occs,
+                                             depths=STAGE1_DEPTHS) if fits(p[0], m, n, k)]
 
     if args.compile_only:
         pts = list(stage1)

@@ -48,6 +48,9 @@ def test_stage1_tries_each_geometry_at_each_occupancy():
     assert set(one) < set(two)
     assert sorted(k for k in two if not k.endswith("_occ2")) == sorted(one)
     assert "a32_wg2x2_wt4x2_dk16_s2_wgm4_plr3_gw0_mk0_x8_occ2" in two
+    # and at each stage-1 depth: the 16x16x4 geometries need depth 32 to rank
+    deep = [T.point_key(*p) for p in T.geometry_points(T.DEFAULT_KNOBS, depths=T.STAGE1_DEPTHS)]
+    assert "a16_wg2x2_wt4x2_dk32_s2_wgm4_plr3_gw0_mk0_x8" in deep and set(one) < set(deep)
 
 
 
