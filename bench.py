@@ -47,10 +47,12 @@ WORKLOADS = {
     "cfg4": (8192, 8192, 256, 3, S.SGEMM_DIST_NORMAL),
     "cfg5": (16384, 128, 4096, 4, S.SGEMM_DIST_UNIFORM),
     # not a BASELINE.json config: few output tiles and a deep K, the case the
-    # split-K kernel exists for (32 tiles of 128 x 64 on 256 compute units)
+    # split-K kernel exists for (64 tiles of 64 x 64, 4 K ranges each, on 256
+    # compute units)
     "deepk": (512, 512, 16384, 5, S.SGEMM_DIST_UNIFORM),
 }
-HEADLINE_METRIC = "FP32 SGEMM TFLOP/s at 4096^3 NN; % of MI355X FP32 MFMA peak"
+# BASELINE.json's metric, verbatim
+HEADLINE_METRIC = "FP32 SGEMM TFLOP/s at 4096\u00b3 NN; % of MI355X FP32 MFMA peak"
 
 
 def log(msg: str):
