@@ -373,6 +373,28 @@ SPLIT_CASES = [
 ]
 
 
+SPLIT_UNALIGNED_CASES = [  # (instance, m, n, k, splits, pad, misalign)
+    ("mt32x32_a32_wg1x1_dk16_s3_sk4", 45, 37, 16 * 5 + 3, 3, 1, 4),   # last range's first tile element-wise
+    ("mt64x64_a16_wg1x4_dk32_s3", 67, 65, 32 * 4 + 6, 2, 3, 12),      # the split-K instance of the catalog
+    ("mt32x32_a32_wg1x1_dk16_sk4_tt", 35, 33, 16 * 4 + 9, 4, 1, 8),   # transposed operands
+]
+
+
+@pytest.mark.parametrize("name,m,n,k,splits,pad,misalign", SPLIT_UNALIGNED_CASES)
+def test_split_k_unaligned_in_vm(name, m, n, k, splits, pad, misalign):
+    """generated_gemm_splitk with odd leading dimensions, buffers starting
+    4-12 bytes past a 16-byte boundary and a K remainder that shifts the last
+    range's K origin: f64 parity with every buffer guarded, rows past m of D
+    untouched, tickets re-armed."""
+    prog, cfg = program(name, "generated_gemm_splitk")
+    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 8, pad)
+    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k),
+                        ldd=m + 2 + pad, splits=splits, misalign=misalign)
+    assert oracle.normwise_error(D[:m, :n], oracle.gemm_f64(opA, opB, C[:m, :n], 0.5, 1.5)) <= oracle.tolerance(k)
+    assert np.all(D[m:, :] == 0), "rows past m of D were written"
+    assert not info["tickets"].any()
+
+
 def _split_operands(cfg, m, n, k, seed, pad=0):
     """Stored A, B, C (each with ``pad`` extra rows: leading dimensions past the
     matrix) and op(A), op(B) as m x k and k x n."""
