@@ -122,23 +122,27 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
     ((512, 512, 16384), "mt64x64_a16_wg1x4_dk32_s3"),
 ]
-# Instances select() chooses among for other shapes, with the fraction of the
-# FP32 MFMA peak each reaches in its K loop on large problems (MI355X,
-# interleaved runs over 15 shapes from 768^3 to 8192^3).  The 64 x 64 one also
-# carries the split-K kernel: against mt128x64_a16_wg2x2_dk16_s2 it measured
-# 125.6 / 127.5 / 114.8 TFLOP/s at 512^2 x 16384, 1024 x 512 x 8192 and
-# 256^2 x 65536 (host-chosen split counts), against 109.0 / 110.5 / 59.0.
-CANDIDATES: Dict[str, float] = {
-    "mt256x256_a32_wg2x2_dk24_s3": 0.959,
-    "mt256x128_a32_wg2x2_dk16_s3_occ2": 0.970,
-    "mt128x64_a16_wg2x2_dk32_s3": 0.967,
-    "mt128x64_a16_wg2x2_dk32_s3_occ2": 0.966,
-    "mt64x64_a16_wg1x4_dk32_s3": 0.926,
+# Instances select() chooses among for other shapes: (fraction of the FP32
+# MFMA peak the K loop reaches, fixed seconds per tile), fitted by least
+# squares on log time to 41 shapes from 768^3 to 16384 x 8192 x 256 (MI355X,
+# interleaved runs; rms error 4.8%).  The plr=2 twin of the 256 x 128 instance
+# pays a smaller fixed cost for a slower loop: it wins below K ~ 480.  The
+# 64 x 64 one also carries the split-K kernel: against
+# mt128x64_a16_wg2x2_dk16_s2 it measured 125.6 / 127.5 / 114.8 TFLOP/s at
+# 512^2 x 16384, 1024 x 512 x 8192 and 256^2 x 65536 (host-chosen split
+# counts), against 109.0 / 110.5 / 59.0.
+CANDIDATES: Dict[str, Tuple[float, float]] = {
+    "mt256x256_a32_wg2x2_dk24_s3": (0.981, 0.0),
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": (0.985, 2.33e-6),
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": (0.961, 1.02e-6),
+    "mt128x64_a16_wg2x2_dk32_s3": (0.924, 0.0),
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": (0.940, 0.66e-6),
+    "mt64x64_a16_wg1x4_dk32_s3": (0.913, 0.0),
 }
 # peak FP32 MFMA rate of one CU (157.3 TFLOP/s / 256) and the share of HBM
 # write bandwidth one CU's epilogue gets when all store at once (fitted)
 _CU_FLOPS = 157.3e12 / GFX950_COMPUTE_UNITS
-_CU_WRITE_BYTES_PER_S = 25e9
+_CU_WRITE_BYTES_PER_S = 24.8e9
 
 
 def paths(name: str, kernel_dir: str = KERNEL_DIR) -> Tuple[str, str]:
@@ -204,7 +208,8 @@ def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_CO
 def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
     """Time model behind select(): the CU with the most work-groups sets the
     time (rounds of tiles x K splits over the CUs, each work-group a K loop at
-    the instance's MFMA efficiency plus its epilogue's stores), and a split
+    the instance's MFMA efficiency plus its fixed cost and its epilogue's
+    stores), and a split
     launch adds its partials' writes and the last work-group's reads.  Two
     work-groups per CU (occ=2) hide half of each epilogue behind the other's
     K loop.  Wave quantisation is the point: 3000^3 in 256 x 128 tiles is 288
@@ -219,7 +224,8 @@ def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GF
     rounds = -(-(tiles * splits) // compute_units)
     occ = max(opt.occ, 1)
     tile_bytes = t0 * t1 * 4
-    loop = 2.0 * t0 * t1 * k_range / (_CU_FLOPS * CANDIDATES.get(name, 0.9))
+    eff, fixed = CANDIDATES.get(name, (0.9, 0.0))
+    loop = 2.0 * t0 * t1 * k_range / (_CU_FLOPS * eff) + fixed
     epilogue = tile_bytes / _CU_WRITE_BYTES_PER_S
     reduce = 2.0 * splits * tile_bytes / _CU_WRITE_BYTES_PER_S if splits > 1 else 0.0
     return rounds * (loop + epilogue / occ) + epilogue * (1.0 - 1.0 / occ) + reduce

@@ -272,9 +272,10 @@ def test_select_prefers_tuned_and_divisible():
         catalog.select(0, 16, 16)
 
 
-# (shape, fastest candidate measured on MI355X in interleaved runs): the first
-# four are among the 15 shapes the efficiencies were fitted on, the others were
-# measured afterwards to check the model
+# (shape, fastest candidate measured on MI355X in interleaved runs).  The
+# model's parameters are fitted on these and 30 other shapes; an earlier,
+# one-parameter-per-instance version fitted on 15 shapes (the first four here
+# among them) already picked the next four before they were measured.
 MEASURED_BEST = [
     ((3000, 3000, 3000), "mt64x64_a16_wg1x4_dk32_s3"),           # 134.9 TFLOP/s; 256x128: 81
     ((6144, 6144, 6144), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 151.3; 256x256: 110
@@ -284,6 +285,9 @@ MEASURED_BEST = [
     ((7000, 7000, 1000), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 139.3 (not fitted on)
     ((4095, 4095, 4095), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.4 (not fitted on)
     ((1792, 1792, 1792), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 109.3 (not fitted on)
+    ((16384, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),  # 137.1; 128x64 occ2: 126.7
+    ((4096, 4096, 128), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),   # 108.5; 128x64 occ2: 103.0
+    ((8192, 8192, 512), "mt256x128_a32_wg2x2_dk16_s3_occ2"),        # 143.3; plr=2: 141.8
 ]
 
 
@@ -303,4 +307,4 @@ def test_time_model_counts_rounds_of_work_groups():
     assert catalog.auto_split(sp, 512, 512, 16384) == 4
     # 4 ranges of 4096 on 256 CUs against one range of 16384 on 64 CUs
     assert catalog.predicted_seconds(sp, 512, 512, 16384) < 0.3 * (
-        2.0 * 64 * 64 * 16384 / (157.3e12 / 256 * catalog.CANDIDATES[sp]))
+        2.0 * 64 * 64 * 16384 / (157.3e12 / 256 * catalog.CANDIDATES[sp][0]))
