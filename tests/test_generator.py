@@ -288,6 +288,10 @@ MEASURED_BEST = [
     ((16384, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),  # 137.1; 128x64 occ2: 126.7
     ((4096, 4096, 128), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),   # 108.5; 128x64 occ2: 103.0
     ((8192, 8192, 512), "mt256x128_a32_wg2x2_dk16_s3_occ2"),        # 143.3; plr=2: 141.8
+    # measured after the fit
+    ((5000, 5000, 300), "mt64x64_a16_wg1x4_dk32_s3"),              # 112.2; 256x128 plr=2: 99
+    ((2048, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),  # 125.9; plr=3: 123
+    ((6000, 3000, 2000), "mt128x64_a16_wg2x2_dk32_s3_occ2"),       # 141.0; 256x128: 108
 ]
 
 
