@@ -265,6 +265,8 @@ def test_cli_writes_co_and_toml(tmp_path):
 def test_select_prefers_tuned_and_divisible():
     for shape, name in catalog.PREFERRED:
         assert catalog.select(*shape) == name
+        # the time model alone reaches the same instances
+        assert min(catalog.CANDIDATES, key=lambda c: catalog.predicted_seconds(c, *shape)) == name
     # shapes outside the table: a candidate of the time model
     assert catalog.divides(catalog.select(8192, 8192, 8192), 8192, 8192, 8192)
     assert catalog.select(100, 70, 33) in catalog.CANDIDATES
