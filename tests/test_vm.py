@@ -501,6 +501,18 @@ def test_vm_buffer_range_check_is_per_dword():
     vm.run("generated_gemm:\n buffer_store_dwordx4 v[6:9], v1, s[8:11], 0 offen\n s_waitcnt vmcnt(0)\n s_endpgm\n")
     after = np.frombuffer(mem.read_bytes(0, 32), dtype=np.uint32).tolist()
     assert after == [1000, 1001, 1002, 7, 8, 1005, 1006, 1007]
+    # a register offset whose sum with the instruction's offset field passes
+    # 2^32 (a "negative" register part): which offset the hardware range-checks
+    # is not modelled, so the VM refuses it; the kernels write such offsets as
+    # one expression with no constant split off
+    vm.v[1] = np.full(64, 0xFFFFFFF8, dtype=np.uint32)
+    vm.exec = 0x1
+    with pytest.raises(NotImplementedError, match="past 32 bits"):
+        vm.run("generated_gemm:\n buffer_load_dword v2, v1, s[8:11], 0 offen offset:8\n s_endpgm\n")
+    # a lane outside EXEC does not count
+    vm.exec = 0x2
+    vm.v[1] = np.array([0xFFFFFFF8] + [0] * 63, dtype=np.uint32)
+    vm.run("generated_gemm:\n buffer_load_dword v2, v1, s[8:11], 0 offen offset:8\n s_waitcnt vmcnt(0)\n s_endpgm\n")
 
 
 def test_vm_atomics_and_lane_counts():
