@@ -102,7 +102,7 @@
 #define SG_OCC 0
 #endif
 #ifndef SG_GW
-#define SG_GW 0
+#define SG_GW 1
 #endif
 #ifndef SG_PAD_A
 #define SG_PAD_A 0
@@ -871,7 +871,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     constexpr int E_RUNS = SM / 4;            // float4 runs per column
     constexpr int E_PER_LANE = AT::N * E_RUNS / 64;
     static_assert(AT::N * E_RUNS % 64 == 0, "a column group is a whole number of float4s per lane");
-    if constexpr ((NT / 64) * E_CHUNK <= G::LDS_FLOATS) {
+    // SG_GW (the reference's global-write flavour, generator.py:2290-2508):
+    // 1 stages through LDS as above when the chunks fit, 0 always stores
+    // straight from the accumulators (no LDS, fewer live registers)
+    if constexpr (SG_GW != 0 && (NT / 64) * E_CHUNK <= G::LDS_FLOATS) {
         {
             // every wave's last K-loop access to LDS is behind this barrier
             __syncthreads();

@@ -5,6 +5,7 @@
 // wrapper both call it.
 
 #include "sgemm_shim.h"
+#include "sgemm_internal.hpp"
 
 #include <hip/hip_runtime_api.h>
 
@@ -315,7 +316,77 @@ struct sgemm_handle {
     uint32_t* tickets = nullptr;              // one per output tile, zero between launches
     size_t ticket_count = 0;
     int compute_units = 0;                    // of the device the module is loaded on
+    int device = 0;                           // the device current at sgemm_open
 };
+
+namespace sgemm_internal {
+
+int plan(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* splits, size_t* ws_bytes,
+         size_t* tiles) {
+    const sgemm_kernel_info& i = h->info;
+    *splits = effective_splits(i, h->compute_units, m, n, k);
+    *tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+             ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+    *ws_bytes = *splits > 1 ? *tiles * *splits * (size_t)i.tile_m * (size_t)i.tile_n * 4 : 0;
+    return SGEMM_OK;
+}
+
+int launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD, uint32_t m, uint32_t n,
+           uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd, float alpha, float beta,
+           const Workspace* ws) {
+    const sgemm_kernel_info& i = h->info;
+    KernArgs ka;
+    memset(&ka, 0, sizeof(ka));
+    ka.a = dA; ka.b = dB; ka.c = dC; ka.d = dD;
+    ka.m = m; ka.n = n; ka.k = k; ka.lda = lda; ka.ldb = ldb; ka.ldc = ldc; ka.ldd = ldd;
+    ka.alpha = alpha; ka.beta = beta;
+    ka.num_wg_x = (int32_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m);
+    ka.num_wg_y = (int32_t)((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+    const uint32_t splits = effective_splits(i, h->compute_units, m, n, k);
+    if (splits == 1) {
+        size_t size = sizeof(ka);
+        void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+        HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
+                                      (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+        return SGEMM_OK;
+    }
+    const size_t tiles = (size_t)ka.num_wg_x * (size_t)ka.num_wg_y;
+    const size_t ws_need = tiles * splits * (size_t)i.tile_m * (size_t)i.tile_n * 4;
+    if (!ws || !ws->partials || !ws->tickets || ws->partial_bytes < ws_need || ws->ticket_count < tiles)
+        return fail(SGEMM_E_INVALID, "split launch needs %zu bytes of partials and %zu tickets", ws_need, tiles);
+    KernArgsSplit ks;
+    memset(&ks, 0, sizeof(ks));
+    ks.base = ka;
+    ks.ws = ws->partials;
+    ks.tickets = ws->tickets;
+    ks.splits = splits;
+    size_t size = sizeof(ks);
+    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ks, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+    HIP_TRY(hipModuleLaunchKernel(h->function_splitk, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, splits,
+                                  (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+    return SGEMM_OK;
+}
+
+int check_launch(const sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD, uint32_t m,
+                 uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd, float beta) {
+    int r = sgemm_check_shape(h, m, n, k, lda, ldb, ldc, ldd);
+    if (r != SGEMM_OK) return r;
+    if (m == 0 || n == 0) return SGEMM_OK;
+    if (!dD || (k && (!dA || !dB)) || (beta != 0.0f && !dC))
+        return fail(SGEMM_E_INVALID, "sgemm_launch: null device pointer");
+    // buffer loads and stores need dword alignment only
+    if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 3u)
+        return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 4-byte aligned");
+    return SGEMM_OK;
+}
+
+hipStream_t stream(const sgemm_handle* h) { return h->stream; }
+
+int device(const sgemm_handle* h) { return h->device; }
+
+int set_error(int code, const char* message) { return fail(code, "%s", message); }
+
+}  // namespace sgemm_internal
 
 extern "C" {
 
@@ -374,6 +445,7 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
             h->compute_units = 0;
             (void)hipGetLastError();
         }
+        h->device = dev;
         if (h->info.split_k > h->info.split_k_max) {
             sgemm_close(h);
             return fail(SGEMM_E_CONFIG, "split_k = %d but %s has no generated_gemm_splitk", info.split_k, co_path);
@@ -509,34 +581,14 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
                  uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                  float alpha, float beta) {
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_launch: null handle");
-    int r = sgemm_check_shape(h, m, n, k, lda, ldb, ldc, ldd);
-    if (r != SGEMM_OK) return r;
-    if (m == 0 || n == 0) return SGEMM_OK;
-    if (!dD || (k && (!dA || !dB)) || (beta != 0.0f && !dC))
-        return fail(SGEMM_E_INVALID, "sgemm_launch: null device pointer");
-    // buffer loads and stores need dword alignment only
-    if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 3u)
-        return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 4-byte aligned");
-    const sgemm_kernel_info& i = h->info;
-    KernArgs ka;
-    memset(&ka, 0, sizeof(ka));
-    ka.a = dA; ka.b = dB; ka.c = dC; ka.d = dD;
-    ka.m = m; ka.n = n; ka.k = k; ka.lda = lda; ka.ldb = ldb; ka.ldc = ldc; ka.ldd = ldd;
-    ka.alpha = alpha; ka.beta = beta;
-    ka.num_wg_x = (int32_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m);
-    ka.num_wg_y = (int32_t)((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
-    const uint32_t splits = effective_splits(i, h->compute_units, m, n, k);
-    if (splits == 1) {
-        size_t size = sizeof(ka);
-        void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-        HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
-                                      (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
-        return SGEMM_OK;
-    }
+    int r = sgemm_internal::check_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, beta);
+    if (r != SGEMM_OK || m == 0 || n == 0) return r;
+    uint32_t splits = 1;
+    size_t ws_need = 0, tiles = 0;
+    sgemm_internal::plan(h, m, n, k, &splits, &ws_need, &tiles);
+    if (splits == 1) return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr);
     // split-K: partials of every (tile, split) plus one ticket per tile; both
     // buffers grow on demand and tickets start (and stay) zero
-    const size_t tiles = (size_t)ka.num_wg_x * (size_t)ka.num_wg_y;
-    const size_t ws_need = tiles * splits * (size_t)i.tile_m * (size_t)i.tile_n * 4;
     if (h->ws_bytes < ws_need || h->ticket_count < tiles) {
         HIP_TRY(hipStreamSynchronize(h->stream));
         if (h->ws_bytes < ws_need) {
@@ -556,17 +608,8 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
             h->ticket_count = tiles;
         }
     }
-    KernArgsSplit ks;
-    memset(&ks, 0, sizeof(ks));
-    ks.base = ka;
-    ks.ws = (float*)h->ws;
-    ks.tickets = h->tickets;
-    ks.splits = splits;
-    size_t size = sizeof(ks);
-    void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ks, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-    HIP_TRY(hipModuleLaunchKernel(h->function_splitk, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, splits,
-                                  (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
-    return SGEMM_OK;
+    const sgemm_internal::Workspace ws{(float*)h->ws, h->ws_bytes, h->tickets, h->ticket_count};
+    return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, &ws);
 }
 
 int sgemm_time(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,

@@ -3,8 +3,10 @@
 Each entry is one (GemmSolutionConfig, GemmOptimizations) pair that
 ``build_all`` compiles into ``kernels/<name>.co`` + ``kernels/<name>.toml``.
 ``select(m, n, k)`` returns the name to use for a problem: the instance the
-gfx950 tuner chose for that shape class, falling back to the largest tile that
-divides the problem.  The reference has no catalog: its tuner prints the best
+gfx950 tuner chose for a BASELINE shape (``PREFERRED``), else the member of
+``CANDIDATES`` with the least ``predicted_seconds`` -- a time model of wave
+quantisation over the compute units, per-tile fixed cost, epilogue stores and
+split-K partials.  The reference has no catalog: its tuner prints the best
 point and keeps nothing (sgemm_tuner.py:116-128).
 """
 from __future__ import annotations
@@ -28,7 +30,7 @@ def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=0, mapk=0, xcd=0, pd=1, occ=0, sk=1):
+def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1):
     return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk)
 
 
@@ -79,6 +81,10 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt128x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 16), _opt(wgm=4, xcd=8)),
     "mt128x128_a32_wg2x2_dk32": (_cfg(MFMA_32x32x2, (2, 2), (2, 2), 32), _opt(wgm=4, xcd=8)),
     "mt64x64_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (1, 1), 16), _opt(wgm=4, xcd=8)),
+    # the direct-store epilogue (gw=0): accumulators straight to D, no LDS staging
+    "mt64x64_a32_wg2x2_dk16_gw0": (_cfg(MFMA_32x32x2, (2, 2), (1, 1), 16), _opt(wgm=4, xcd=8, gw=0)),
+    "mt128x64_a16_wg2x2_dk32_s3_gw0": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
+                                       _opt(wgm=4, plr=3, xcd=8, gw=0, sk=0)),
     "mt128x64_a16_wg4x1_dk32": (_cfg(MFMA_16x16x4, (4, 1), (2, 4), 32), _opt(wgm=4, xcd=8)),
     "mt64x128_a32_wg2x2_dk16": (_cfg(MFMA_32x32x2, (2, 2), (1, 2), 16), _opt(xcd=8)),
     # variants that exercise every knob in the parity tests
@@ -184,9 +190,10 @@ def divides(name: str, m: int, n: int, k: int) -> bool:
 def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> int:
     """K ranges the host library uses for an instance built with split_k = 0
     (the rule of sgemm_set_split_k): none when the tiles fill the compute
-    units, else the s <= min(16, K tiles / 4) with the fewest rounds of
-    work-groups per unit of K work, ceil(tiles * s / CUs) / s (smallest s
-    among ties)."""
+    units, else the s <= min(MAX_SPLIT_K, K tiles / 4) with the fewest rounds
+    of work-groups per unit of K work, ceil(tiles * s / CUs) / s (smallest s
+    among ties); an instance built with a fixed split count uses that count.
+    Either way at most one range per K tile."""
     cfg, opt = SOLUTIONS[name]
     t0, t1 = cfg.tile_size
     tiles = -(-m // t0) * -(-n // t1)

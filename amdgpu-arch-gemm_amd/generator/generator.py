@@ -94,9 +94,14 @@ class GemmOptimizations:
                        with >= 3 LDS buffers, reads the next tile's first
                        operands before the barrier; 3 is 2 with the memory
                        instructions interleaved one by one between MFMAs.
-    * ``gw``        -- epilogue flavour: 0 stores straight from the
-                       accumulators, 1 is the same store path (kept for the
-                       reference's knob space; both paths are identical today).
+    * ``gw``        -- epilogue (global write) flavour, as the reference's
+                       ``gw_naive`` / ``gw_vgpr_minimized`` pair
+                       (generator.py:2290-2508): 0 stores straight from the
+                       accumulators (float4 per accumulator slot, 16 bytes in
+                       each of atom_n columns per instruction, no LDS); 1
+                       stages each MFMA column group through LDS and stores
+                       whole column runs (falls back to 0 when the staging
+                       chunks do not fit the kernel's LDS).
     * ``map_k_idx`` -- rotate the first K tile by ``tile_x & (map_k_idx - 1)``.
     * ``xcd``       -- (gfx950 only) number of XCDs to give contiguous tile
                        ranges to; 0 or 1 leaves the hardware order.

@@ -17,15 +17,20 @@ stdout line) and print the best.  Additions:
   on the best ``--refine`` geometries (stage 2), optionally crossed with
   ``--split-k`` (split-K kernel; 0 = split count chosen per problem);
   ``--occ`` (waves per SIMD the registers are capped for, default 0 and 2)
-  applies to both stages, and stage 1 tries depth_k 16 and 32.  ``--space
-  reference`` is the reference's own 9-knob product.
-* every result is appended to ``<out>/results.jsonl`` and a rerun skips
-  points already there (resume);
+  applies to both stages, and stage 1 tries depth_k 16 and 32 (``--stage1-depths``);
+  ``--gw`` adds the epilogue flavour to stage 2 and ``--tiles`` narrows stage
+  1's macro-tiles.  ``--space reference`` is the reference's own 9-knob product.
+* every result is appended to ``<out>/results.jsonl`` with the point's
+  ``source_sha`` (generated source, compiler and flags); a rerun skips points
+  already there with the same sha (resume) and rebuilds and re-times the
+  others, so an edited kernel is never timed from a stale code object;
 * each point runs in isolation: compile failures, runner failures and
   ``--timeout`` expiries are recorded and the sweep continues (the reference
   aborts on the first failing point, sgemm_tuner.py:121-123);
-* the winner is re-emitted as ``<out>/generated_gemm.co`` + ``.toml`` (the
-  reference overwrites one artifact per point and keeps none, :67, :107);
+* the fastest point that passes validation (the runner's validation_flag = 1
+  on the shape clipped to 1024 per dimension) is re-emitted as
+  ``<out>/generated_gemm.co`` + ``.toml`` (the reference overwrites one
+  artifact per point and keeps none, :67, :107);
 * ``--compile-only`` builds every candidate without a GPU; ``--no-compile``
   benchmarks candidates built earlier; ``--in-process`` times them through the
   ctypes shim instead of one runner process per point.
@@ -49,6 +54,8 @@ if _PKG not in sys.path:
     sys.path.insert(0, _PKG)
 
 from generator.generator import (  # noqa: E402
+    DEFAULT_HIPCC_PATH,
+    HIPCC_KERNEL_FLAGS,
     DataType,
     FunctionArgument,
     GemmOptimizations,
@@ -82,7 +89,8 @@ GFX950_WGM = [1, 4, 8]
 GFX950_XCD = [0, 8]
 GFX950_PLR = [1, 2, 3]
 GFX950_PD = [1, 2]
-DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=2, wgm=4, xcd=8, plr=3, gw=0, map_k_idx=0)
+GFX950_GW = [1, 0]
+DEFAULT_KNOBS = dict(depth_k=16, vmem_stage=2, wgm=4, xcd=8, plr=3, gw=1, map_k_idx=0)
 # K depths every geometry is tried at in stage 1
 STAGE1_DEPTHS = (16, 32)
 ARCH = "gfx950"
@@ -124,14 +132,15 @@ def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
 
 
 def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
-                    depths: Sequence[int] = (16,)) -> Iterable[Point]:
+                    depths: Sequence[int] = (16,), tiles: Optional[Sequence[Tuple[int, int]]] = None) -> Iterable[Point]:
     """Stage-1 candidates: every macro-tile x wave-group x atom geometry at the
     default code-shape knobs, once per occupancy target in ``occs`` and K
     depth in ``depths``: a geometry that only pays with two work-groups per
     CU (the 4096^3 winner, 256 x 128) or with a deeper K tile (16x16x4 atoms:
     128 x 64 runs 30% faster at depth 32 than at 16) must reach stage 2 at
-    that setting."""
-    tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
+    that setting.  ``tiles`` narrows the macro-tiles to the given list."""
+    if tiles is None:
+        tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
     groups = GFX950_WIDE_WAVE_GROUPS if wide else GFX950_WAVE_GROUPS
     for (mt0, mt1), wg, mfma, occ, dk in product(tiles, groups, SUPPORTED_MFMAS, occs, depths):
         if mt0 % (mfma[0] * wg[0]) or mt1 % (mfma[1] * wg[1]):
@@ -143,14 +152,17 @@ def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
             yield p
 
 
-def knob_points(cfg: GemmSolutionConfig, split_ks: Sequence[int] = (1,), occs: Sequence[int] = (0,)) -> Iterable[Point]:
+def knob_points(cfg: GemmSolutionConfig, split_ks: Sequence[int] = (1,), occs: Sequence[int] = (0,),
+                gws: Sequence[int] = (1,)) -> Iterable[Point]:
     """Stage-2 candidates of one geometry; ``split_ks`` and ``occs`` add the
-    gfx950-only split-K (0 = chosen per problem) and occupancy knobs."""
-    for dk, st, wgm, xcd, plr, pd, sk, occ in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM, GFX950_XCD,
-                                                      GFX950_PLR, GFX950_PD, split_ks, occs):
+    gfx950-only split-K (0 = chosen per problem) and occupancy knobs, ``gws``
+    the epilogue flavour (1: staged through LDS, 0: stores straight from the
+    accumulators)."""
+    for dk, st, wgm, xcd, plr, pd, sk, occ, gw in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM,
+                                                          GFX950_XCD, GFX950_PLR, GFX950_PD, split_ks, occs, gws):
         if pd == 2 and plr < 2:
             continue
-        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, 0, 0, xcd, pd, occ, sk)
+        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, gw, 0, xcd, pd, occ, sk)
         if p:
             yield p
 
@@ -172,16 +184,40 @@ def point_dir(out: str) -> str:
     return POINTS_DIR or os.path.join(out, "points")
 
 
+def point_source(p: Point) -> Tuple[str, str]:
+    """(HIP source, source_sha) of a point: the sha covers everything the code
+    object is built from -- the generated source (kernel template plus the
+    point's defines) and the compiler and its flags."""
+    cfg, opt = p
+    cfg.name = point_key(cfg, opt)
+    src = gemm(None, "generated_gemm", ARCH, cfg, opt, default_arguments())
+    h = hashlib.sha256()
+    for part in (src, DEFAULT_HIPCC_PATH, " ".join(HIPCC_KERNEL_FLAGS), ARCH):
+        h.update(part.encode())
+        h.update(b"\0")
+    return src, h.hexdigest()[:16]
+
+
+def built_sha(out: str, key: str) -> Optional[str]:
+    """source_sha recorded in a compiled point's .toml (None if absent)."""
+    co = os.path.join(point_dir(out), f"{key}.co")
+    toml = os.path.join(point_dir(out), f"{key}.toml")
+    if not (os.path.exists(co) and os.path.exists(toml)):
+        return None
+    return read_toml(toml).get("source_sha")
+
+
 def build_point(out: str, p: Point) -> Tuple[str, int]:
+    """Compiles one point unless an up-to-date build is there: a .co/.toml pair
+    whose source_sha matches the current source (an edit to the kernel
+    template, the generator's defines or the flags rebuilds it)."""
     cfg, opt = p
     key = point_key(cfg, opt)
     d = point_dir(out)
-    co = os.path.join(d, f"{key}.co")
-    if os.path.exists(co) and os.path.exists(os.path.join(d, f"{key}.toml")):
+    src, sha = point_source(p)
+    if built_sha(out, key) == sha:
         return key, 0
-    cfg.name = key
-    src = gemm(None, "generated_gemm", ARCH, cfg, opt, default_arguments())
-    rc = compile(key, src, ARCH, d, cfg, opt)
+    rc = compile(key, src, ARCH, d, cfg, opt, extra_keys={"source_sha": sha})
     hip = os.path.join(d, f"{key}.hip")
     if os.path.exists(hip):
         os.remove(hip)
@@ -265,19 +301,25 @@ def sweep(points: List[Point], out: str, m: int, n: int, k: int, bench, timeout:
     done = load_results(results_path)
     shape = f"{m}x{n}x{k}"
     recs = []
-    for cfg, opt in points:
+    for p in points:
+        cfg, opt = p
         key = point_key(cfg, opt)
+        _, sha = point_source(p)
         rkey = f"{shape}:{key}"
-        if rkey in done:
+        # resume only results of the same source: a record of an older kernel
+        # template, generator or flags is benchmarked again
+        if rkey in done and done[rkey].get("source_sha") == sha:
             recs.append(done[rkey])
             continue
         rec = {"key": rkey, "point": key, "shape": [m, n, k], "tile": list(cfg.tile_size), "mfma": list(cfg.mfma),
                "wave_group": list(cfg.wave_group), "wave_tiling": list(cfg.wave_tiling), "depth_k": cfg.depth_k,
-               "vmem_stage": cfg.vmem_stage, **opt.to_dict(), "gflops": 0.0, "status": "ok"}
+               "vmem_stage": cfg.vmem_stage, **opt.to_dict(), "source_sha": sha, "gflops": 0.0, "status": "ok"}
         co = os.path.join(point_dir(out), f"{key}.co")
         toml = os.path.join(point_dir(out), f"{key}.toml")
         if compiled.get(key, 0) != 0 or not os.path.exists(co):
             rec["status"] = "compile_error"
+        elif built_sha(out, key) != sha:
+            rec["status"] = "stale_build"   # built from other sources (--no-compile over an old build)
         elif spills(out, key):
             rec["status"] = "spills"
         else:
@@ -296,10 +338,75 @@ def sweep(points: List[Point], out: str, m: int, n: int, k: int, bench, timeout:
     return recs
 
 
-def emit_best(out: str, best: Dict):
+def validation_shape(m: int, n: int, k: int) -> Tuple[int, int, int]:
+    """The tuned shape clipped to at most 1024 per dimension: a CPU reference
+    GEMM of it takes about a second on a few host threads."""
+    return min(m, 1024), min(n, 1024), min(k, 1024)
+
+
+class RunnerValidator:
+    """The reference's check: the runner with validation_flag = 1 (its own CPU
+    GEMM; normwise 1e-5 * sqrt(K) and elementwise |gpu - cpu| < 1e-3) on
+    validation_shape(m, n, k)."""
+
+    def __init__(self, bench, m, n, k, timeout=600.0):
+        self.bench, self.shape, self.timeout = bench, validation_shape(m, n, k), timeout
+
+    def __call__(self, co, toml) -> Tuple[bool, str]:
+        m, n, k = self.shape
+        ret = subprocess.run([self.bench, co, toml, str(m), str(n), str(k), "0", "1", "1"], stdout=subprocess.PIPE,
+                             stderr=subprocess.STDOUT, timeout=self.timeout)
+        out = ret.stdout.decode(errors="replace")
+        ok = ret.returncode == 0 and "validation: PASS" in out
+        detail = [ln for ln in out.splitlines() if ln.startswith(("normwise", "# of mismatches", "validation"))]
+        return ok, f"{m}x{n}x{k}: " + "; ".join(detail)
+
+
+class ShimValidator:
+    """For --in-process sweeps without a runner executable: the kernel through
+    the C-ABI shim on validation_shape(m, n, k), against a float64 numpy GEMM
+    of the same seeded inputs, normwise bar 1e-5 * sqrt(K)."""
+
+    def __init__(self, m, n, k):
+        self.shape = validation_shape(m, n, k)
+
+    def __call__(self, co, toml) -> Tuple[bool, str]:
+        import numpy as np
+        from shim import sgemm_shim as S
+        m, n, k = self.shape
+        with S.Kernel(co, toml) as kern:
+            sa = (k, m) if kern.info.trans_a else (m, k)
+            sb = (n, k) if kern.info.trans_b else (k, n)
+            A = S.fill_matrix(*sa, 7, 0)
+            B = S.fill_matrix(*sb, 7, 1)
+            C = S.fill_matrix(m, n, 7, 2)
+            D, _ = kern.run(A, B, C, m, n, k, alpha=1.0, beta=1.0)
+            opA = A.T if kern.info.trans_a else A
+            opB = B.T if kern.info.trans_b else B
+        ref = opA.astype(np.float64) @ opB.astype(np.float64) + C.astype(np.float64)
+        err = float(np.max(np.abs(D - ref)) / max(np.max(np.abs(ref)), 1e-30))
+        tol = 1e-5 * max(k, 1) ** 0.5
+        return bool(err <= tol), f"{m}x{n}x{k}: normwise error vs float64 {err:.3e} (tolerance {tol:.3e})"
+
+
+def emit_best(out: str, recs: List[Dict], validate=None) -> Optional[Dict]:
+    """Copies the fastest point that passes ``validate(co, toml) -> (ok, detail)``
+    to <out>/generated_gemm.co + .toml and returns its record (None if no
+    point passes); a point that fails is marked and the next one tried."""
     src = point_dir(out)
-    for ext in ("co", "toml"):
-        shutil.copyfile(os.path.join(src, f"{best['point']}.{ext}"), os.path.join(out, f"generated_gemm.{ext}"))
+    for rec in sorted((r for r in recs if r["status"] == "ok" and r["gflops"] > 0), key=lambda r: -r["gflops"]):
+        co = os.path.join(src, f"{rec['point']}.co")
+        toml = os.path.join(src, f"{rec['point']}.toml")
+        if validate is not None:
+            ok, detail = validate(co, toml)
+            rec["validation"] = detail
+            print(f"validation of {rec['point']}: {'PASS' if ok else 'FAIL'} ({detail})", flush=True)
+            if not ok:
+                continue
+        for ext, path in (("co", co), ("toml", toml)):
+            shutil.copyfile(path, os.path.join(out, f"generated_gemm.{ext}"))
+        return rec
+    return None
 
 
 def main(argv=None):
@@ -326,10 +433,21 @@ def main(argv=None):
                     help="comma-separated split-K values for stage 2 (0 = chosen per problem; default 1: no split)")
     ap.add_argument("--occ", default="0,2",
                     help="comma-separated occupancy targets for stage 2 (0 = compiler's choice; 2 = two waves per SIMD)")
+    ap.add_argument("--gw", default="1",
+                    help="comma-separated epilogue flavours for stage 2 (1 = staged through LDS, 0 = direct stores)")
+    ap.add_argument("--tiles", default=None,
+                    help="comma-separated macro-tiles MT0xMT1 for stage 1 (default: the --space list)")
+    ap.add_argument("--stage1-depths", default=",".join(str(d) for d in STAGE1_DEPTHS),
+                    help="comma-separated K depths every stage-1 geometry is tried at")
     args = ap.parse_args(argv)
     m, n, k, out = args.m, args.n, args.k, args.output_folder
     split_ks = [int(x) for x in args.split_k.split(",") if x.strip()]
     occs = [int(x) for x in args.occ.split(",") if x.strip()]
+    gws = [int(x) for x in args.gw.split(",") if x.strip()]
+    depths = [int(x) for x in args.stage1_depths.split(",") if x.strip()]
+    tiles = None
+    if args.tiles:
+        tiles = [tuple(int(v) for v in t.lower().split("x")) for t in args.tiles.split(",") if t.strip()]
     os.makedirs(out, exist_ok=True)
     global POINTS_DIR
     POINTS_DIR = args.points_dir
@@ -339,13 +457,13 @@ def main(argv=None):
         stage1 = [p for p in reference_points() if fits(p[0], m, n, k)]
     else:
         stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide", occs=occs,
-                                             depths=STAGE1_DEPTHS) if fits(p[0], m, n, k)]
+                                             depths=depths, tiles=tiles) if fits(p[0], m, n, k)]
 
     if args.compile_only:
         pts = list(stage1)
         if args.all_shapes and args.space != "reference":
             for cfg, _ in stage1:
-                pts += [p for p in knob_points(cfg, split_ks, occs) if fits(p[0], m, n, k)]
+                pts += [p for p in knob_points(cfg, split_ks, occs, gws) if fits(p[0], m, n, k)]
         res = build_points(out, pts, args.jobs)
         bad = sum(1 for v in res.values() if v)
         print(f"compiled {len(res) - bad} of {len(res)} candidates into {point_dir(out)}")
@@ -369,7 +487,7 @@ def main(argv=None):
         seen = set(by_key)
         for r in ranked:
             cfg = by_key[r["point"]][0]
-            for p in knob_points(cfg, split_ks, occs):
+            for p in knob_points(cfg, split_ks, occs, gws):
                 kk = point_key(*p)
                 if kk not in seen and fits(p[0], m, n, k):
                     seen.add(kk)
@@ -380,8 +498,13 @@ def main(argv=None):
     if not ok:
         print("No valid configurations found.")
         return 1
-    best = max(ok, key=lambda r: r["gflops"])
-    emit_best(out, best)
+    # the emitted pair is checked first: the runner's own CPU validation when
+    # the --bench executable exists, else the shim against a float64 GEMM
+    validate = RunnerValidator(args.bench, m, n, k) if os.path.isfile(args.bench) else ShimValidator(m, n, k)
+    best = emit_best(out, recs, validate)
+    if best is None:
+        print("No configuration passed validation.")
+        return 1
     print(f"Best: {best['gflops']:.1f} Gflops ({best['gflops'] / 1e3 / 157.3 * 100:.1f}% of the FP32 MFMA peak), "
           f"MT: {tuple(best['tile'])}, DK: {best['depth_k']}, MI: {tuple(best['mfma'])}, wg: {tuple(best['wave_group'])}, "
           f"wgm: {best['wgm']}, plr: {best['plr']}, gw: {best['gw']}, map_k_idx: {best['map_k_idx']}, "

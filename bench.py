@@ -76,6 +76,19 @@ def read_traffic(kernel: str, workload: str):
         return None
 
 
+def host_cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
     """Times the reference cpuGemm (or the oracle port) on a column slice."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -102,6 +115,8 @@ def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
         "value": tflops,
         "unit": "TFLOP/s",
         "cores": 1,
+        "host_cpu": host_cpu_model(),
+        "host_cores": os.cpu_count(),
         "kind": kind,
         "sample": f"D[:, :{cols}] of the {m}x{n}x{k} workload (n={cols} columns), single thread, {t:.1f} s",
         "seconds": t,

@@ -356,6 +356,44 @@ def _sample_columns(n, count, seed):
     return np.array(sorted(cols))
 
 
+def test_baseline_config1_32cube(kernels):
+    """BASELINE.json config 1 on the GPU: 32^3, A and B U[-1,1) from seed 0,
+    C = 0, alpha = 1, beta = 0, one wave with the 32x32x2 atom (the
+    reference's one-wave 32 x 32 kernel, test_vm.py:539-627).  Every element
+    of D against a numpy float64 matmul and against the oracle cpuGemm; the
+    VM runs the same case on the CPU (tests/test_vm.py)."""
+    name = "mt32x32_a32_wg1x1_dk16"
+    m = n = k = 32
+    _say(f"config cfg1_32cube {m}x{n}x{k} seed 0 -> {name}")
+    A = S.fill_matrix(m, k, 0, 0)
+    B = S.fill_matrix(k, n, 0, 1)
+    C = np.zeros((m, n), dtype=np.float32)
+    with _kernel(name) as kern:
+        assert kern.tile[:2] == (32, 32) and kern.info.workitems == 64
+        D, _ = kern.run(A, B, C, m, n, k, alpha=1.0, beta=0.0)
+    _check(D, A.astype(np.float64) @ B.astype(np.float64), k, "cfg1 vs float64")
+    _check(D, oracle.cpu_gemm(A, B, C, 1.0, 0.0), k, "cfg1 vs cpuGemm")
+
+
+def test_baseline_config2_whole_d(kernels):
+    """BASELINE.json config 2 (1024^3, U[-1,1) seed 1, C zero-initialised,
+    alpha = 1, beta = 0) with the selected instance: every element of D
+    against the oracle cpuGemm (the reference's summation order), and the
+    oracle itself against float64, at the same bar."""
+    m = n = k = 1024
+    name = catalog.select(m, n, k)
+    _say(f"config cfg2 whole D {m}x{n}x{k} seed 1 -> {name}")
+    A = S.fill_matrix(m, k, 1, 0)
+    B = S.fill_matrix(k, n, 1, 1)
+    C = np.zeros((m, n), dtype=np.float32)
+    with _kernel(name) as kern:
+        D, _ = kern.run(A, B, C, m, n, k, alpha=1.0, beta=0.0)
+    ref = oracle.cpu_gemm_mt(A, B, C, 1.0, 0.0, threads=16)
+    err = _check(D, ref, k, "cfg2 whole D vs cpuGemm")
+    err64 = _check(D, A.astype(np.float64) @ B.astype(np.float64), k, "cfg2 whole D vs float64")
+    _say(f"  normwise error {err:.3e} (vs cpuGemm), {err64:.3e} (vs float64), tolerance {oracle.tolerance(k):.3e}")
+
+
 @pytest.mark.parametrize("cid,m,n,k,seed,dist", BASELINE_CONFIGS)
 def test_baseline_config(kernels, cid, m, n, k, seed, dist):
     """Each BASELINE.json GPU config with its selected instance: sampled columns
@@ -559,6 +597,8 @@ def test_generator_runner_validates(kernels):
     _say(out)
     assert ret.returncode == 0, out
     assert "validation: PASS" in out
+    # the reference's elementwise rule (|gpu - cpu| < 1e-3) over all m * n outputs
+    assert f"# of mismatches: 0/{1024 * 1024}\n" in out
     lines = out.split("\n")
     assert lines[-3].startswith("Gflops: ")  # what sgemm_tuner.py:115 parses
     assert float(lines[-3].split(":")[-1]) > 0

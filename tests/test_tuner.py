@@ -47,10 +47,10 @@ def test_stage1_tries_each_geometry_at_each_occupancy():
     two = [T.point_key(*p) for p in T.geometry_points(T.DEFAULT_KNOBS, occs=(0, 2))]
     assert set(one) < set(two)
     assert sorted(k for k in two if not k.endswith("_occ2")) == sorted(one)
-    assert "a32_wg2x2_wt4x2_dk16_s2_wgm4_plr3_gw0_mk0_x8_occ2" in two
+    assert "a32_wg2x2_wt4x2_dk16_s2_wgm4_plr3_gw1_mk0_x8_occ2" in two
     # and at each stage-1 depth: the 16x16x4 geometries need depth 32 to rank
     deep = [T.point_key(*p) for p in T.geometry_points(T.DEFAULT_KNOBS, depths=T.STAGE1_DEPTHS)]
-    assert "a16_wg2x2_wt4x2_dk32_s2_wgm4_plr3_gw0_mk0_x8" in deep and set(one) < set(deep)
+    assert "a16_wg2x2_wt4x2_dk32_s2_wgm4_plr3_gw1_mk0_x8" in deep and set(one) < set(deep)
 
 
 
@@ -79,44 +79,72 @@ def test_point_keys_distinguish_every_knob():
     assert any(k.endswith("_sk4") for k in keys) and any("_occ2" in k for k in keys)
 
 
-def _fake_points(out, keys, spilling=()):
+def _fake_points(out, pts, spilling=(), stale=()):
+    """Stand-in code objects for points, with the .toml keys the sweep reads
+    (source_sha of the current source unless the key is in ``stale``)."""
     d = T.point_dir(out)
     os.makedirs(d, exist_ok=True)
-    for k in keys:
+    for p in pts:
+        k = T.point_key(*p)
         open(os.path.join(d, f"{k}.co"), "wb").write(k.encode())
-        g.write_toml({"name": k, "scratch_bytes_per_lane": 64 if k in spilling else 0},
+        sha = "0" * 16 if k in stale else T.point_source(p)[1]
+        g.write_toml({"name": k, "scratch_bytes_per_lane": 64 if k in spilling else 0, "source_sha": sha},
                      os.path.join(d, f"{k}.toml"))
 
 
 def test_sweep_resumes_isolates_failures_and_emits_the_best(tmp_path, monkeypatch):
     out = str(tmp_path)
     monkeypatch.setattr(T, "POINTS_DIR", None)
-    pts = [T.make_point((32, 32, 1, 2), (2, 2), wt, 16, 2, 4, 3, 0, 0, 8) for wt in ((1, 1), (2, 2), (4, 4), (2, 1))]
+    pts = [T.make_point((32, 32, 1, 2), (2, 2), wt, 16, 2, 4, 3, 1, 0, 8)
+           for wt in ((1, 1), (2, 2), (4, 4), (2, 1), (1, 2), (2, 4))]
     keys = [T.point_key(*p) for p in pts]
-    _fake_points(out, keys[:3], spilling={keys[1]})
-    compiled = {keys[0]: 0, keys[1]: 0, keys[2]: 0, keys[3]: 1}   # the last failed to compile
+    _fake_points(out, [pts[i] for i in (0, 1, 2, 4, 5)], spilling={keys[1]}, stale={keys[5]})
+    compiled = {keys[0]: 0, keys[1]: 0, keys[2]: 0, keys[3]: 1, keys[4]: 0, keys[5]: 0}   # keys[3] failed to compile
     calls = []
+    speed = {keys[2]: 1234.5, keys[4]: 2000.0}
 
     def bench(co, toml, timeout):
         calls.append(os.path.basename(co))
         if "wt1x1" in co:
             raise RuntimeError("runner crashed")               # isolated, the sweep goes on
-        return 0, 1234.5
+        return 0, speed[os.path.basename(co)[:-3]]
 
     results = os.path.join(out, "results.jsonl")
     recs = T.sweep(pts, out, 256, 256, 64, bench, 10.0, results, compiled)
     status = {r["point"]: r["status"] for r in recs}
     assert status[keys[0]].startswith("error") and status[keys[1]] == "spills"
-    assert status[keys[2]] == "ok" and status[keys[3]] == "compile_error"
-    assert len(calls) == 2
+    assert status[keys[2]] == "ok" and status[keys[3]] == "compile_error" and status[keys[4]] == "ok"
+    assert status[keys[5]] == "stale_build"                    # built from another source: never timed
+    assert len(calls) == 3
+    assert all(r["source_sha"] == T.point_source(p)[1] for r, p in zip(recs, pts))
     # resume: nothing is benchmarked again, the records come back from the JSONL file
     recs2 = T.sweep(pts, out, 256, 256, 64, bench, 10.0, results, compiled)
-    assert len(calls) == 2 and [r["status"] for r in recs2] == [r["status"] for r in recs]
-    assert len(open(results).read().splitlines()) == 4
-    best = max((r for r in recs if r["status"] == "ok"), key=lambda r: r["gflops"])
-    T.emit_best(out, best)
+    assert len(calls) == 3 and [r["status"] for r in recs2] == [r["status"] for r in recs]
+    assert len(open(results).read().splitlines()) == 6
+    # a record of another source is not resumed: the point is timed again
+    lines = [json.loads(x) for x in open(results).read().splitlines()]
+    lines[2]["source_sha"] = "f" * 16
+    with open(results, "w") as f:
+        f.write("".join(json.dumps(x) + "\n" for x in lines))
+    T.sweep(pts, out, 256, 256, 64, bench, 10.0, results, compiled)
+    assert calls[3:] == [keys[2] + ".co"]
+    # emission: the fastest point that validates (keys[4] fails, keys[2] is next)
+    checked = []
+
+    def validate(co, toml):
+        checked.append(os.path.basename(co)[:-3])
+        return os.path.basename(co)[:-3] != keys[4], "fake check"
+
+    best = T.emit_best(out, recs, validate)
+    assert checked == [keys[4], keys[2]] and best["point"] == keys[2]
     assert open(os.path.join(out, "generated_gemm.co"), "rb").read() == keys[2].encode()
     assert g.read_toml(os.path.join(out, "generated_gemm.toml"))["name"] == keys[2]
+    assert T.emit_best(out, recs, lambda co, toml: (False, "no")) is None
+
+
+def test_validation_shape_is_clipped():
+    assert T.validation_shape(4096, 128, 4096) == (1024, 128, 1024)
+    assert T.validation_shape(300, 200, 100) == (300, 200, 100)
 
 
 def test_compile_only_builds_stage1_with_split_and_occupancy_knobs(tmp_path):

@@ -118,7 +118,7 @@ def test_reference_arange_cases_in_vm(case):
 
 @pytest.mark.parametrize("name", ["mt64x64_a32_wg2x2_dk16", "mt128x64_a32_wg4x1_dk8_s3", "mt64x64_a16_wg2x2_dk8",
                                   "mt16x16_a16_wg1x1_dk16_mapk4", "mt64x64_a32_wg1x1_dk16",
-                                  "mt128x64_a16_wg4x1_dk32"])
+                                  "mt128x64_a16_wg4x1_dk32", "mt64x64_a32_wg2x2_dk16_gw0"])
 def test_multi_wave_and_knob_variants_in_vm(name):
     _, cfg = program(name)
     t0, t1 = cfg.tile_size
@@ -513,6 +513,114 @@ def test_vm_buffer_range_check_is_per_dword():
     vm.exec = 0x2
     vm.v[1] = np.array([0xFFFFFFF8] + [0] * 63, dtype=np.uint32)
     vm.run("generated_gemm:\n buffer_load_dword v2, v1, s[8:11], 0 offen offset:8\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+
+
+# ------------------------------------------- memory instruction KATs
+# The reference's per-instruction memory tests (test_vm.py:187-407): buffer
+# loads and stores of 1, 2 and 4 dwords, LDS reads and writes of 32, 64 and
+# 128 bits, scalar loads of 1, 2 and 4 dwords.  Here every dword of every
+# lane is a distinct random word and lanes address memory through a random
+# permutation, so a swapped dword order, a wrong lane stride, a dropped dword
+# or a lane mix-up fails; a copy taken before the s_waitcnt must still hold
+# the old register value (results land at the wait), and lanes outside EXEC
+# neither load nor store.
+_WIDTHS = [(1, "dword", "b32"), (2, "dwordx2", "b64"), (4, "dwordx4", "b128")]
+
+
+def _words(count, seed):
+    return np.random.default_rng(seed).integers(0, 2 ** 32, size=count, dtype=np.uint64).astype(np.uint32)
+
+
+@pytest.mark.parametrize("nd,sfx,_", _WIDTHS)
+def test_buffer_load_widths_known_answer(nd, sfx, _):
+    stride = 4 * nd
+    words = _words(64 * nd, 10 + nd)
+    perm = np.random.default_rng(20 + nd).permutation(64)
+    vm = GcnVirtualMachine(104, 256, 64)
+    mem = V.Memory(8192, "vmem")
+    mem.allocate_region(4096, 64 * stride, "buf")
+    mem.write_bytes(4096, words.tobytes())
+    vm.vmem = mem
+    # base 16 bytes before the buffer; soffset 8 and the offset field 8 bring it back
+    vm.s[8], vm.s[9], vm.s[10], vm.s[11] = 4096 - 16, 0, 64 * stride + 16, 0x20000
+    vm.s[12] = 8
+    vm.v[0] = (perm * stride).astype(np.uint32)
+    vm.v[2:2 + nd] = 0xDEADBEEF
+    dst = f"v[2:{1 + nd}]" if nd > 1 else "v2"
+    vm.exec = 0xFFFF_FFFF_0000_FFFF
+    vm.run(f"generated_gemm:\n buffer_load_{sfx} {dst}, v0, s[8:11], s12 offen offset:8\n"
+           f" v_mov_b32 v30, v2\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    live = vm.exec_mask()
+    want = words.reshape(64, nd)[perm].T          # [dword][lane]
+    for i in range(nd):
+        assert np.array_equal(vm.v[2 + i][live], want[i][live]), i
+        assert np.all(vm.v[2 + i][~live] == 0xDEADBEEF), i
+    assert np.all(vm.v[30][live] == 0xDEADBEEF)   # read before the wait: the old value
+
+
+@pytest.mark.parametrize("nd,sfx,_", _WIDTHS)
+def test_buffer_store_widths_known_answer(nd, sfx, _):
+    stride = 4 * nd
+    words = _words(64 * nd, 30 + nd).reshape(nd, 64)
+    perm = np.random.default_rng(40 + nd).permutation(64)
+    vm = GcnVirtualMachine(104, 256, 64)
+    mem = V.Memory(8192, "vmem")
+    mem.allocate_region(4096, 64 * stride, "buf")
+    mem.write_bytes(4096, np.full(64 * nd, 0x5A5A5A5A, dtype=np.uint32).tobytes())
+    vm.vmem = mem
+    vm.s[8], vm.s[9], vm.s[10], vm.s[11] = 4096, 0, 64 * stride, 0x20000
+    vm.v[0] = (perm * stride).astype(np.uint32)
+    vm.v[2:2 + nd] = words
+    src = f"v[2:{1 + nd}]" if nd > 1 else "v2"
+    vm.exec = 0x0F0F_0F0F_FFFF_FFFF
+    vm.run(f"generated_gemm:\n buffer_store_{sfx} {src}, v0, s[8:11], 0 offen\n s_waitcnt vmcnt(0)\n s_endpgm\n")
+    got = np.frombuffer(mem.read_bytes(4096, 64 * stride), dtype=np.uint32).reshape(64, nd)
+    live = vm.exec_mask()
+    for lane in range(64):
+        slot = got[perm[lane]]
+        if live[lane]:
+            assert np.array_equal(slot, words[:, lane]), lane
+        else:
+            assert np.all(slot == 0x5A5A5A5A), lane
+
+
+@pytest.mark.parametrize("nd,_,sfx", _WIDTHS)
+def test_ds_write_then_read_widths_known_answer(nd, _, sfx):
+    stride = 4 * nd
+    words = _words(64 * nd, 50 + nd).reshape(nd, 64)
+    perm = np.random.default_rng(60 + nd).permutation(64)
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.v[0] = (perm * stride).astype(np.uint32)
+    vm.v[2:2 + nd] = words
+    src = f"v[2:{1 + nd}]" if nd > 1 else "v2"
+    dst = f"v[10:{9 + nd}]" if nd > 1 else "v10"
+    vm.run(f"generated_gemm:\n ds_write_{sfx} v0, {src} offset:64\n s_waitcnt lgkmcnt(0)\n s_endpgm\n")
+    lds = np.frombuffer(bytes(vm.lds.mem[64:64 + 64 * stride]), dtype=np.uint32).reshape(64, nd)
+    for lane in range(64):
+        assert np.array_equal(lds[perm[lane]], words[:, lane]), lane
+    # read back through a different permutation: lane l gets slot q[l]
+    q = np.random.default_rng(70 + nd).permutation(64)
+    vm.v[1] = (q * stride).astype(np.uint32)
+    vm.v[10:10 + nd] = 0xDEADBEEF
+    vm.run(f"generated_gemm:\n ds_read_{sfx} {dst}, v1 offset:64\n v_mov_b32 v30, v10\n"
+           f" s_waitcnt lgkmcnt(0)\n s_endpgm\n")
+    for i in range(nd):
+        assert np.array_equal(vm.v[10 + i], lds[q, i]), i
+    assert np.all(vm.v[30] == 0xDEADBEEF)
+
+
+@pytest.mark.parametrize("nd,sfx", [(1, "dword"), (2, "dwordx2"), (4, "dwordx4")])
+def test_s_load_widths_known_answer(nd, sfx):
+    words = _words(64, 80 + nd)
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.smem.write_bytes(0, words.tobytes())
+    vm.s[0], vm.s[1] = 32, 0               # pointer 32 bytes in, offset field 0x10
+    vm.s[4:4 + nd] = 0xDEADBEEF
+    dst = f"s[4:{3 + nd}]" if nd > 1 else "s4"
+    vm.run(f"generated_gemm:\n s_load_{sfx} {dst}, s[0:1], 0x10\n s_mov_b32 s30, s4\n"
+           f" s_waitcnt lgkmcnt(0)\n s_endpgm\n")
+    assert vm.s[4:4 + nd].tolist() == words[12:12 + nd].tolist()
+    assert vm.s[30] == 0xDEADBEEF
 
 
 def test_vm_atomics_and_lane_counts():
