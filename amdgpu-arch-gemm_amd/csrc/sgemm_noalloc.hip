@@ -1,0 +1,103 @@
+// sgemm_launch_noalloc: sgemm_launch for callers that cannot allocate device
+// memory (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc).  A split-K launch needs a workspace -- the tile partials and one
+// ticket per output tile -- which sgemm_launch allocates on the handle's first
+// launch that needs it; here it lives in a fixed device array, `scratch`,
+// compiled into this library, one copy per device, held until the process
+// ends.  Nothing on this path calls hipMalloc, hipFree or any allocating
+// routine.
+//
+// Host code never uses the array's name as a device address: the address of
+// each device's copy is looked up once, with that device current, through
+// hipGetSymbolAddress, and that pointer is what the kernels receive.
+
+#include "sgemm_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <mutex>
+
+namespace {
+
+constexpr size_t kTicketBytes = (size_t)SGEMM_NOALLOC_MAX_TILES * 4u;
+constexpr size_t kScratchBytes = (size_t)SGEMM_NOALLOC_PARTIAL_BYTES + kTicketBytes;
+
+// Split-K partials (the first SGEMM_NOALLOC_PARTIAL_BYTES bytes), then the
+// tickets.  Every call on a device shares that device's copy and leaves its
+// contents behind; tickets are cleared by every call that uses them.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Zeroes the tickets of one launch (a kernel rather than a memset, so that a
+// caller may capture the call in a HIP graph).
+__global__ void __launch_bounds__(256) clear_tickets(uint32_t* __restrict__ t, uint32_t count) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < count) t[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mutex;
+void* g_scratch[kMaxDevices];  // device address of each device's `scratch`, null until looked up
+
+// Address of `scratch` on device `dev`, looked up once per device with that
+// device current (the calling thread's current device is restored).
+int scratch_address(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return sgemm_internal::set_error(SGEMM_E_INVALID, "device id out of range");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    if (!g_scratch[dev]) {
+        int cur = 0;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void* p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            char msg[256];
+            snprintf(msg, sizeof(msg), "hipGetSymbolAddress(scratch) on device %d failed: %s (%d)", dev,
+                     hipGetErrorString(e), (int)e);
+            return sgemm_internal::set_error(e != hipSuccess ? (int)e : SGEMM_E_NO_DEVICE, msg);
+        }
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return SGEMM_OK;
+}
+
+}  // namespace
+
+extern "C" int sgemm_launch_noalloc(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                                    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                                    uint32_t ldd, float alpha, float beta) {
+    if (!h) return sgemm_internal::set_error(SGEMM_E_INVALID, "sgemm_launch_noalloc: null handle");
+    int r = sgemm_internal::check_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, beta);
+    if (r != SGEMM_OK || m == 0 || n == 0) return r;
+    uint32_t splits = 1;
+    size_t need = 0, tiles = 0;
+    sgemm_internal::plan(h, m, n, k, &splits, &need, &tiles);
+    if (splits == 1)  // generated_gemm uses no workspace
+        return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr);
+    if (need > (size_t)SGEMM_NOALLOC_PARTIAL_BYTES || tiles > (size_t)SGEMM_NOALLOC_MAX_TILES) {
+        char msg[256];
+        snprintf(msg, sizeof(msg),
+                 "sgemm_launch_noalloc: a %ux%ux%u launch in %u K ranges needs %zu bytes of partials for %zu tiles; "
+                 "the static scratch holds %u bytes and %u tiles", m, n, k, splits, need, tiles,
+                 (unsigned)SGEMM_NOALLOC_PARTIAL_BYTES, (unsigned)SGEMM_NOALLOC_MAX_TILES);
+        return sgemm_internal::set_error(SGEMM_E_SHAPE, msg);
+    }
+    void* base = nullptr;
+    if ((r = scratch_address(sgemm_internal::device(h), &base)) != SGEMM_OK) return r;
+    float* partials = static_cast<float*>(base);
+    uint32_t* tickets = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(base) + SGEMM_NOALLOC_PARTIAL_BYTES);
+    hipStream_t s = sgemm_internal::stream(h);
+    hipLaunchKernelGGL(clear_tickets, dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, s, tickets,
+                       (uint32_t)tiles);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        char msg[256];
+        snprintf(msg, sizeof(msg), "clear_tickets launch failed: %s (%d)", hipGetErrorString(e), (int)e);
+        return sgemm_internal::set_error((int)e, msg);
+    }
+    const sgemm_internal::Workspace ws{partials, (size_t)SGEMM_NOALLOC_PARTIAL_BYTES, tickets,
+                                       (size_t)SGEMM_NOALLOC_MAX_TILES};
+    return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, &ws);
+}

@@ -19,6 +19,9 @@ LIBRARY_PATH = os.path.join(_HERE, "libsgemm_shim.so")
 SGEMM_DIST_UNIFORM = 0
 SGEMM_DIST_NORMAL = 1
 SGEMM_DIST_ZERO = 2
+# static split-K scratch of sgemm_launch_noalloc (include/sgemm_shim.h)
+SGEMM_NOALLOC_PARTIAL_BYTES = 32 << 20
+SGEMM_NOALLOC_MAX_TILES = 16384
 
 # every symbol the header declares, with (restype, argtypes)
 _u32 = ctypes.c_uint32
@@ -65,6 +68,7 @@ SIGNATURES = {
     "sgemm_memcpy_d2h": (_int, [_vp, _vp, ctypes.c_size_t]),
     "sgemm_memset": (_int, [_vp, _int, ctypes.c_size_t]),
     "sgemm_launch": (_int, _LAUNCH_ARGS),
+    "sgemm_launch_noalloc": (_int, _LAUNCH_ARGS),
     "sgemm_time": (_int, _LAUNCH_ARGS + [_int, _int, ctypes.POINTER(_f32)]),
     "sgemm_time_each": (_int, _LAUNCH_ARGS + [_int, ctypes.POINTER(_f32)]),
     "sgemm_synchronize": (_int, [_vp]),
@@ -257,6 +261,12 @@ class Kernel:
     def launch(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, lda=None, ldb=None, ldc=None, ldd=None):
         _check("sgemm_launch", load_library().sgemm_launch(*self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd,
                                                                          alpha, beta)))
+
+    def launch_noalloc(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, lda=None, ldb=None, ldc=None, ldd=None):
+        """launch() without device allocation: a split launch works in the
+        library's static per-device scratch (calls on one device must not overlap)."""
+        _check("sgemm_launch_noalloc", load_library().sgemm_launch_noalloc(
+            *self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta)))
 
     def time(self, a, b, c, d, m, n, k, alpha=1.0, beta=0.0, warmup=1, runs=10,
              lda=None, ldb=None, ldc=None, ldd=None) -> float:

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 3
+#define SGEMM_SHIM_ABI_VERSION 4
 
 /* Most K ranges generated_gemm_splitk splits one output tile into. */
 #define SGEMM_MAX_SPLIT_K 16
@@ -152,6 +152,27 @@ int sgemm_memset(void* dptr, int value, size_t bytes);
 int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
                  uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                  float alpha, float beta);
+
+/* Static split-K scratch of sgemm_launch_noalloc: bytes of tile partials and
+ * output tiles (one ticket each) one launch may use. */
+#define SGEMM_NOALLOC_PARTIAL_BYTES (32u << 20)
+#define SGEMM_NOALLOC_MAX_TILES 16384u
+
+/* sgemm_launch without any device allocation.  No counterpart in the
+ * reference (its kernel needs no workspace); it is for callers that cannot
+ * call hipMalloc: code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation.  Same arguments, checks and results as sgemm_launch
+ * (bit-identical D for the same handle settings); a split launch takes its
+ * partials and tickets from a fixed device array compiled into this library
+ * (SGEMM_NOALLOC_PARTIAL_BYTES + 4 * SGEMM_NOALLOC_MAX_TILES bytes per device,
+ * held until the process ends) instead of the handle's workspace, and clears
+ * the tickets it uses with a kernel on the handle's stream.  A launch needing
+ * more partial bytes or tiles than that returns SGEMM_E_SHAPE.  Every call on
+ * a device shares that device's array: calls that overlap on one device (two
+ * streams, two handles, two threads) race and must be ordered by the caller. */
+int sgemm_launch_noalloc(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
+                         uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                         float alpha, float beta);
 
 /* `warmup` untimed launches, then `runs` launches bracketed by HIP events on
  * the handle's stream; *total_ms is the event time of all `runs` launches.

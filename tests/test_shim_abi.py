@@ -34,8 +34,16 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 3
+    assert lib.sgemm_abi_version() == 4
     assert ctypes.sizeof(S.KernelInfo) == 4 * 19  # 19 ints, as in sgemm_kernel_info
+
+
+def test_noalloc_limits_match_the_header():
+    text = open(HEADER).read()
+    got = {k: eval(v.replace("u", ""), {}) for k, v in
+           re.findall(r"#define (SGEMM_NOALLOC_[A-Z_]+) \(?([0-9u <]+)\)?", text)}
+    assert got == {"SGEMM_NOALLOC_PARTIAL_BYTES": S.SGEMM_NOALLOC_PARTIAL_BYTES,
+                   "SGEMM_NOALLOC_MAX_TILES": S.SGEMM_NOALLOC_MAX_TILES}
 
 
 def test_no_device_is_an_error_code_not_a_crash(tmp_path):
@@ -82,6 +90,8 @@ def test_null_arguments_are_rejected():
     size = ctypes.c_size_t()
     assert lib.sgemm_workspace_size(None, 64, 64, 64, ctypes.byref(size)) == -1
     assert lib.sgemm_launch_splits(None, 64, 64, 64, None) == -1
+    assert lib.sgemm_launch_noalloc(None, None, None, None, None, 64, 64, 16, 64, 16, 64, 64, 1.0, 0.0) == -1
+    assert b"null handle" in lib.sgemm_last_error()
 
 
 def test_runner_usage_error_exit_code():

@@ -1,0 +1,96 @@
+"""sgemm_launch_noalloc (the entry point that allocates nothing) on the GPU.
+
+It must give what sgemm_launch gives -- the same kernels with the same split
+count, so D is bit-identical -- on two calls in a row, the second with a
+smaller problem (the static scratch keeps the first call's partials and
+tickets), and must reject a launch whose partials exceed the scratch before
+launching anything.  Every call goes through the C-ABI (ctypes).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from generator import catalog
+from shim import sgemm_shim as S
+
+pytestmark = pytest.mark.gpu
+
+NAME = "mt64x64_a16_wg1x4_dk32_s3"   # carries generated_gemm_splitk; split count chosen per problem
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _kernel():
+    co, toml = catalog.paths(NAME)
+    return S.Kernel(co, toml)
+
+
+def _problem(m, n, k, seed):
+    A, B, C = S.fill_matrix(m, k, seed, 0), S.fill_matrix(k, n, seed, 1), S.fill_matrix(m, n, seed, 2)
+    return A, B, C, [S.DeviceBuffer.from_array(x) for x in (A, B, C)]
+
+
+def _d(kern, launch, bufs, m, n, k, alpha, beta):
+    dA, dB, dC = bufs
+    dD = S.DeviceBuffer(4 * m * n)
+    dD.upload(np.full((m, n), np.nan, dtype=np.float32))
+    getattr(kern, launch)(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
+    kern.synchronize()
+    return dD.download().reshape(n, m).T.copy()
+
+
+@pytest.mark.parametrize("first,second", [
+    ((512, 512, 16384), (256, 256, 4096)),     # 4 then 16 K ranges: the second call is smaller
+    ((333, 290, 5003), (70, 45, 1001)),       # ragged tiles and K remainders
+])
+def test_noalloc_matches_launch_on_two_calls(kernels, first, second):
+    with _kernel() as ref_kern, _kernel() as kern:
+        for i, (m, n, k) in enumerate((first, second)):
+            splits = kern.launch_splits(m, n, k)
+            _say(f"noalloc call {i + 1}: {NAME} {m}x{n}x{k}, {splits} K ranges")
+            assert splits > 1, "the case must exercise the split-K scratch"
+            A, B, C, bufs = _problem(m, n, k, 31 + i)
+            D = _d(kern, "launch_noalloc", bufs, m, n, k, 0.5, -1.0)
+            D_ref = _d(ref_kern, "launch", bufs, m, n, k, 0.5, -1.0)
+            assert np.array_equal(D, D_ref), "sgemm_launch_noalloc and sgemm_launch differ"
+            err = oracle.normwise_error(D, oracle.cpu_gemm_mt(A, B, C, 0.5, -1.0, threads=16))
+            assert err <= oracle.tolerance(k), err
+
+
+def test_noalloc_without_split_and_repeated(kernels):
+    """An unsplit launch needs no workspace at all; repeated split calls on
+    one device give the same bits (tickets are cleared by each call)."""
+    with _kernel() as kern:
+        m, n, k = 1024, 1024, 256                # 256 tiles fill the 256 CUs: no split
+        _say(f"noalloc no split {m}x{n}x{k}")
+        assert kern.launch_splits(m, n, k) == 1
+        _, _, _, bufs = _problem(m, n, k, 41)
+        assert np.array_equal(_d(kern, "launch_noalloc", bufs, m, n, k, 1.0, 1.0),
+                              _d(kern, "launch", bufs, m, n, k, 1.0, 1.0))
+        m, n, k = 128, 192, 8192
+        _say(f"noalloc repeated {m}x{n}x{k}, {kern.launch_splits(m, n, k)} K ranges")
+        _, _, _, bufs = _problem(m, n, k, 42)
+        first = _d(kern, "launch_noalloc", bufs, m, n, k, 1.0, 0.0)
+        for _ in range(3):
+            assert np.array_equal(_d(kern, "launch_noalloc", bufs, m, n, k, 1.0, 0.0), first)
+
+
+def test_noalloc_rejects_more_than_its_scratch(kernels):
+    """1024^2 in 64 x 64 tiles with 16 K ranges needs 256 * 16 * 16 KiB = 64 MiB
+    of partials, twice the static scratch: an error, and D is untouched."""
+    with _kernel() as kern:
+        kern.set_split_k(16)
+        m = n = 1024
+        k = 16 * 32 * 4
+        need = kern.workspace_size(m, n, k)
+        _say(f"noalloc oversize {m}x{n}x{k}: {need} bytes")
+        assert need > S.SGEMM_NOALLOC_PARTIAL_BYTES
+        _, _, _, (dA, dB, dC) = _problem(m, n, k, 43)
+        dD = S.DeviceBuffer(4 * m * n)
+        dD.upload(np.full((m, n), 3.0, dtype=np.float32))
+        with pytest.raises(S.SgemmError, match="static scratch"):
+            kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.0, beta=0.0)
+        kern.synchronize()
+        assert np.all(dD.download() == 3.0)
