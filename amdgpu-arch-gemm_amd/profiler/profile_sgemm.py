@@ -13,7 +13,7 @@ tracing, and no pass asks for more than the hardware collects at once):
   2. --pmc FETCH_SIZE                HBM read KiB per dispatch
   3. --pmc WRITE_SIZE                HBM write KiB per dispatch
   4. --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES
-                                     MFMA utilisation and the effective clock
+                                     MFMA utilisation and the shader clock
   5. --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE
   6./7. FETCH_SIZE and WRITE_SIZE of copy_probe (a plain copy of a known byte
      count), whose ratio to the true bytes scales the SGEMM's counters.
@@ -21,6 +21,26 @@ tracing, and no pass asks for more than the hardware collects at once):
 The summary (markdown) lists the commands and the figures; a one-line
 ``<kernel>_<workload>_traffic.txt`` next to it carries the scaled HBM bytes per
 launch that bench.py reports as roofline.traffic.
+
+How the MFMA figures are derived (all per dispatch, medians over the
+dispatches after the first):
+  * SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs is compared with the ideal
+    MFMA cycle count, 2MNK / (64 FLOP per SIMD-cycle); a ratio of 1 says every
+    MFMA cycle issued is useful work.
+  * SQ_BUSY_CYCLES is summed over the shader engines (the agent's Array_Count,
+    32 on MI355X): divided by them it is the cycles the kernel kept each
+    engine busy.  MfmaUtil = MFMA busy cycles per SIMD / busy cycles per
+    engine, both from the same dispatch, so no timestamp enters it.
+  * The shader clock is busy cycles per engine over the same PMC dispatch's
+    duration (a lower bound if the engines idle inside that window); a clock
+    above the agent's maximum engine clock marks the figure invalid.  Counter
+    collection serialises dispatches, so a PMC dispatch runs a few
+    microseconds longer than the same kernel back to back; the kernel-trace
+    pass gives the unperturbed duration and achieved rate, and the busy
+    cycles are also shown as time at the maximum clock for comparison.
+  * GRBM_GUI_ACTIVE is reported only as the counter window: it covers the
+    profiler's own work around a dispatch as well, so for short kernels it
+    overstates the kernel's cycles (it read 2.9 GHz over a 20 us dispatch).
 """
 from __future__ import annotations
 
@@ -122,11 +142,13 @@ def kernel_stats(csv_path, kernel_substr):
 
 
 def gpu_agent(out_dir):
-    """(XCD count, CU count, SIMD count) of the GPU agent from rocprofv3's agent info."""
+    """(XCD count, CU count, SIMD count, shader engine count, max engine clock MHz)
+    of the GPU agent from rocprofv3's agent info."""
     with open(find(out_dir, "run_agent_info.csv")) as f:
         for row in csv.DictReader(f):
             if row.get("Agent_Type") == "GPU":
-                return int(row["Num_Xcc"]), int(row["Cu_Count"]), int(row["Simd_Count"])
+                return (int(row["Num_Xcc"]), int(row["Cu_Count"]), int(row["Simd_Count"]), int(row["Array_Count"]),
+                        float(row["Max_Engine_Clk_Fcompute"]))
     raise RuntimeError(f"no GPU agent in {out_dir}")
 
 
@@ -146,6 +168,8 @@ def main():
                     help="untimed runner launches first (default: about 0.1 s of the workload, so the "
                          "engine clock has ramped up before the dispatches the medians describe)")
     ap.add_argument("--cus", type=int, default=256)
+    ap.add_argument("--analyze-only", action="store_true",
+                    help="derive the summary from the rocprofv3 output already in --out (no GPU work)")
     args = ap.parse_args()
 
     m, n, k, seed, dist = WORKLOADS[args.workload]
@@ -156,8 +180,12 @@ def main():
     probe = [PROBE, str(PROBE_BYTES), "3"]
     cmds = {}
 
+    def profile(pass_args, out_dir, program, timeout):
+        if not args.analyze_only:
+            rocprof(pass_args, out_dir, program, timeout)
+
     d = os.path.join(args.out, "trace")
-    rocprof(["--kernel-trace", "--stats"], d, runner, 300)
+    profile(["--kernel-trace", "--stats"], d, runner, 300)
     cmds["trace"] = "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o run -- " + " ".join(
         os.path.relpath(c, ROOT) if os.path.isabs(c) else c for c in runner)
     ks = kernel_stats(find(d, "run_kernel_stats.csv"), "generated_gemm")
@@ -171,7 +199,7 @@ def main():
     values = {}
     for key, counters in passes.items():
         d = os.path.join(args.out, f"pmc_{key}")
-        rocprof(["--pmc", *counters], d, runner, 120)
+        profile(["--pmc", *counters], d, runner, 120)
         cmds[key] = f"rocprofv3 --pmc {' '.join(counters)} --output-format csv -d <out>/pmc_{key} -o run -- <runner>"
         per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "generated_gemm")
         for c in counters:
@@ -182,11 +210,11 @@ def main():
     probe_vals = {}
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
         d = os.path.join(args.out, f"probe_{c.lower()}")
-        rocprof(["--pmc", c], d, probe, 120)
+        profile(["--pmc", c], d, probe, 120)
         per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "copy_probe")
         probe_vals[c] = per[c]
 
-    xcc, cus, simds = gpu_agent(os.path.join(args.out, "pmc_mfma"))
+    xcc, cus, simds, engines, max_mhz = gpu_agent(os.path.join(args.out, "pmc_mfma"))
     med = {c: steady(v) for c, v in values.items()}
     probe_kib = PROBE_BYTES / 1024.0
     fetch_scale = probe_kib / statistics.median(probe_vals["FETCH_SIZE"])
@@ -197,14 +225,27 @@ def main():
     avg_s = steady(trace_durations(os.path.join(args.out, "trace"), "generated_gemm"))
     flops = 2.0 * m * n * k
     alg_bytes = 4.0 * (m * k + k * n + m * n)
-    # GRBM_GUI_ACTIVE is reported summed over the XCDs: divide for per-XCD cycles.
-    mfma = [(b, a / xcc, dur) for b, a, dur in zip(values["SQ_VALU_MFMA_BUSY_CYCLES"], values["GRBM_GUI_ACTIVE"],
-                                                   values["duration_s_mfma"])]
-    mfma_util = 100.0 * steady([b / (a * simds) for b, a, _ in mfma])
-    clock_mhz = steady([a / dur / 1e6 for _, a, dur in mfma])
-    lds_rate = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
     tflops = flops / avg_s / 1e12
+    # MFMA cycles per SIMD: measured, and the ideal at 64 FLOP per SIMD-cycle
+    ideal_per_simd = flops / 64.0 / simds
+    busy_per_simd = med["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+    # per dispatch of the PMC pass: shader-busy cycles per engine, MfmaUtil and
+    # the clock over that dispatch's own duration
+    disp = list(zip(values["SQ_VALU_MFMA_BUSY_CYCLES"], values["SQ_BUSY_CYCLES"], values["GRBM_GUI_ACTIVE"],
+                    values["duration_s_mfma"]))
+    sq_per_engine = steady([q / engines for _, q, _, _ in disp])
+    mfma_util = 100.0 * steady([(b / simds) / (q / engines) for b, q, _, _ in disp])
+    clock_pmc_mhz = steady([q / engines / dur / 1e6 for _, q, _, dur in disp])
+    pmc_dur = steady([dur for _, _, _, dur in disp])
+    gui_window_mhz = steady([a / xcc / dur / 1e6 for _, _, a, dur in disp])
+    clock_mhz = clock_pmc_mhz
+    clock_ok = clock_mhz <= max_mhz
+    tflops_pmc = flops / pmc_dur / 1e12
     clock_peak = cus * 256 * clock_mhz * 1e6 / 1e12
+    busy_us_at_max = sq_per_engine / max_mhz            # the engine-busy cycles at the maximum clock, in us
+    lds_rate = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
+    valid = "valid" if clock_ok else f"INVALID (above the {max_mhz:.0f} MHz maximum)"
+    util_check = "holds" if mfma_util >= 100.0 * tflops_pmc / PEAK_TFLOPS - 1e-9 else "FAILS"
 
     summary = args.summary or os.path.join(args.out, "summary.md")
     os.makedirs(os.path.dirname(os.path.abspath(summary)), exist_ok=True)
@@ -230,10 +271,19 @@ def main():
         f"{ks['min_ns'] / 1e3:.2f} us / {ks['max_ns'] / 1e3:.2f} us |",
         f"| kernel-trace duration, median after the first dispatch | {avg_s * 1e6:.2f} us |",
         f"| achieved (median duration) | {tflops:.2f} TFLOP/s = {100 * tflops / PEAK_TFLOPS:.1f}% of {PEAK_TFLOPS} (nominal) |",
-        f"| effective clock (GRBM_GUI_ACTIVE / {xcc} XCDs / dispatch time, PMC pass) | {clock_mhz:.0f} MHz -> "
-        f"clock-adjusted peak {clock_peak:.1f} TFLOP/s, achieved {100 * tflops / clock_peak:.1f}% of it |",
-        f"| MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcc} x {simds} SIMDs) | {mfma_util:.1f}% |",
-        f"| SQ_BUSY_CYCLES (median per dispatch) | {med['SQ_BUSY_CYCLES']:.4g} |",
+        f"| MFMA busy cycles per SIMD (SQ_VALU_MFMA_BUSY_CYCLES / {simds}) vs the ideal 2MNK / 64 / {simds} | "
+        f"{busy_per_simd:.6g} / {ideal_per_simd:.6g} = {busy_per_simd / ideal_per_simd:.4f} |",
+        f"| shader-busy cycles per engine (SQ_BUSY_CYCLES / {engines}) | {sq_per_engine:.6g} |",
+        f"| PMC-pass dispatch duration, median (counter collection serialises dispatches) | {pmc_dur * 1e6:.2f} us "
+        f"= {tflops_pmc:.2f} TFLOP/s |",
+        f"| MfmaUtil = MFMA busy per SIMD / shader-busy per engine (same dispatch) | {mfma_util:.1f}% "
+        f"(>= achieved / peak of that dispatch, {100 * tflops_pmc / PEAK_TFLOPS:.1f}%: {util_check}) |",
+        f"| shader clock = busy cycles per engine / the same dispatch's duration | {clock_mhz:.0f} MHz, {valid} -> "
+        f"clock-adjusted peak {clock_peak:.1f} TFLOP/s; that dispatch reached {100 * tflops_pmc / clock_peak:.1f}% of it |",
+        f"| busy cycles per engine at the {max_mhz:.0f} MHz maximum | {busy_us_at_max:.2f} us (kernel-trace median "
+        f"{avg_s * 1e6:.2f} us) |",
+        f"| GRBM_GUI_ACTIVE / {xcc} XCDs over the PMC dispatch (counter window, not the kernel's cycles) | "
+        f"{gui_window_mhz:.0f} MHz equivalent |",
         f"| LDS bank conflicts / conflict-free accesses (SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE) | "
         f"{lds_rate:.4f} ({med['SQ_LDS_BANK_CONFLICT']:.4g} / {med['SQ_LDS_IDX_ACTIVE']:.4g}) |",
         f"| FETCH_SIZE / WRITE_SIZE raw (KiB per dispatch, median) | {med['FETCH_SIZE']:.1f} / {med['WRITE_SIZE']:.1f} |",
@@ -254,7 +304,8 @@ def main():
         f.write(f"fetch_bytes_per_launch: {fetch_bytes:.0f}\n")
         f.write(f"write_bytes_per_launch: {write_bytes:.0f}\n")
         f.write(f"mfma_util_pct: {mfma_util:.2f}\n")
-        f.write(f"effective_clock_mhz: {clock_mhz:.0f}\n")
+        f.write(f"shader_clock_mhz: {clock_mhz:.0f}\n")
+        f.write(f"clock_valid: {int(clock_ok)}\n")
     log("\n".join(lines))
 
 
