@@ -125,6 +125,12 @@
 #ifndef SG_KERNEL_NAME_SPLITK
 #define SG_KERNEL_NAME_SPLITK generated_gemm_splitk
 #endif
+#ifndef SG_STREAMK
+#define SG_STREAMK 0
+#endif
+#ifndef SG_KERNEL_NAME_STREAMK
+#define SG_KERNEL_NAME_STREAMK generated_gemm_streamk
+#endif
 
 namespace sg {
 
@@ -328,19 +334,32 @@ __device__ __forceinline__ void tile_coords(int z, int nwgx, int nwgy, int& tx, 
 #define SG_OCC_ATTR
 #endif
 
-// One output tile: the K loop over [0, k) of the (already offset) operands,
-// then the epilogue.  With SPLIT the work-group covers K range blockIdx.z of
-// `splits` equal ranges (whole K tiles), writes its raw partial tile to `ws`,
-// and the last of the tile's work-groups to take a ticket reduces the
-// partials and runs the epilogue.
-template <bool SPLIT>
+// How a work-group's accumulators leave the K loop.  FIX_NONE: straight to
+// the epilogue.  Otherwise the work-group covered part of the tile's K range:
+// it stores its raw accumulators as partial `slot` of the `parts` partials at
+// `ws`, takes a ticket, and the last of the `parts` arrivals combines the
+// partials and runs the epilogue.  FIX_SPLIT re-reads partials 0, 1, ...,
+// parts - 1 (its own included) and sums them in that order; FIX_STREAM
+// (parts == 2) adds the other partial to its own accumulators -- a two-term
+// sum, the same bits whichever work-group arrives last.  Either way the result
+// does not depend on timing.
+constexpr int FIX_NONE = 0, FIX_SPLIT = 1, FIX_STREAM = 2;
+struct Fixup {
+    int kind;
+    float* ws;          // partial 0 of this tile (FIX_SPLIT) or of this stream-K boundary (FIX_STREAM)
+    uint32_t* ticket;   // zero before the first arrival; re-armed to zero by the last one
+    uint32_t parts;
+    uint32_t slot;
+};
+
+// One output tile (tx, ty): the K loop over [k_first, k_first + k) of the
+// operands, the fix-up, then the epilogue.
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const float* __restrict__ b,
                                           const float* __restrict__ c, float* __restrict__ d,
                                           uint32_t m, uint32_t n, uint32_t k_total,
                                           uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
-                                          float alpha, float beta, int32_t numWorkgroupX,
-                                          int32_t numWorkgroupY, float* ws, uint32_t* tickets,
-                                          uint32_t splits) {
+                                          float alpha, float beta, int tx, int ty, uint32_t k_first, uint32_t k,
+                                          const Fixup fx, const int tid) {
     using namespace sg;
     typedef G::atom AT;
     typedef AT::acc_t acc_t;
@@ -350,23 +369,12 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 
     __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
 
-    const int tid = threadIdx.x;
     const int lane = tid & 63;
     // wave-uniform (a scalar register): the epilogue's buffer descriptors
     // derived from it then need no per-lane waterfall loop
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % SG_WG0;
     const int wn = wave / SG_WG0;
-
-    // Logical tile: the XCD renumbering and grouping act on the 2-D tile grid;
-    // a split launch takes its K range from blockIdx.z.  (Both orderings of
-    // the whole (tile, range) grid tried -- range by range, and tile by tile --
-    // measured slower on MI355X.)
-    const int tiles = numWorkgroupX * numWorkgroupY;
-    const int split = SPLIT ? (int)blockIdx.z : 0;
-    int tx, ty;
-    tile_coords(xcd_order((int)blockIdx.x + numWorkgroupX * (int)blockIdx.y, tiles), numWorkgroupX, numWorkgroupY,
-                tx, ty);
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
 
@@ -378,21 +386,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     };
     const char* const a_lim = reinterpret_cast<const char*>(a) + (TA ? extent(m, lda, k_total) : extent(k_total, lda, m));
     const char* const b_lim = reinterpret_cast<const char*>(b) + (TB ? extent(k_total, ldb, n) : extent(n, ldb, k_total));
-
-    // K range of this work-group: all of it, or range `split` of `splits`
-    // ranges of whole K tiles (the last range takes the remainder; ranges past
-    // the end are empty and contribute a zero partial).
-    uint32_t k = k_total;
-    if constexpr (SPLIT) {
-        const uint32_t kt_all = (k_total + DK - 1) / DK;
-        const uint32_t per = (kt_all + splits - 1) / splits;
-        const uint32_t t_first = min((uint32_t)split * per, kt_all);
-        const uint32_t k_first = t_first * DK;
-        const uint32_t k_end = min(k_first + per * DK, k_total);
-        k = k_end > k_first ? k_end - k_first : 0u;
-        a += TA ? (size_t)k_first : (size_t)k_first * lda;
-        b += TB ? (size_t)k_first * ldb : (size_t)k_first;
-    }
+    // the K range [k_first, k_first + k): a range of whole K tiles, the last
+    // one possibly cut at k_total
+    a += TA ? (size_t)k_first : (size_t)k_first * lda;
+    b += TB ? (size_t)k_first * ldb : (size_t)k_first;
     const int ktiles = (int)((k + DK - 1) / DK);
     // Uniform per work-group: every tile takes the vector path (float4 chunks
     // through buffer loads, dword alignment is enough) except for the K
@@ -785,11 +782,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     if (slow) kloop(SlowPath{});
     else kloop(FastPath{});
 
-    if constexpr (SPLIT) {
-        // ---- split-K: publish the partial, the tile's last arrival reduces ----
-        // Partial s of a tile: float4 chunk ch of thread tid (slots 4h..4h+3
-        // of atom (i, j), ch = (i * WT1 + j) * ACC / 4 + h) is float4 number
-        // (s * CH + ch) * NT + tid of the tile's workspace.
+    if (fx.kind != FIX_NONE) {
+        // ---- publish the partial; the last arrival combines ----
+        // Partial s: float4 chunk ch of thread tid (slots 4h..4h+3 of atom
+        // (i, j), ch = (i * WT1 + j) * ACC / 4 + h) is float4 number
+        // (s * CH + ch) * NT + tid from fx.ws.
         //
         // Partials are written and read with device-scope (sc1) buffer
         // accesses, coherent across the XCDs' L2 caches by themselves, and the
@@ -801,10 +798,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         constexpr int HC = AT::ACC / 4;
         constexpr int CH = WT0 * WT1 * HC;
         constexpr uint32_t PART_BYTES = (uint32_t)CH * NT * 16;
-        const uint32_t tile = (uint32_t)tx + (uint32_t)ty * (uint32_t)numWorkgroupX;
         const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc(ws + (size_t)tile * splits * (PART_BYTES / 4), (short)0,
-                                              (int)(splits * PART_BYTES), BUFFER_RSRC_WORD3);
+            __builtin_amdgcn_make_buffer_rsrc(fx.ws, (short)0, (int)(fx.parts * PART_BYTES), BUFFER_RSRC_WORD3);
 #pragma unroll
         for (int i = 0; i < WT0; ++i)
 #pragma unroll
@@ -815,46 +810,63 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                     f32x4 v;
                     v.x = acc[i][j][4 * h]; v.y = acc[i][j][4 * h + 1];
                     v.z = acc[i][j][4 * h + 2]; v.w = acc[i][j][4 * h + 3];
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (ch * NT + tid) * 16,
-                                                           (int)((uint32_t)split * PART_BYTES), CPOL_SC1);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, tid * 16,
+                                                           (int)(fx.slot * PART_BYTES) + ch * NT * 16, CPOL_SC1);
                 }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __shared__ uint32_t arrived;
         __syncthreads();
-        if (tid == 0)
-            arrived = __hip_atomic_fetch_add(tickets + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) arrived = __hip_atomic_fetch_add(fx.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        if (arrived + 1 != splits) return;
-        // Sum partials 0, 1, ..., splits - 1 in that order (the own one is
-        // re-read too), so the result does not depend on the arrival order.
+        if (arrived + 1 != fx.parts) return;
         auto read_part = [&](uint32_t sp, int ch) __attribute__((always_inline)) {
-            return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (ch * NT + tid) * 16,
-                                                                                    (int)(sp * PART_BYTES), CPOL_SC1));
+            return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rs, tid * 16, (int)(sp * PART_BYTES) + ch * NT * 16, CPOL_SC1));
         };
-#pragma unroll
-        for (int i = 0; i < WT0; ++i)
-#pragma unroll
-            for (int j = 0; j < WT1; ++j)
-#pragma unroll
-                for (int h = 0; h < HC; ++h) {
-                    const f32x4 v = read_part(0, (i * WT1 + j) * HC + h);
-                    acc[i][j][4 * h] = v.x; acc[i][j][4 * h + 1] = v.y;
-                    acc[i][j][4 * h + 2] = v.z; acc[i][j][4 * h + 3] = v.w;
-                }
-        for (uint32_t sp = 1; sp < splits; ++sp) {
+        if (fx.kind == FIX_SPLIT) {
+            // Sum partials 0, 1, ..., parts - 1 in that order (the own one is
+            // re-read too), so the result does not depend on the arrival order.
 #pragma unroll
             for (int i = 0; i < WT0; ++i)
 #pragma unroll
                 for (int j = 0; j < WT1; ++j)
 #pragma unroll
                     for (int h = 0; h < HC; ++h) {
-                        const f32x4 v = read_part(sp, (i * WT1 + j) * HC + h);
+                        const f32x4 v = read_part(0, (i * WT1 + j) * HC + h);
+                        acc[i][j][4 * h] = v.x; acc[i][j][4 * h + 1] = v.y;
+                        acc[i][j][4 * h + 2] = v.z; acc[i][j][4 * h + 3] = v.w;
+                    }
+            for (uint32_t sp = 1; sp < fx.parts; ++sp) {
+#pragma unroll
+                for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                    for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                        for (int h = 0; h < HC; ++h) {
+                            const f32x4 v = read_part(sp, (i * WT1 + j) * HC + h);
+                            acc[i][j][4 * h] += v.x; acc[i][j][4 * h + 1] += v.y;
+                            acc[i][j][4 * h + 2] += v.z; acc[i][j][4 * h + 3] += v.w;
+                        }
+            }
+        } else {
+            // two partials: own + other, commutative.  Read in batches of one
+            // atom's chunks so the loads never hold more than ACC extra
+            // registers (all of them at once would spill the largest tiles).
+#pragma unroll
+            for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                for (int j = 0; j < WT1; ++j) {
+#pragma unroll
+                    for (int h = 0; h < HC; ++h) {
+                        const f32x4 v = read_part(1u - fx.slot, (i * WT1 + j) * HC + h);
                         acc[i][j][4 * h] += v.x; acc[i][j][4 * h + 1] += v.y;
                         acc[i][j][4 * h + 2] += v.z; acc[i][j][4 * h + 3] += v.w;
                     }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
         }
         // every arrival of this launch has been counted: re-arm for the next one
-        if (tid == 0) __hip_atomic_store(tickets + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(fx.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- epilogue: D = alpha * acc + beta * C ----
@@ -1016,20 +1028,33 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     }
 }
 
+// Tile of work-group (bx, by) of a 2-D tile grid: the XCD renumbering and
+// the grouping act on the 2-D grid.  (Both orderings of a split launch's whole
+// (tile, range) grid tried -- range by range, and tile by tile -- measured
+// slower on MI355X than this per-slice order.)
+__device__ __forceinline__ void grid_tile(int bx, int by, int nwgx, int nwgy, int& tx, int& ty) {
+    sg::tile_coords(sg::xcd_order(bx + nwgx * by, nwgx * nwgy), nwgx, nwgy, tx, ty);
+}
+
 extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
 SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
                const float* __restrict__ c, float* __restrict__ d,
                uint32_t m, uint32_t n, uint32_t k,
                uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY) {
-    gemm_tile<false>(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, numWorkgroupX, numWorkgroupY,
-                     nullptr, nullptr, 1u);
+    int tx, ty;
+    grid_tile((int)blockIdx.x, (int)blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
+    gemm_tile(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, tx, ty, 0u, k,
+              Fixup{FIX_NONE, nullptr, nullptr, 1u, 0u}, (int)threadIdx.x);
 }
 
 #if SG_SPLITK
 // Split-K variant: the reference's 15 arguments, then
 //   offset 80 ws (float*)   88 tickets (uint32_t*)   96 splits (uint32_t) -> 100 B, padded to 104
 // Launch: grid = (numWorkgroupX, numWorkgroupY, splits), splits >= 1.
+// Work-group (x, y, z) takes tile (x, y) and K range z: the K tiles are split
+// into `splits` ranges of ceil(K tiles / splits) (the last takes the
+// remainder; ranges past the end are empty and contribute a zero partial).
 // ws holds numWorkgroupX * numWorkgroupY * splits * MT0 * MT1 floats;
 // tickets holds numWorkgroupX * numWorkgroupY zeros before the first launch
 // and is left zeroed by every launch.  Launches sharing ws/tickets must not
@@ -1041,7 +1066,91 @@ SG_KERNEL_NAME_SPLITK(const float* __restrict__ a, const float* __restrict__ b,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                       float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY,
                       float* ws, uint32_t* tickets, uint32_t splits) {
-    gemm_tile<true>(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, numWorkgroupX, numWorkgroupY,
-                    ws, tickets, splits);
+    constexpr uint32_t DK = SG_DK;
+    int tx, ty;
+    grid_tile((int)blockIdx.x, (int)blockIdx.y, numWorkgroupX, numWorkgroupY, tx, ty);
+    const uint32_t split = blockIdx.z;
+    const uint32_t kt_all = (k + DK - 1) / DK;
+    const uint32_t per = (kt_all + splits - 1) / splits;
+    const uint32_t k_first = min(split * per, kt_all) * DK;
+    const uint32_t k_end = min(k_first + per * DK, k);
+    const uint32_t tile = (uint32_t)tx + (uint32_t)ty * (uint32_t)numWorkgroupX;
+    gemm_tile(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, tx, ty, k_first,
+              k_end > k_first ? k_end - k_first : 0u,
+              Fixup{FIX_SPLIT, ws + (size_t)tile * splits * (sg::G::MT0 * sg::G::MT1), tickets + tile, splits, split},
+              (int)threadIdx.x);
+}
+#endif
+
+#if SG_STREAMK
+// Stream-K variant for tile grids that leave a partial last round of
+// work-groups: the reference's 15 arguments, then
+//   offset 80 ws (float*)   88 tickets (uint32_t*)   96 sk_tiles (uint32_t)   100 groups (uint32_t) -> 104 B
+// Launch: grid = (G, 1, 1), G = groups (passed explicitly: the kernel reads no
+// hidden argument; for speed at most the work-groups resident at once, though
+// no work-group ever waits for another), with
+// T = numWorkgroupX * numWorkgroupY tiles, G <= sk_tiles <= T, and T - sk_tiles
+// a multiple of G, and sk_tiles * ceil(k / DK) * G below 2^32.  The K tiles of
+// the first sk_tiles logical tiles form one
+// sequence of sk_tiles * ceil(k / DK) iterations; work-group w (after the XCD
+// renumbering) takes iterations [S w / G, S (w + 1) / G), at least one tile's
+// worth, so every tile of the sequence is cut at most once, at a work-group
+// boundary: the two work-groups either side of boundary w store partials 0
+// (head) and 1 (tail) of ws[w], and the later one adds them and runs the
+// epilogue.  Then the work-group runs the remaining (data-parallel) tiles
+// sk_tiles + w, + G, ... whole.  ws holds G * 2 * MT0 * MT1 floats and tickets
+// G zeros, left zero by the launch; launches sharing them must not overlap.
+extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
+SG_KERNEL_NAME_STREAMK(const float* __restrict__ a, const float* __restrict__ b,
+                       const float* __restrict__ c, float* __restrict__ d,
+                       uint32_t m, uint32_t n, uint32_t k,
+                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
+                       float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY,
+                       float* ws, uint32_t* tickets, uint32_t sk_tiles, uint32_t groups) {
+    constexpr uint32_t DK = SG_DK;
+    constexpr size_t PART_FLOATS = (size_t)sg::G::MT0 * sg::G::MT1;
+    const uint32_t w = (uint32_t)sg::xcd_order((int)blockIdx.x, (int)groups);
+    const uint32_t tiles = (uint32_t)numWorkgroupX * (uint32_t)numWorkgroupY;
+    const uint32_t kt = (k + DK - 1) / DK;
+    // 32-bit iteration arithmetic: the host keeps sk_tiles * kt * groups below 2^32
+    const uint32_t total = sk_tiles * kt;
+    const uint32_t it_end = total * (w + 1) / groups;
+    uint32_t it = total * w / groups;
+    uint32_t dp = sk_tiles + w;
+    // one call site for both phases: the stream-K iterations first, then the
+    // data-parallel tiles (a second inlined copy of the tile would double the
+    // kernel's registers)
+    for (;;) {
+        uint32_t t, k0, k1;
+        if (it < it_end) {
+            t = it / kt;
+            k0 = it - t * kt;
+            k1 = min(kt, it_end - t * kt);
+            it = t * kt + k1;
+        } else if (dp < tiles) {
+            t = dp;
+            k0 = 0;
+            k1 = kt;
+            dp += groups;
+        } else {
+            break;
+        }
+        Fixup fx{FIX_NONE, nullptr, nullptr, 1u, 0u};
+        if (k0 > 0 || k1 < kt) {
+            // cut at boundary w (this work-group has the tail, from k0) or
+            // w + 1 (the head, up to k1)
+            const uint32_t bnd = k0 > 0 ? w : w + 1;
+            fx = Fixup{FIX_STREAM, ws + (size_t)bnd * 2 * PART_FLOATS, tickets + bnd, 2u, k0 > 0 ? 1u : 0u};
+        }
+        int tx, ty;
+        sg::tile_coords((int)t, numWorkgroupX, numWorkgroupY, tx, ty);
+        const uint32_t kf = k0 * DK, ke = min(k1 * DK, k);
+        // the thread index made opaque per tile: nothing derived from it is
+        // hoisted out of this loop to stay live through the K loop
+        int tid = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        __syncthreads();  // every wave is done with the previous tile's LDS
+        gemm_tile(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta, tx, ty, kf, ke - kf, fx, tid);
+    }
 }
 #endif

@@ -1,7 +1,7 @@
 // sgemm_launch_noalloc: sgemm_launch for callers that cannot allocate device
 // memory (code under HIP graph capture, serving loops, harnesses that forbid
-// hipMalloc).  A split-K launch needs a workspace -- the tile partials and one
-// ticket per output tile -- which sgemm_launch allocates on the handle's first
+// hipMalloc).  A split-K or stream-K launch needs a workspace -- partial tiles
+// and their tickets -- which sgemm_launch allocates on the handle's first
 // launch that needs it; here it lives in a fixed device array, `scratch`,
 // compiled into this library, one copy per device, held until the process
 // ends.  Nothing on this path calls hipMalloc, hipFree or any allocating
@@ -71,33 +71,54 @@ extern "C" int sgemm_launch_noalloc(sgemm_handle* h, const float* dA, const floa
     if (!h) return sgemm_internal::set_error(SGEMM_E_INVALID, "sgemm_launch_noalloc: null handle");
     int r = sgemm_internal::check_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, beta);
     if (r != SGEMM_OK || m == 0 || n == 0) return r;
-    uint32_t splits = 1;
-    size_t need = 0, tiles = 0;
-    sgemm_internal::plan(h, m, n, k, &splits, &need, &tiles);
-    if (splits == 1)  // generated_gemm uses no workspace
-        return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr);
-    if (need > (size_t)SGEMM_NOALLOC_PARTIAL_BYTES || tiles > (size_t)SGEMM_NOALLOC_MAX_TILES) {
-        char msg[256];
-        snprintf(msg, sizeof(msg),
-                 "sgemm_launch_noalloc: a %ux%ux%u launch in %u K ranges needs %zu bytes of partials for %zu tiles; "
-                 "the static scratch holds %u bytes and %u tiles", m, n, k, splits, need, tiles,
-                 (unsigned)SGEMM_NOALLOC_PARTIAL_BYTES, (unsigned)SGEMM_NOALLOC_MAX_TILES);
-        return sgemm_internal::set_error(SGEMM_E_SHAPE, msg);
-    }
-    void* base = nullptr;
-    if ((r = scratch_address(sgemm_internal::device(h), &base)) != SGEMM_OK) return r;
-    float* partials = static_cast<float*>(base);
-    uint32_t* tickets = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(base) + SGEMM_NOALLOC_PARTIAL_BYTES);
     hipStream_t s = sgemm_internal::stream(h);
-    hipLaunchKernelGGL(clear_tickets, dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, s, tickets,
-                       (uint32_t)tiles);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        char msg[256];
-        snprintf(msg, sizeof(msg), "clear_tickets launch failed: %s (%d)", hipGetErrorString(e), (int)e);
-        return sgemm_internal::set_error((int)e, msg);
+    sgemm_internal::Part parts[3];
+    const int count = sgemm_internal::decompose(h, m, n, k, lda, ldb, ldc, ldd, parts);
+    // every part's needs are checked before anything is launched
+    for (int q = 0; q < count; ++q) {
+        const sgemm_internal::Part& pt = parts[q];
+        if (pt.kh != h && (r = sgemm_check_shape(pt.kh, pt.m, pt.n, k, lda, ldb, ldc, ldd)) != SGEMM_OK) return r;
+        const sgemm_internal::Plan p = sgemm_internal::plan(pt.kh, pt.m, pt.n, k);
+        if (p.partial_bytes > (size_t)SGEMM_NOALLOC_PARTIAL_BYTES || p.ticket_count > (size_t)SGEMM_NOALLOC_MAX_TILES) {
+            char msg[256];
+            snprintf(msg, sizeof(msg),
+                     "sgemm_launch_noalloc: a %ux%ux%u launch (%u K ranges, %u stream-K tiles) needs %zu bytes of "
+                     "partials and %zu tickets; the static scratch holds %u bytes and %u tickets", pt.m, pt.n, k,
+                     p.splits, p.sk_tiles, p.partial_bytes, p.ticket_count, (unsigned)SGEMM_NOALLOC_PARTIAL_BYTES,
+                     (unsigned)SGEMM_NOALLOC_MAX_TILES);
+            return sgemm_internal::set_error(SGEMM_E_SHAPE, msg);
+        }
     }
-    const sgemm_internal::Workspace ws{partials, (size_t)SGEMM_NOALLOC_PARTIAL_BYTES, tickets,
-                                       (size_t)SGEMM_NOALLOC_MAX_TILES};
-    return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, &ws);
+    for (int q = 0; q < count; ++q) {
+        const sgemm_internal::Part& pt = parts[q];
+        const float* a = dA ? dA + pt.a_off : dA;
+        const float* b = dB ? dB + pt.b_off : dB;
+        const float* c = dC ? dC + pt.c_off : dC;
+        float* d = dD + pt.d_off;
+        const sgemm_internal::Plan p = sgemm_internal::plan(pt.kh, pt.m, pt.n, k);
+        if (!p.partial_bytes) {  // generated_gemm uses no workspace
+            r = sgemm_internal::launch(pt.kh, a, b, c, d, pt.m, pt.n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr, s);
+            if (r != SGEMM_OK) return r;
+            continue;
+        }
+        void* base = nullptr;
+        if ((r = scratch_address(sgemm_internal::device(h), &base)) != SGEMM_OK) return r;
+        float* partials = static_cast<float*>(base);
+        uint32_t* tickets =
+            reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(base) + SGEMM_NOALLOC_PARTIAL_BYTES);
+        // the parts run in order on one stream, so they share the scratch
+        hipLaunchKernelGGL(clear_tickets, dim3((unsigned)((p.ticket_count + 255) / 256)), dim3(256), 0, s, tickets,
+                           (uint32_t)p.ticket_count);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            char msg[256];
+            snprintf(msg, sizeof(msg), "clear_tickets launch failed: %s (%d)", hipGetErrorString(e), (int)e);
+            return sgemm_internal::set_error((int)e, msg);
+        }
+        const sgemm_internal::Workspace ws{partials, (size_t)SGEMM_NOALLOC_PARTIAL_BYTES, tickets,
+                                           (size_t)SGEMM_NOALLOC_MAX_TILES};
+        r = sgemm_internal::launch(pt.kh, a, b, c, d, pt.m, pt.n, k, lda, ldb, ldc, ldd, alpha, beta, &ws, s);
+        if (r != SGEMM_OK) return r;
+    }
+    return SGEMM_OK;
 }

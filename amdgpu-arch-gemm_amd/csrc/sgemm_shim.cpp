@@ -187,6 +187,12 @@ int load_config(const char* path, sgemm_kernel_info* info) {
     CFG_TRY(toml_int(t, "vmem_stage", &info->vmem_stage, false, 1));
     // default split count of generated_gemm_splitk (absent: no split; 0: per problem)
     CFG_TRY(toml_int(t, "split_k", &info->split_k, false, 1));
+    // default stream-K setting (absent: off)
+    CFG_TRY(toml_int(t, "stream_k", &info->stream_k, false, 0));
+    if (info->stream_k < 0 || info->stream_k > 2)
+        return fail(SGEMM_E_CONFIG, "stream_k = %d outside 0..2", info->stream_k);
+    CFG_TRY(toml_int(t, "stream_k_rounds", &info->stream_k_rounds, false, 0));
+    if (info->stream_k_rounds < 0) return fail(SGEMM_E_CONFIG, "stream_k_rounds = %d < 0", info->stream_k_rounds);
     if (info->split_k < 0 || info->split_k > SGEMM_MAX_SPLIT_K)
         return fail(SGEMM_E_CONFIG, "split_k = %d outside 0..%d", info->split_k, SGEMM_MAX_SPLIT_K);
     if (a_type || b_type || cd_type || scalar_type) return fail(SGEMM_E_CONFIG, "only FP32 (type 0) kernels are supported");
@@ -271,6 +277,32 @@ uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_
     return s < 1 ? 1 : (uint32_t)s;
 }
 
+// Tiles of the stream-K phase of an unsplit launch (0: no stream-K).  With
+// T tiles and G resident work-groups of generated_gemm_streamk, stream-K runs
+// when T > G and the data-parallel grid would leave a partial last round that
+// costs at least 3% (ceil(T / G) rounds against T / G) within the instance's
+// stream_k_rounds (0: any number of rounds), or always when the setting is 2
+// and T > G.  The stream-K phase then takes the last partial
+// round plus one whole round, T % G + G tiles (G when T % G == 0), so every
+// work-group covers at least one tile's worth of K iterations; the kernel's
+// 32-bit iteration arithmetic needs those tiles' K tiles times G below 2^32.
+uint32_t stream_k_tiles(const sgemm_kernel_info& i, size_t tiles, uint32_t k) {
+    if (i.stream_k == 0 || i.stream_k_groups <= 0 || k == 0) return 0;
+    const uint64_t g = (uint64_t)i.stream_k_groups, t = tiles;
+    if (t <= g) return 0;
+    const uint64_t rem = t % g;
+    if (i.stream_k == 1) {
+        const uint64_t rounds = (t + g - 1) / g;
+        if (rem == 0 || rounds * g * 100 < t * 103) return 0;
+        if (i.stream_k_rounds > 0 && rounds > (uint64_t)i.stream_k_rounds) return 0;
+    }
+    const uint64_t sk = rem ? rem + g : g;
+    // the kernel's iteration arithmetic is 32-bit
+    const uint64_t kt = ((uint64_t)k + (uint32_t)i.depth_k - 1) / (uint32_t)i.depth_k;
+    if (sk * kt * g >= (1ull << 32)) return 0;
+    return (uint32_t)sk;
+}
+
 // ------------------------------------------------------- seeded values ---
 const uint64_t kGamma = 0x9E3779B97F4A7C15ull;
 
@@ -317,23 +349,36 @@ struct sgemm_handle {
     size_t ticket_count = 0;
     int compute_units = 0;                    // of the device the module is loaded on
     int device = 0;                           // the device current at sgemm_open
+    hipFunction_t function_streamk = nullptr; // null when the code object has none
+    sgemm_handle* edge = nullptr;             // small-tile kernel for thin edge strips (sgemm_set_edge_kernel)
 };
 
 namespace sgemm_internal {
 
-int plan(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* splits, size_t* ws_bytes,
-         size_t* tiles) {
+Plan plan(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k) {
     const sgemm_kernel_info& i = h->info;
-    *splits = effective_splits(i, h->compute_units, m, n, k);
-    *tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
-             ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
-    *ws_bytes = *splits > 1 ? *tiles * *splits * (size_t)i.tile_m * (size_t)i.tile_n * 4 : 0;
-    return SGEMM_OK;
+    Plan p;
+    p.tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+              ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+    const size_t tile_bytes = (size_t)i.tile_m * (size_t)i.tile_n * 4;
+    p.splits = effective_splits(i, h->compute_units, m, n, k);
+    if (p.splits > 1) {
+        p.partial_bytes = p.tiles * p.splits * tile_bytes;
+        p.ticket_count = p.tiles;
+        return p;
+    }
+    p.sk_tiles = stream_k_tiles(i, p.tiles, k);
+    if (p.sk_tiles) {
+        p.sk_groups = (uint32_t)i.stream_k_groups;
+        p.partial_bytes = (size_t)p.sk_groups * 2 * tile_bytes;
+        p.ticket_count = p.sk_groups;
+    }
+    return p;
 }
 
 int launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD, uint32_t m, uint32_t n,
            uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd, float alpha, float beta,
-           const Workspace* ws) {
+           const Workspace* ws, hipStream_t stream) {
     const sgemm_kernel_info& i = h->info;
     KernArgs ka;
     memset(&ka, 0, sizeof(ka));
@@ -342,28 +387,34 @@ int launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, f
     ka.alpha = alpha; ka.beta = beta;
     ka.num_wg_x = (int32_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m);
     ka.num_wg_y = (int32_t)((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
-    const uint32_t splits = effective_splits(i, h->compute_units, m, n, k);
-    if (splits == 1) {
+    const Plan p = plan(h, m, n, k);
+    if (p.splits == 1 && !p.sk_tiles) {
         size_t size = sizeof(ka);
         void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
         HIP_TRY(hipModuleLaunchKernel(h->function, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, 1,
-                                      (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+                                      (unsigned)i.workitems, 1, 1, 0, stream, nullptr, extra));
         return SGEMM_OK;
     }
-    const size_t tiles = (size_t)ka.num_wg_x * (size_t)ka.num_wg_y;
-    const size_t ws_need = tiles * splits * (size_t)i.tile_m * (size_t)i.tile_n * 4;
-    if (!ws || !ws->partials || !ws->tickets || ws->partial_bytes < ws_need || ws->ticket_count < tiles)
-        return fail(SGEMM_E_INVALID, "split launch needs %zu bytes of partials and %zu tickets", ws_need, tiles);
+    if (!ws || !ws->partials || !ws->tickets || ws->partial_bytes < p.partial_bytes || ws->ticket_count < p.ticket_count)
+        return fail(SGEMM_E_INVALID, "launch needs %zu bytes of partials and %zu tickets", p.partial_bytes,
+                    p.ticket_count);
     KernArgsSplit ks;
     memset(&ks, 0, sizeof(ks));
     ks.base = ka;
     ks.ws = ws->partials;
     ks.tickets = ws->tickets;
-    ks.splits = splits;
     size_t size = sizeof(ks);
     void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ks, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
-    HIP_TRY(hipModuleLaunchKernel(h->function_splitk, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, splits,
-                                  (unsigned)i.workitems, 1, 1, 0, h->stream, nullptr, extra));
+    if (p.splits > 1) {
+        ks.splits = p.splits;
+        HIP_TRY(hipModuleLaunchKernel(h->function_splitk, (unsigned)ka.num_wg_x, (unsigned)ka.num_wg_y, p.splits,
+                                      (unsigned)i.workitems, 1, 1, 0, stream, nullptr, extra));
+        return SGEMM_OK;
+    }
+    ks.splits = p.sk_tiles;      // generated_gemm_streamk: sk_tiles at 96, groups at 100
+    ks.pad = p.sk_groups;
+    HIP_TRY(hipModuleLaunchKernel(h->function_streamk, p.sk_groups, 1, 1, (unsigned)i.workitems, 1, 1, 0, stream,
+                                  nullptr, extra));
     return SGEMM_OK;
 }
 
@@ -378,6 +429,30 @@ int check_launch(const sgemm_handle* h, const float* dA, const float* dB, const 
     if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 3u)
         return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 4-byte aligned");
     return SGEMM_OK;
+}
+
+int decompose(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc,
+              uint32_t ldd, Part out[3]) {
+    const sgemm_kernel_info& i = h->info;
+    out[0] = Part{const_cast<sgemm_handle*>(h), m, n, 0, 0, 0, 0};
+    const sgemm_handle* e = h->edge;
+    if (!e || k == 0) return 1;
+    const uint32_t tm = (uint32_t)i.tile_m, tn = (uint32_t)i.tile_n;
+    uint32_t me = m % tm, ne = n % tn;
+    // thin strips only: at most a quarter of a tile, next to a non-empty interior
+    if (!(me && me * 4 <= tm && m > me)) me = 0;
+    if (!(ne && ne * 4 <= tn && n > ne)) ne = 0;
+    if (!me && !ne) return 1;
+    const uint32_t mi = m - me, ni = n - ne;
+    int count = 0;
+    out[count++] = Part{const_cast<sgemm_handle*>(h), mi, ni, 0, 0, 0, 0};
+    sgemm_handle* eh = const_cast<sgemm_handle*>(e);
+    if (me)  // rows [mi, m) of every column
+        out[count++] = Part{eh, me, n, i.trans_a ? (size_t)mi * lda : (size_t)mi, 0, (size_t)mi, (size_t)mi};
+    if (ne)  // columns [ni, n) of rows [0, mi)
+        out[count++] = Part{eh, mi, ne, 0, i.trans_b ? (size_t)ni : (size_t)ni * ldb, (size_t)ni * ldc,
+                            (size_t)ni * ldd};
+    return count;
 }
 
 hipStream_t stream(const sgemm_handle* h) { return h->stream; }
@@ -446,6 +521,21 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
             (void)hipGetLastError();
         }
         h->device = dev;
+        // optional stream-K kernel: G = resident work-groups per CU x CUs
+        h->info.stream_k_groups = 0;
+        if (hipModuleGetFunction(&h->function_streamk, h->module, "generated_gemm_streamk") == hipSuccess) {
+            int per_cu = 0;
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, h->function_streamk, h->info.workitems, 0) ==
+                    hipSuccess && per_cu > 0 && h->compute_units > 0) {
+                h->info.stream_k_groups = per_cu * h->compute_units;
+            } else {
+                (void)hipGetLastError();
+            }
+        } else {
+            h->function_streamk = nullptr;
+            (void)hipGetLastError();
+        }
+        if (!h->info.stream_k_groups) h->info.stream_k = 0;
         if (h->info.split_k > h->info.split_k_max) {
             sgemm_close(h);
             return fail(SGEMM_E_CONFIG, "split_k = %d but %s has no generated_gemm_splitk", info.split_k, co_path);
@@ -530,14 +620,26 @@ int sgemm_set_split_k(sgemm_handle* h, int splits) {
 
 int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes) {
     if (!h || !bytes) return fail(SGEMM_E_INVALID, "sgemm_workspace_size: null argument");
-    const sgemm_kernel_info& i = h->info;
-    const uint32_t s = effective_splits(i, h->compute_units, m, n, k);
     *bytes = 0;
-    if (s > 1 && m && n) {
-        const size_t tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
-                             ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
-        *bytes = tiles * s * (size_t)i.tile_m * (size_t)i.tile_n * 4 + tiles * 4;
+    if (m && n) {
+        const sgemm_internal::Plan p = sgemm_internal::plan(h, m, n, k);
+        *bytes = p.partial_bytes ? p.partial_bytes + p.ticket_count * 4 : 0;
     }
+    return SGEMM_OK;
+}
+
+int sgemm_set_stream_k(sgemm_handle* h, int mode) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_stream_k: null handle");
+    if (mode < 0 || mode > 2) return fail(SGEMM_E_INVALID, "stream-K mode %d outside 0..2", mode);
+    if (mode && !h->info.stream_k_groups)
+        return fail(SGEMM_E_CONFIG, "stream-K needs generated_gemm_streamk, absent from this code object");
+    h->info.stream_k = mode;
+    return SGEMM_OK;
+}
+
+int sgemm_stream_k_tiles(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* sk_tiles) {
+    if (!h || !sk_tiles) return fail(SGEMM_E_INVALID, "sgemm_stream_k_tiles: null argument");
+    *sk_tiles = (m && n) ? (int)sgemm_internal::plan(h, m, n, k).sk_tiles : 0;
     return SGEMM_OK;
 }
 
@@ -577,39 +679,84 @@ int sgemm_memset(void* dptr, int value, size_t bytes) {
     return SGEMM_OK;
 }
 
+namespace {
+
+// One part of a launch on `stream` with kernel handle `kh`: its split-K /
+// stream-K workspace is kh's own, grown on demand (both streams drained
+// first, fresh tickets zeroed on `stream`).
+int launch_part(sgemm_handle* kh, hipStream_t stream, const float* dA, const float* dB, const float* dC, float* dD,
+                uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd, float alpha,
+                float beta) {
+    const sgemm_internal::Plan p = sgemm_internal::plan(kh, m, n, k);
+    if (!p.partial_bytes)
+        return sgemm_internal::launch(kh, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr, stream);
+    const size_t ws_need = p.partial_bytes, tickets = p.ticket_count;
+    if (kh->ws_bytes < ws_need || kh->ticket_count < tickets) {
+        HIP_TRY(hipStreamSynchronize(stream));
+        HIP_TRY(hipStreamSynchronize(kh->stream));
+        if (kh->ws_bytes < ws_need) {
+            if (kh->ws) HIP_TRY(hipFree(kh->ws));
+            kh->ws = nullptr;
+            kh->ws_bytes = 0;
+            HIP_TRY(hipMalloc(&kh->ws, ws_need));
+            kh->ws_bytes = ws_need;
+        }
+        if (kh->ticket_count < tickets) {
+            if (kh->tickets) HIP_TRY(hipFree(kh->tickets));
+            kh->tickets = nullptr;
+            kh->ticket_count = 0;
+            HIP_TRY(hipMalloc((void**)&kh->tickets, tickets * 4));
+            // ordered before the launch below on the same stream
+            HIP_TRY(hipMemsetAsync(kh->tickets, 0, tickets * 4, stream));
+            kh->ticket_count = tickets;
+        }
+    }
+    const sgemm_internal::Workspace ws{(float*)kh->ws, kh->ws_bytes, kh->tickets, kh->ticket_count};
+    return sgemm_internal::launch(kh, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, &ws, stream);
+}
+
+}  // namespace
+
 int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
                  uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                  float alpha, float beta) {
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_launch: null handle");
     int r = sgemm_internal::check_launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, beta);
     if (r != SGEMM_OK || m == 0 || n == 0) return r;
-    uint32_t splits = 1;
-    size_t ws_need = 0, tiles = 0;
-    sgemm_internal::plan(h, m, n, k, &splits, &ws_need, &tiles);
-    if (splits == 1) return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, nullptr);
-    // split-K: partials of every (tile, split) plus one ticket per tile; both
-    // buffers grow on demand and tickets start (and stay) zero
-    if (h->ws_bytes < ws_need || h->ticket_count < tiles) {
-        HIP_TRY(hipStreamSynchronize(h->stream));
-        if (h->ws_bytes < ws_need) {
-            if (h->ws) HIP_TRY(hipFree(h->ws));
-            h->ws = nullptr;
-            h->ws_bytes = 0;
-            HIP_TRY(hipMalloc(&h->ws, ws_need));
-            h->ws_bytes = ws_need;
-        }
-        if (h->ticket_count < tiles) {
-            if (h->tickets) HIP_TRY(hipFree(h->tickets));
-            h->tickets = nullptr;
-            h->ticket_count = 0;
-            HIP_TRY(hipMalloc((void**)&h->tickets, tiles * 4));
-            // ordered before the launch below on the same stream
-            HIP_TRY(hipMemsetAsync(h->tickets, 0, tiles * 4, h->stream));
-            h->ticket_count = tiles;
-        }
+    sgemm_internal::Part parts[3];
+    const int count = sgemm_internal::decompose(h, m, n, k, lda, ldb, ldc, ldd, parts);
+    for (int q = 0; q < count; ++q) {
+        const sgemm_internal::Part& pt = parts[q];
+        if (pt.kh != h && (r = sgemm_check_shape(pt.kh, pt.m, pt.n, k, lda, ldb, ldc, ldd)) != SGEMM_OK) return r;
+        r = launch_part(pt.kh, h->stream, dA ? dA + pt.a_off : dA, dB ? dB + pt.b_off : dB, dC ? dC + pt.c_off : dC,
+                        dD + pt.d_off, pt.m, pt.n, k, lda, ldb, ldc, ldd, alpha, beta);
+        if (r != SGEMM_OK) return r;
     }
-    const sgemm_internal::Workspace ws{(float*)h->ws, h->ws_bytes, h->tickets, h->ticket_count};
-    return sgemm_internal::launch(h, dA, dB, dC, dD, m, n, k, lda, ldb, ldc, ldd, alpha, beta, &ws);
+    return SGEMM_OK;
+}
+
+int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_edge_kernel: null handle");
+    if (edge) {
+        if (edge == h || edge->edge) return fail(SGEMM_E_INVALID, "an edge kernel must be another handle without an edge");
+        if (edge->info.trans_a != h->info.trans_a || edge->info.trans_b != h->info.trans_b)
+            return fail(SGEMM_E_CONFIG, "the edge kernel's layout (trans_a/trans_b) differs from the main kernel's");
+        if (edge->info.tile_m > h->info.tile_m || edge->info.tile_n > h->info.tile_n)
+            return fail(SGEMM_E_CONFIG, "the edge kernel's tile %dx%d is larger than the main kernel's %dx%d",
+                        edge->info.tile_m, edge->info.tile_n, h->info.tile_m, h->info.tile_n);
+        if (edge->device != h->device) return fail(SGEMM_E_CONFIG, "the edge kernel is loaded on another device");
+    }
+    h->edge = edge;
+    return SGEMM_OK;
+}
+
+int sgemm_edge_interior(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* m_int, uint32_t* n_int) {
+    if (!h || !m_int || !n_int) return fail(SGEMM_E_INVALID, "sgemm_edge_interior: null argument");
+    sgemm_internal::Part parts[3];
+    sgemm_internal::decompose(h, m, n, k, m, k, m, m, parts);
+    *m_int = parts[0].m;
+    *n_int = parts[0].n;
+    return SGEMM_OK;
 }
 
 int sgemm_time(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,

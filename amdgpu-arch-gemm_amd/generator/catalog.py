@@ -30,8 +30,9 @@ def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1):
-    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk)
+def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1, stk=0, stk_rounds=0):
+    return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk,
+                             stream_k=stk, stream_k_rounds=stk_rounds)
 
 
 # name -> (config, optimizations)
@@ -50,11 +51,15 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt128x64_a16_wg2x2_dk32_s3": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2), _opt(wgm=4, plr=3, xcd=8, sk=0)),
     # winners of the wide sweep (all wave groups, 32..256 tiles)
     "mt256x256_a32_wg4x2_dk16_s3": (_cfg(MFMA_32x32x2, (4, 2), (2, 4), 16, stages=2), _opt(wgm=8, plr=3, xcd=8)),
-    "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2), _opt(wgm=8, plr=3, xcd=8, sk=0)),
+    # stream-K only up to two rounds of tiles: interleaved runs at 4096 deep
+    # gained 4-13% at 1280^2..2304^2 (1.0-1.7 rounds) and lost 3-13% on longer
+    # grids (3000^3, 3840^2, 4864^2)
+    "mt64x64_a16_wg1x4_dk32_s3": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2),
+                                  _opt(wgm=8, plr=3, xcd=8, sk=0, stk=1, stk_rounds=2)),
     "mt128x64_a16_wg2x2_dk16_s2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 16, stages=1), _opt(wgm=1, plr=3, xcd=0, sk=0)),
     # two work-groups per CU (registers capped for 2 waves per SIMD)
     "mt128x64_a16_wg2x2_dk32_s3_occ2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
-                                        _opt(wgm=4, plr=3, xcd=8, occ=2, sk=0)),
+                                        _opt(wgm=4, plr=3, xcd=8, occ=2, sk=0, stk=1)),
     "mt256x128_a32_wg2x2_dk16_s3_occ2": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16, stages=2),
                                          _opt(wgm=4, plr=3, xcd=8, occ=2)),
     # the same with the refill's memory instructions not interleaved one by one
@@ -93,6 +98,9 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     "mt128x64_a32_wg4x1_dk8_s3": (_cfg(MFMA_32x32x2, (4, 1), (1, 2), 8, stages=2), _opt(mapk=4, plr=3)),
     "mt64x64_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (2, 2), 16), _opt(wgm=8, mapk=8, xcd=8, plr=2)),
     "mt16x16_a16_wg1x1_dk16_s3_plr3": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, mapk=4)),
+    # stream-K on one-wave tiles (plain and transposed) for the VM and GPU stream-K tests
+    "mt32x32_a32_wg1x1_dk16_s3_stk": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, stk=1)),
+    "mt32x32_a16_wg2x2_dk16_stk_tn": (_cfg(MFMA_16x16x4, (2, 2), (1, 1), 16, ta=True), _opt(stk=1)),
     # split-K (default split count 4) on a one-wave tile, plain and transposed
     "mt32x32_a32_wg1x1_dk16_s3_sk4": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, stages=2), _opt(plr=3, sk=4)),
     "mt32x32_a32_wg1x1_dk16_sk4_tt": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, ta=True, tb=True), _opt(sk=4)),
@@ -146,6 +154,45 @@ CANDIDATES: Dict[str, Tuple[float, float]] = {
     "mt128x64_a16_wg2x2_dk32_s3_occ2": (0.940, 0.66e-6),
     "mt64x64_a16_wg1x4_dk32_s3": (0.913, 0.0),
 }
+# small-tile instance attached (sgemm_set_edge_kernel) to the large-tile ones
+# for thin edge strips: the 64 x 64 tile with split-K for the strips' few tiles
+EDGE_KERNEL: Dict[str, str] = {
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": "mt64x64_a16_wg1x4_dk32_s3",
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": "mt64x64_a16_wg1x4_dk32_s3",
+    "mt256x256_a32_wg2x2_dk24_s3": "mt64x64_a16_wg1x4_dk32_s3",
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": "mt64x64_a16_wg1x4_dk32_s3",
+}
+
+
+def edge_interior(name: str, m: int, n: int, k: int) -> Tuple[int, int]:
+    """(m, n) of the interior the host library gives the instance itself when
+    its EDGE_KERNEL is attached (the rule of sgemm_set_edge_kernel: a strip of
+    at most a quarter of a tile next to a non-empty interior goes to the edge
+    kernel)."""
+    if name not in EDGE_KERNEL or k == 0:
+        return m, n
+    cfg, _ = SOLUTIONS[name]
+    t0, t1 = cfg.tile_size
+    me, ne = m % t0, n % t1
+    if not (me and me * 4 <= t0 and m > me):
+        me = 0
+    if not (ne and ne * 4 <= t1 and n > ne):
+        ne = 0
+    return m - me, n - ne
+
+
+# resident stream-K work-groups per CU of the stream-K instances (the
+# compiler's occupancy of generated_gemm_streamk; the host library queries it)
+STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
+    "mt64x64_a16_wg1x4_dk32_s3": 3,
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": 2,
+}
+# rate of the streamed tiles relative to whole tiles: interleaved runs at
+# 1792^2..4864^2 x 4096 and 3000^3 measured 0.89-0.92 of the model's whole-tile
+# rate when every tile is streamed, approaching 1 as the streamed share falls
+_STREAM_K_RATE = 0.91
+# the gap between two dependent launches on one stream
+_LAUNCH_SECONDS = 4e-6
 # peak FP32 MFMA rate of one CU (157.3 TFLOP/s / 256) and the share of HBM
 # write bandwidth one CU's epilogue gets when all store at once (fitted)
 _CU_FLOPS = 157.3e12 / GFX950_COMPUTE_UNITS
@@ -213,7 +260,45 @@ def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_CO
     return max(1, min(s, ktiles))
 
 
+def stream_k_tiles(tiles: int, groups: int, k: int, mode: int = 1, depth_k: int = 1, max_rounds: int = 0) -> int:
+    """Tiles of the stream-K phase the host library gives an unsplit launch of
+    ``tiles`` tiles over ``groups`` resident stream-K work-groups (the rule of
+    sgemm_set_stream_k; 0 = no stream-K): with T > G, the last partial round
+    plus one whole round, T % G + G tiles, when ceil(T / G) rounds cost at
+    least 3% over T / G and take at most ``max_rounds`` (0: any; mode 1) or
+    always (mode 2, G tiles when T % G == 0), as long as those tiles' K tiles
+    (``depth_k`` deep) times G stay below 2^32."""
+    if mode == 0 or groups <= 0 or k == 0 or tiles <= groups:
+        return 0
+    rem = tiles % groups
+    if mode == 1:
+        rounds = -(-tiles // groups)
+        if rem == 0 or rounds * groups * 100 < tiles * 103 or (max_rounds and rounds > max_rounds):
+            return 0
+    sk = rem + groups if rem else groups
+    # the kernel's iteration arithmetic is 32-bit
+    if sk * -(-k // depth_k) * groups >= 1 << 32:
+        return 0
+    return sk
+
+
 def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
+    """predicted_launch_seconds of the parts a launch of ``name`` runs: with
+    its EDGE_KERNEL attached, the interior plus the thin edge strips the edge
+    kernel takes, one after another."""
+    mi, ni = edge_interior(name, m, n, k)
+    if (mi, ni) == (m, n):
+        return predicted_launch_seconds(name, m, n, k, compute_units)
+    edge = EDGE_KERNEL[name]
+    t = predicted_launch_seconds(name, mi, ni, k, compute_units)
+    if mi < m:
+        t += predicted_launch_seconds(edge, m - mi, n, k, compute_units) + _LAUNCH_SECONDS
+    if ni < n:
+        t += predicted_launch_seconds(edge, mi, n - ni, k, compute_units) + _LAUNCH_SECONDS
+    return t
+
+
+def predicted_launch_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
     """Time model behind select(): the CU with the most work-groups sets the
     time (rounds of tiles x K splits over the CUs, each work-group a K loop at
     the instance's MFMA efficiency plus its fixed cost and its epilogue's
@@ -221,7 +306,10 @@ def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GF
     launch adds its partials' writes and the last work-group's reads.  Two
     work-groups per CU (occ=2) hide half of each epilogue behind the other's
     K loop.  Wave quantisation is the point: 3000^3 in 256 x 128 tiles is 288
-    work-groups, two rounds on 32 CUs, at half the speed of 64 x 64 tiles."""
+    work-groups, two rounds on 32 CUs, at half the speed of 64 x 64 tiles.  An
+    instance with a stream-K kernel that the host would use on this grid
+    (stream_k_tiles) has no partial round: its tiles are spread evenly over the
+    CUs, the streamed ones at _STREAM_K_RATE."""
     cfg, opt = SOLUTIONS[name]
     t0, t1 = cfg.tile_size
     dk = cfg.depth_k
@@ -236,6 +324,15 @@ def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GF
     loop = 2.0 * t0 * t1 * k_range / (_CU_FLOPS * eff) + fixed
     epilogue = tile_bytes / _CU_WRITE_BYTES_PER_S
     reduce = 2.0 * splits * tile_bytes / _CU_WRITE_BYTES_PER_S if splits > 1 else 0.0
+    sk = 0
+    if splits == 1 and opt.stream_k:
+        groups = compute_units * STREAM_K_GROUPS_PER_CU.get(name, max(opt.occ, 1))
+        sk = stream_k_tiles(tiles, groups, k, 1, dk, opt.stream_k_rounds)
+    if sk:
+        # stream-K: no partial last round; the streamed tiles run at a lower
+        # rate (their cuts, partials and the fix-up)
+        per_cu = ((tiles - sk) * (loop + epilogue / occ) + sk * (loop / _STREAM_K_RATE + epilogue / occ))
+        return per_cu / compute_units + epilogue * (1.0 - 1.0 / occ)
     return rounds * (loop + epilogue / occ) + epilogue * (1.0 - 1.0 / occ) + reduce
 
 

@@ -118,6 +118,16 @@ class GemmOptimizations:
                        The value is the launch's default split count: 0 lets
                        the host pick one per problem (split only when the
                        tiles cannot fill the GPU), 2..16 fixes it.
+    * ``stream_k``  -- (gfx950 only) 1 also builds ``generated_gemm_streamk``,
+                       which spreads the K iterations of the tiles past the
+                       last whole round of work-groups over every resident
+                       work-group (each tile cut at most once, fixed up by a
+                       commutative two-partial sum); the host uses it when a
+                       grid would leave a partial last round.
+    * ``stream_k_rounds`` -- (host policy, written to the .toml) the most
+                       whole-tile rounds of work-groups for which the host
+                       still picks stream-K on its own (0: no limit); tiles
+                       whose stream-K kernel loses on long grids set it.
     """
 
     def __init__(
@@ -131,6 +141,8 @@ class GemmOptimizations:
         pd: Optional[int] = None,
         occ: Optional[int] = None,
         split_k: Optional[int] = None,
+        stream_k: Optional[int] = None,
+        stream_k_rounds: Optional[int] = None,
     ):
         self.level = level
         self.wgm = 1
@@ -141,6 +153,8 @@ class GemmOptimizations:
         self.pd = 1
         self.occ = 0
         self.split_k = 1
+        self.stream_k = 0
+        self.stream_k_rounds = 0
         self._setup_optimizations()
         if wgm is not None:
             self.wgm = wgm
@@ -158,6 +172,10 @@ class GemmOptimizations:
             self.occ = occ
         if split_k is not None:
             self.split_k = split_k
+        if stream_k is not None:
+            self.stream_k = stream_k
+        if stream_k_rounds is not None:
+            self.stream_k_rounds = stream_k_rounds
         if self.wgm < 1:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
@@ -170,6 +188,10 @@ class GemmOptimizations:
             raise RuntimeError(f"Invalid occupancy target {self.occ}")
         if not 0 <= self.split_k <= MAX_SPLIT_K:
             raise RuntimeError(f"Invalid split_k {self.split_k} (0 = auto, or 1..{MAX_SPLIT_K})")
+        if self.stream_k not in (0, 1):
+            raise RuntimeError(f"Invalid stream_k {self.stream_k} (0 or 1)")
+        if self.stream_k_rounds < 0:
+            raise RuntimeError(f"Invalid stream_k_rounds {self.stream_k_rounds} (0 = no limit)")
 
     def _setup_optimizations(self):
         if self.level != 0:
@@ -187,11 +209,13 @@ class GemmOptimizations:
             "pd": int(self.pd),
             "occ": int(self.occ),
             "split_k": int(self.split_k),
+            "stream_k": int(self.stream_k),
+            "stream_k_rounds": int(self.stream_k_rounds),
         }
 
     def __repr__(self) -> str:
         return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
-                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, split_k={self.split_k})")
+                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, split_k={self.split_k}, stream_k={self.stream_k})")
 
 
 def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int,
@@ -541,6 +565,7 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_PD": opt.pd,
         "SG_OCC": opt.occ,
         "SG_SPLITK": int(opt.split_k != 1),
+        "SG_STREAMK": int(opt.stream_k),
         "SG_MAPK": opt.map_k_idx,
         "SG_PLR": opt.plr,
         "SG_GW": opt.gw,
@@ -672,6 +697,8 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     d.update(parse_resource_usage(remarks))
     if opt is not None and opt.split_k != 1:
         d.update({f"splitk_{k}": v for k, v in parse_resource_usage(remarks, "generated_gemm_splitk").items()})
+    if opt is not None and opt.stream_k:
+        d.update({f"streamk_{k}": v for k, v in parse_resource_usage(remarks, "generated_gemm_streamk").items()})
     if extra_keys:
         d.update(extra_keys)
     write_toml(d, toml_path)

@@ -47,6 +47,9 @@ class KernelInfo(ctypes.Structure):
         ("trans_b", ctypes.c_int),
         ("split_k", ctypes.c_int),
         ("split_k_max", ctypes.c_int),
+        ("stream_k", ctypes.c_int),
+        ("stream_k_groups", ctypes.c_int),
+        ("stream_k_rounds", ctypes.c_int),
     ]
 
 
@@ -62,6 +65,10 @@ SIGNATURES = {
     "sgemm_set_split_k": (_int, [_vp, _int]),
     "sgemm_workspace_size": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_size_t)]),
     "sgemm_launch_splits": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
+    "sgemm_set_stream_k": (_int, [_vp, _int]),
+    "sgemm_set_edge_kernel": (_int, [_vp, _vp]),
+    "sgemm_edge_interior": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
+    "sgemm_stream_k_tiles": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
     "sgemm_malloc": (_int, [ctypes.POINTER(_vp), ctypes.c_size_t]),
     "sgemm_free": (_int, [_vp]),
     "sgemm_memcpy_h2d": (_int, [_vp, _vp, ctypes.c_size_t]),
@@ -250,6 +257,30 @@ class Kernel:
         """K ranges a launch of this shape uses with the current setting (1 = no split)."""
         out = _int()
         _check("sgemm_launch_splits", load_library().sgemm_launch_splits(self.handle, m, n, k, ctypes.byref(out)))
+        return int(out.value)
+
+    def set_stream_k(self, mode: int):
+        """0: never stream-K; 1: when a partial last round of work-groups costs >= 3%; 2: whenever tiles > groups."""
+        _check("sgemm_set_stream_k", load_library().sgemm_set_stream_k(self.handle, int(mode)))
+        self._refresh_info()
+
+    def set_edge_kernel(self, edge: Optional["Kernel"]):
+        """Attaches a small-tile kernel for thin edge strips (None detaches); it must stay open while attached."""
+        _check("sgemm_set_edge_kernel", load_library().sgemm_set_edge_kernel(self.handle,
+                                                                            edge.handle if edge else None))
+        self.edge = edge
+
+    def edge_interior(self, m, n, k) -> Tuple[int, int]:
+        """(m, n) of the part of an m x n x k launch this kernel runs itself."""
+        mi, ni = _u32(), _u32()
+        _check("sgemm_edge_interior", load_library().sgemm_edge_interior(self.handle, m, n, k, ctypes.byref(mi),
+                                                                         ctypes.byref(ni)))
+        return int(mi.value), int(ni.value)
+
+    def stream_k_tiles(self, m, n, k) -> int:
+        """Tiles of the stream-K phase of an m x n x k launch (0: no stream-K)."""
+        out = _int()
+        _check("sgemm_stream_k_tiles", load_library().sgemm_stream_k_tiles(self.handle, m, n, k, ctypes.byref(out)))
         return int(out.value)
 
     def _args(self, a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta):

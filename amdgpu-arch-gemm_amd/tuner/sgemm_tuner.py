@@ -439,6 +439,7 @@ def main(argv=None):
                     help="comma-separated macro-tiles MT0xMT1 for stage 1 (default: the --space list)")
     ap.add_argument("--stage1-depths", default=",".join(str(d) for d in STAGE1_DEPTHS),
                     help="comma-separated K depths every stage-1 geometry is tried at")
+    ap.add_argument("--summary", default=None, help="write a markdown summary of the sweep to this path")
     args = ap.parse_args(argv)
     m, n, k, out = args.m, args.n, args.k, args.output_folder
     split_ks = [int(x) for x in args.split_k.split(",") if x.strip()]
@@ -510,7 +511,30 @@ def main(argv=None):
           f"wgm: {best['wgm']}, plr: {best['plr']}, gw: {best['gw']}, map_k_idx: {best['map_k_idx']}, "
           f"vmem_stage: {best['vmem_stage']}, xcd: {best['xcd']}, split_k: {best.get('split_k', 1)}, "
           f"occ: {best.get('occ', 0)} -> {out}/generated_gemm.co")
+    if args.summary:
+        write_summary(args.summary, recs, best, m, n, k, argv if argv is not None else sys.argv[1:])
     return 0
+
+
+def write_summary(path: str, recs: List[Dict], best: Dict, m: int, n: int, k: int, argv: Sequence[str],
+                  top: int = 10):
+    """Markdown summary of a sweep: the command, points by status, the top
+    points by Gflops and the emitted (validated) winner."""
+    from collections import Counter
+    status = Counter(r["status"] if not r["status"].startswith("error") else "error" for r in recs)
+    ok = sorted((r for r in recs if r["status"] == "ok" and r["gflops"] > 0), key=lambda r: -r["gflops"])
+    lines = [f"# Tuner sweep at {m}x{n}x{k}", "", "Command (from the repository root on the GPU box):", "",
+             "    python amdgpu-arch-gemm_amd/tuner/sgemm_tuner.py " + " ".join(argv), "",
+             f"{len(recs)} points: " + ", ".join(f"{v} {s}" for s, v in sorted(status.items())) + ".", "",
+             f"| rank | point | tile | TFLOP/s | % of {157.3} |", "|---|---|---|---|---|"]
+    for i, r in enumerate(ok[:top], 1):
+        lines.append(f"| {i} | `{r['point']}` | {r['tile'][0]}x{r['tile'][1]} | {r['gflops'] / 1e3:.2f} | "
+                     f"{r['gflops'] / 1e3 / 157.3 * 100:.1f} |")
+    lines += ["", f"Emitted `generated_gemm.co` + `.toml`: `{best['point']}`, {best['gflops'] / 1e3:.2f} TFLOP/s; "
+              f"validation {best.get('validation', 'not run')}.", ""]
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        f.write("\n".join(lines))
 
 
 if __name__ == "__main__":

@@ -50,6 +50,10 @@ WORKLOADS = {
     # split-K kernel exists for (64 tiles of 64 x 64, 4 K ranges each, on 256
     # compute units)
     "deepk": (512, 512, 16384, 5, S.SGEMM_DIST_UNIFORM),
+    # not a BASELINE.json config: one past the headline in every dimension, so
+    # a fixed tile grid leaves one-row and one-column sliver tiles (edge
+    # strips) and a partial last round
+    "q4097": (4097, 4097, 4097, 6, S.SGEMM_DIST_UNIFORM),
 }
 # BASELINE.json's metric, verbatim
 HEADLINE_METRIC = "FP32 SGEMM TFLOP/s at 4096\u00b3 NN; % of MI355X FP32 MFMA peak"
@@ -137,6 +141,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-k", type=int, default=None,
                     help="K ranges per output tile (0 = per problem; default: the instance's own setting)")
+    ap.add_argument("--stream-k", type=int, default=None,
+                    help="stream-K mode (0 off, 1 auto, 2 forced; default: the instance's own setting)")
+    ap.add_argument("--no-edge", action="store_true", help="do not attach the catalog's edge kernel")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -154,10 +161,20 @@ def main():
     A = S.fill_matrix(m, k, seed, 0, dist)
     B = S.fill_matrix(k, n, seed, 1, dist)
     kern = S.Kernel(co, toml)
+    edge = None
+    if name in catalog.EDGE_KERNEL and not args.no_edge:
+        edge = S.Kernel(*catalog.paths(catalog.EDGE_KERNEL[name]))
+        kern.set_edge_kernel(edge)
+    interior = kern.edge_interior(m, n, k)
+    if interior != (m, n):
+        log(f"edge strips: interior {interior[0]}x{interior[1]} on {name}, strips on {catalog.EDGE_KERNEL[name]}")
     if args.split_k is not None:
         kern.set_split_k(args.split_k)
+    if args.stream_k is not None:
+        kern.set_stream_k(args.stream_k)
     splits = kern.launch_splits(m, n, k)
-    log(f"K ranges per output tile: {splits}")
+    sk_tiles = kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0
+    log(f"K ranges per output tile: {splits}; stream-K tiles: {sk_tiles}")
     dA, dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
     dD = S.DeviceBuffer(m * n * 4)
     dD.zero()
@@ -219,6 +236,8 @@ def main():
             "alpha": 1.0, "beta": 0.0,
             "kernel": name,
             "split_k": splits,
+            "stream_k_tiles": sk_tiles,
+            "edge_kernel": catalog.EDGE_KERNEL[name] if interior != (m, n) else None,
             "pct_of_fp32_mfma_peak": round(100.0 * value / FP32_MFMA_PEAK_TFLOPS, 2),
             "device": info["name"],
             "peak_sclk_mhz": info["clock_khz"] / 1000.0,
@@ -243,6 +262,8 @@ def main():
     else:
         line["cpu_baseline"] = None
     kern.close()
+    if edge is not None:
+        edge.close()
     print(json.dumps(line), flush=True)
 
 

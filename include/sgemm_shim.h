@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 4
+#define SGEMM_SHIM_ABI_VERSION 6
 
 /* Most K ranges generated_gemm_splitk splits one output tile into. */
 #define SGEMM_MAX_SPLIT_K 16
@@ -74,6 +74,12 @@ typedef struct sgemm_kernel_info {
     int split_k;          /* K ranges per output tile for sgemm_launch: 0 = chosen per problem
                              (sgemm_set_split_k), else a fixed count (toml key split_k, default 1) */
     int split_k_max;      /* SGEMM_MAX_SPLIT_K if the code object has generated_gemm_splitk, else 1 */
+    int stream_k;         /* stream-K setting for unsplit launches (sgemm_set_stream_k; toml key
+                             stream_k, default 0) */
+    int stream_k_groups;  /* work-groups of generated_gemm_streamk resident at once (per-CU occupancy
+                             x compute units), 0 when the code object has no stream-K kernel */
+    int stream_k_rounds;  /* most rounds of whole tiles the auto setting still uses stream-K for
+                             (toml key stream_k_rounds; 0: no limit) */
 } sgemm_kernel_info;
 
 /* Message of the last failure on this thread ("" if none). */
@@ -126,13 +132,53 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
 int sgemm_set_split_k(sgemm_handle* h, int splits);
 
 /* Device bytes the handle's workspace needs for an m x n x k launch with its
- * current split count (0 when the launch does not split).  No counterpart in
- * the reference (its kernel needs no workspace). */
+ * current split and stream-K settings (0 when the launch needs none).  No
+ * counterpart in the reference (its kernel needs no workspace). */
 int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes);
 
 /* K ranges an m x n x k launch with the handle's current setting uses
  * (1: generated_gemm, no split).  No counterpart in the reference. */
 int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits);
+
+/* Sets how unsplit launches treat a tile grid that leaves a partial last
+ * round of work-groups: 0 never uses stream-K; 1 (auto) launches
+ * generated_gemm_streamk when the grid of T tiles over G = stream_k_groups
+ * resident work-groups has T > G and ceil(T / G) rounds cost at least 3% over
+ * T / G, within the instance's stream_k_rounds; 2 whenever T > G.  The stream-K launch runs G work-groups: the last
+ * partial round plus one whole round of tiles (T % G + G tiles, G when T % G
+ * == 0) are cut into G equal runs of K iterations, each at least one tile
+ * long, so a tile is cut at most once and its two partials are added by the
+ * later of the two work-groups (the same bits whichever finishes last); the
+ * other tiles run whole.  The handle's workspace then holds 2 G partial tiles
+ * and G tickets.  SGEMM_E_CONFIG without generated_gemm_streamk.  No
+ * counterpart in the reference (its grid is one work-group per tile,
+ * generator_runner.cpp:127-131). */
+int sgemm_set_stream_k(sgemm_handle* h, int mode);
+
+/* Attaches `edge`, another loaded kernel with a smaller tile and the same
+ * trans_a / trans_b, that later launches of h use for thin edge strips: when
+ * m % MT0 (or n % MT1) is at most a quarter of h's tile, the launch runs h's
+ * kernel on the tile-aligned interior and the edge kernel on the strip of
+ * rows past the last whole tile row (every column) and the strip of columns
+ * past the last whole tile column (interior rows), one after another on h's
+ * stream, instead of paying a whole tile of MFMA work for each sliver (4097^3
+ * in 256 x 128 tiles: 561 tiles, 49 of them one row or column wide).  The
+ * strips use the edge kernel's own split-K / stream-K settings and workspace.
+ * NULL detaches.  `edge` must stay open while attached; launches through h
+ * must not overlap other work on `edge`'s workspace.  No counterpart in the
+ * reference, whose tuner skips shapes its tiles do not divide
+ * (tuner/sgemm_tuner.py:97-100). */
+int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge);
+
+/* The interior (*m_int x *n_int) an m x n x k launch of h gives h's own
+ * kernel: m and n unless an edge kernel takes thin strips.  No counterpart in
+ * the reference. */
+int sgemm_edge_interior(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* m_int, uint32_t* n_int);
+
+/* Tiles an m x n x k launch with the handle's current settings gives the
+ * stream-K phase (0: the launch does not use generated_gemm_streamk).  No
+ * counterpart in the reference. */
+int sgemm_stream_k_tiles(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* sk_tiles);
 
 /* Device memory (generator_runner.cpp:236-242, :291, :319-322). */
 int sgemm_malloc(void** dptr, size_t bytes);
@@ -146,7 +192,8 @@ int sgemm_memset(void* dptr, int value, size_t bytes);
  * the same 80-byte kernarg buffer, passed through hipModuleLaunchKernel's
  * HIP_LAUNCH_PARAM_BUFFER_POINTER with a grid of (ceil(m/MT0), ceil(n/MT1)) blocks.
  * With a split count above 1 (sgemm_set_split_k) it launches the split kernel
- * instead, with the handle's workspace; launches of one handle share that
+ * instead (or, under sgemm_set_stream_k, the stream-K kernel), with the handle's
+ * workspace; launches of one handle share that
  * workspace, so they must run in order on the handle's stream.  Device
  * pointers need 4-byte alignment only (SGEMM_E_INVALID otherwise). */
 int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,

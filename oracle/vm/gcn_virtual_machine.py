@@ -538,6 +538,8 @@ _salu2("s_mul_hi_u32", lambda a, b: (a * b) >> 32)
 _salu2("s_and_b32", lambda a, b: a & b, lambda a, b, r: (r & MASK32) != 0)
 _salu2("s_or_b32", lambda a, b: a | b, lambda a, b, r: (r & MASK32) != 0)
 _salu2("s_xor_b32", lambda a, b: a ^ b, lambda a, b, r: (r & MASK32) != 0)
+_salu2("s_andn2_b32", lambda a, b: a & ~b & MASK32, lambda a, b, r: (r & MASK32) != 0)
+_salu2("s_orn2_b32", lambda a, b: (a | ~b) & MASK32, lambda a, b, r: (r & MASK32) != 0)
 _salu2("s_lshl_b32", lambda a, b: a << (b & 31), lambda a, b, r: (r & MASK32) != 0)
 _salu2("s_lshr_b32", lambda a, b: a >> (b & 31), lambda a, b, r: (r & MASK32) != 0)
 _salu2("s_ashr_i32", lambda a, b: _sext(a, 32) >> (b & 31), lambda a, b, r: (r & MASK32) != 0)
@@ -972,6 +974,23 @@ def _v_readfirstlane(vm, ins, prog):
     mask = vm.exec_mask()
     lane = int(np.argmax(mask)) if mask.any() else 0
     vm.ws32(ins.ops[0], int(src[lane]))
+
+
+@op("v_readlane_b32")
+def _v_readlane(vm, ins, prog):
+    """sdst = vsrc[lane]; the lane select is an SGPR or a constant (its low 6
+    bits), and EXEC does not apply."""
+    lane = vm.rs32(ins.ops[2]) & (WAVE - 1)
+    vm.ws32(ins.ops[0], int(vm.regfile(ins.ops[1])[ins.ops[1].index][lane]))
+
+
+@op("v_writelane_b32")
+def _v_writelane(vm, ins, prog):
+    """vdst[lane] = ssrc; the other lanes keep their value, EXEC does not apply
+    (the compiler uses it to park scalar registers in vector lanes)."""
+    lane = vm.rs32(ins.ops[2]) & (WAVE - 1)
+    dst = ins.ops[0]
+    vm.regfile(dst)[dst.index][lane] = np.uint32(vm.rs32(ins.ops[1]))
 
 
 @op("v_lshl_add_u64")
@@ -1413,11 +1432,17 @@ def pack_splitk_kernargs(base: bytes, ws: int, tickets: int, splits: int) -> byt
     return raw + b"\0" * (104 - len(raw))
 
 
+def pack_streamk_kernargs(base: bytes, ws: int, tickets: int, sk_tiles: int, groups: int) -> bytes:
+    """The stream-K kernel's image: the 15 arguments (80 bytes), then ws at 80,
+    tickets at 88, sk_tiles at 96 and groups at 100: 104 bytes."""
+    return base[:80] + struct.pack("<QQII", ws, tickets, sk_tiles, groups)
+
+
 def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: np.ndarray,
               C: Optional[np.ndarray] = None, alpha: float = 1.0, beta: float = 0.0,
               mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None,
               splits: int = 0, order: Optional[Sequence[Tuple[int, int, int]]] = None,
-              misalign: int = 0) -> Tuple[np.ndarray, Dict]:
+              misalign: int = 0, stream_k: Optional[Tuple[int, int]] = None) -> Tuple[np.ndarray, Dict]:
     """Runs a compiled SGEMM kernel on column-major A, B, C.
 
     Without ``mnk`` the problem is A (m x k) @ B (k x n) with tight leading
@@ -1427,7 +1452,10 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     full ldd x n storage when ``mnk`` is given, else m x n.
 
     ``splits >= 1`` runs ``generated_gemm_splitk`` instead, over a grid of
-    ``splits`` K ranges, with its workspace and zeroed tickets; ``order`` is the
+    ``splits`` K ranges, with its workspace and zeroed tickets;
+    ``stream_k = (groups, sk_tiles)`` runs ``generated_gemm_streamk`` over
+    ``groups`` work-groups with ``sk_tiles`` stream-K tiles, its workspace of
+    2 * groups partial tiles and ``groups`` zeroed tickets; ``order`` is the
     work-group order (see run_kernel).  The returned info holds the tickets
     after the launch.  ``misalign`` (a multiple of 4 below 16) moves the start
     of every buffer that many bytes past a 4 KiB boundary."""
@@ -1448,9 +1476,14 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     nwgx, nwgy = (m + tile[0] - 1) // tile[0], (n + tile[1] - 1) // tile[1]
     blobs = [A.ravel(order="F"), B.ravel(order="F"), Cm.ravel(order="F"),
              np.zeros(ldd * n, dtype=np.float32)]
+    if splits and stream_k:
+        raise ValueError("a launch is split-K or stream-K, not both")
     if splits:
         blobs.append(np.full(nwgx * nwgy * splits * tile[0] * tile[1], np.nan, dtype=np.float32))
         blobs.append(np.zeros(nwgx * nwgy, dtype=np.uint32))
+    if stream_k:
+        blobs.append(np.full(stream_k[0] * 2 * tile[0] * tile[1], np.nan, dtype=np.float32))
+        blobs.append(np.zeros(stream_k[0], dtype=np.uint32))
     # every buffer gets exactly its own bytes as an allocated region, with
     # unallocated gaps between them: any access past a buffer raises
     offs, pos = [], 4096
@@ -1467,6 +1500,10 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
         ka = pack_splitk_kernargs(ka, offs[4], offs[5], splits)
         grid: Tuple[int, ...] = (nwgx, nwgy, splits)
         prog = as_program(program, "generated_gemm_splitk")
+    elif stream_k:
+        ka = pack_streamk_kernargs(ka, offs[4], offs[5], stream_k[1], stream_k[0])
+        grid = (stream_k[0], 1, 1)
+        prog = as_program(program, "generated_gemm_streamk")
     else:
         grid = (nwgx, nwgy)
         prog = as_program(program)
@@ -1476,5 +1513,7 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
         D = D[:m, :]
     if splits:
         info["tickets"] = np.frombuffer(mem.read_bytes(offs[5], nwgx * nwgy * 4), dtype=np.uint32).copy()
+    if stream_k:
+        info["tickets"] = np.frombuffer(mem.read_bytes(offs[5], stream_k[0] * 4), dtype=np.uint32).copy()
     info.update({"instructions": count, "grid": grid, "d_offset": offs[3], "memory": mem})
     return D, info

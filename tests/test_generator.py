@@ -286,7 +286,7 @@ MEASURED_BEST = [
     ((2500, 2500, 2500), "mt64x64_a16_wg1x4_dk32_s3"),           # 122.8 (not fitted on)
     ((7000, 7000, 1000), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 139.3 (not fitted on)
     ((4095, 4095, 4095), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.4 (not fitted on)
-    ((1792, 1792, 1792), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 109.3 (not fitted on)
+    ((1792, 1792, 1792), "mt64x64_a16_wg1x4_dk32_s3"),           # 127.9 with stream-K; 128x64 occ2: 111.8
     ((16384, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),  # 137.1; 128x64 occ2: 126.7
     ((4096, 4096, 128), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),   # 108.5; 128x64 occ2: 103.0
     ((8192, 8192, 512), "mt256x128_a32_wg2x2_dk16_s3_occ2"),        # 143.3; plr=2: 141.8

@@ -508,6 +508,131 @@ def test_host_split_rule_matches_the_catalog(kernels):
                 assert kern.launch_splits(m, n, k) == catalog.auto_split(name, m, n, k, cus), (name, m, n, k)
 
 
+# ---------------------------------------------------------------- stream-K
+STREAM_INSTANCES = ["mt32x32_a32_wg1x1_dk16_s3_stk", "mt32x32_a16_wg2x2_dk16_stk_tn", "mt64x64_a16_wg1x4_dk32_s3",
+                    "mt128x64_a16_wg2x2_dk32_s3_occ2"]
+
+
+def _stream_shape(cfg, groups, rounds, seed):
+    """A ragged m x n whose tile grid has about `rounds` * groups tiles."""
+    rng = np.random.default_rng(seed)
+    t0, t1 = cfg.tile_size
+    target = int(rounds * groups)
+    tx = max(2, int(round((target * t1 / t0) ** 0.5)))
+    ty = -(-target // tx)
+    return tx * t0 - int(rng.integers(0, t0)), ty * t1 - int(rng.integers(0, t1))
+
+
+@pytest.mark.parametrize("name", STREAM_INSTANCES)
+@pytest.mark.parametrize("rounds,mode", [(1.3, 1), (2.6, 2), (2.0, 2)])
+def test_stream_k(kernels, name, rounds, mode):
+    """generated_gemm_streamk on a grid with a partial last round (and, forced,
+    on whole rounds): the library's stream-K tile count is the catalog's rule,
+    D matches the oracle, repeated launches give the same bits (tickets
+    re-armed, the two-partial sum commutative), and the plain launch agrees to
+    the same bar."""
+    cfg, _ = catalog.SOLUTIONS[name]
+    with _kernel(name) as kern:
+        groups = kern.info.stream_k_groups
+        assert groups > 0, "the code object has no stream-K kernel"
+        m, n = _stream_shape(cfg, groups, rounds, int(rounds * 10) + mode)
+        k = 3 * cfg.depth_k + 7
+        t0, t1 = cfg.tile_size
+        tiles = -(-m // t0) * -(-n // t1)
+        kern.set_stream_k(mode)
+        sk = kern.stream_k_tiles(m, n, k)
+        _say(f"stream-K {name} {m}x{n}x{k}: {tiles} tiles, {groups} groups, mode {mode}, {sk} stream-K tiles")
+        assert sk == catalog.stream_k_tiles(tiles, groups, k, mode, cfg.depth_k, kern.info.stream_k_rounds)
+        assert sk > 0
+        A, B, opA, opB = _operands(name, m, n, k, 23)
+        C = S.fill_matrix(m, n, 23, 2)
+        dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (A, B, C))
+        dD = S.DeviceBuffer(4 * m * n)
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=-1.0)
+        kern.synchronize()
+        D = dD.download().reshape(n, m).T.copy()
+        for _ in range(2):
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=-1.0)
+        kern.synchronize()
+        assert np.array_equal(dD.download().reshape(n, m).T, D), "repeated stream-K launches differ"
+        kern.set_stream_k(0)
+        assert kern.stream_k_tiles(m, n, k) == 0
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=-1.0)
+        kern.synchronize()
+        D_plain = dD.download().reshape(n, m).T.copy()
+    ref = oracle.cpu_gemm_mt(opA, opB, C, 0.5, -1.0, threads=16)
+    _check(D, ref, k, f"{name} stream-K")
+    _check(D_plain, ref, k, f"{name} plain")
+
+
+# ---------------------------------------------------------------- edge strips
+EDGE_CASES = [
+    # (main, edge, m, n, k): thin strips below and right of the interior
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 3 + 5, 128 * 4 + 7, 100),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 2 + 1, 128 * 5, 257),   # bottom only
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 2, 128 * 3 + 1, 64),    # right only
+    ("mt256x256_a32_wg2x2_dk24_s3", "mt64x64_a16_wg1x4_dk32_s3", 1025, 1025, 1025),
+    ("mt256x256_a32_wg2x2_dk16_s3_tn", "mt64x64_a16_wg2x2_dk32_s3_tn", 256 * 2 + 33, 256 + 3, 90),  # A^T
+    ("mt128x64_a16_wg2x2_dk32_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 128 * 3 + 2, 64 * 2 + 16, 77),
+]
+
+
+@pytest.mark.parametrize("main,edge,m,n,k", EDGE_CASES)
+def test_edge_kernel_strips(kernels, main, edge, m, n, k):
+    """A launch with an attached edge kernel: the main kernel on the
+    tile-aligned interior, the edge kernel on the thin bottom and right strips.
+    D against the oracle with padded leading dimensions (rows past m of D
+    untouched), the library's interior is the catalog's rule, and
+    sgemm_launch_noalloc gives the same bits."""
+    cfg, _ = catalog.SOLUTIONS[main]
+    ra, ca = (k, m) if cfg.trans_a else (m, k)
+    rb, cb = (n, k) if cfg.trans_b else (k, n)
+    lda, ldb, ldc, ldd = ra + 3, rb + 1, m + 2, m + 5
+    Af, Bf, Cf = S.fill_matrix(lda, ca, 41, 0), S.fill_matrix(ldb, cb, 41, 1), S.fill_matrix(ldc, n, 41, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    with _kernel(main) as kern, _kernel(edge) as ekern:
+        assert kern.edge_interior(m, n, k) == (m, n)
+        kern.set_edge_kernel(ekern)
+        mi, ni = kern.edge_interior(m, n, k)
+        _say(f"edge strips {main} + {edge} {m}x{n}x{k}: interior {mi}x{ni}")
+        assert (mi, ni) == catalog.edge_interior(main, m, n, k) if main in catalog.EDGE_KERNEL else (mi, ni) != (m, n)
+        assert (mi, ni) != (m, n)
+        outs = []
+        for launch in ("launch", "launch_noalloc"):
+            dD = S.DeviceBuffer.from_array(np.full((ldd, n), 9.5, dtype=np.float32))
+            getattr(kern, launch)(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5, lda=lda, ldb=ldb, ldc=ldc, ldd=ldd)
+            kern.synchronize()
+            outs.append(dD.download().reshape(n, ldd).T.copy())
+    assert np.array_equal(outs[0], outs[1]), "noalloc and launch differ"
+    Dfull = outs[0]
+    opA = np.asfortranarray(Af[:ra, :ca].T if cfg.trans_a else Af[:m, :k])
+    opB = np.asfortranarray(Bf[:rb, :cb].T if cfg.trans_b else Bf[:k, :n])
+    _check(Dfull[:m, :], oracle.cpu_gemm_mt(opA, opB, Cf[:m, :n], 1.5, -0.5, threads=16), k, f"{main}+{edge}")
+    assert np.all(Dfull[m:, :] == 9.5), "rows past m of D were written"
+
+
+def test_edge_kernel_errors(kernels):
+    with _kernel("mt256x128_a32_wg2x2_dk16_s3_occ2") as kern, _kernel("mt64x64_a16_wg2x2_dk32_s3_tn") as tn, \
+            _kernel("mt256x256_a32_wg2x2_dk24_s3") as big:
+        with pytest.raises(S.SgemmError, match="layout"):
+            kern.set_edge_kernel(tn)
+        with pytest.raises(S.SgemmError, match="larger"):
+            kern.set_edge_kernel(big)
+        with pytest.raises(S.SgemmError):
+            kern.set_edge_kernel(kern)
+        kern.set_edge_kernel(None)
+
+
+def test_stream_k_errors(kernels):
+    with _kernel("mt256x128_a32_wg2x2_dk16_s3_occ2") as kern:
+        assert kern.info.stream_k_groups == 0
+        with pytest.raises(S.SgemmError):
+            kern.set_stream_k(1)
+    with _kernel("mt64x64_a16_wg1x4_dk32_s3") as kern:
+        with pytest.raises(S.SgemmError):
+            kern.set_stream_k(3)
+
+
 def test_split_k_errors(kernels):
     with _kernel("mt32x32_a32_wg1x1_dk16_s3_sk4") as kern:
         assert kern.split_k == 4 and kern.info.split_k_max == 16

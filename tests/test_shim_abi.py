@@ -34,8 +34,8 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 4
-    assert ctypes.sizeof(S.KernelInfo) == 4 * 19  # 19 ints, as in sgemm_kernel_info
+    assert lib.sgemm_abi_version() == 6
+    assert ctypes.sizeof(S.KernelInfo) == 4 * 22  # 22 ints, as in sgemm_kernel_info
 
 
 def test_noalloc_limits_match_the_header():
@@ -92,6 +92,10 @@ def test_null_arguments_are_rejected():
     assert lib.sgemm_launch_splits(None, 64, 64, 64, None) == -1
     assert lib.sgemm_launch_noalloc(None, None, None, None, None, 64, 64, 16, 64, 16, 64, 64, 1.0, 0.0) == -1
     assert b"null handle" in lib.sgemm_last_error()
+    assert lib.sgemm_set_stream_k(None, 1) == -1
+    assert lib.sgemm_stream_k_tiles(None, 64, 64, 64, None) == -1
+    assert lib.sgemm_set_edge_kernel(None, None) == -1
+    assert lib.sgemm_edge_interior(None, 64, 64, 64, None, None) == -1
 
 
 def test_runner_usage_error_exit_code():

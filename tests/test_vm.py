@@ -428,6 +428,67 @@ def test_split_k_in_vm(name, m, n, k, splits):
         assert np.array_equal(D2, D) and not info2["tickets"].any()
 
 
+# ------------------------------------------------------------- stream-K
+STREAM_CASES = [
+    # (instance, m, n, k, groups): T tiles over G work-groups, stream-K tiles T % G + G
+    ("mt32x32_a32_wg1x1_dk16_s3_stk", 96, 96, 16 * 7 + 5, 4),     # 9 tiles: 5 streamed, 4 whole; K remainder
+    ("mt32x32_a32_wg1x1_dk16_s3_stk", 70, 45, 100, 4),            # 6 ragged tiles, all streamed
+    ("mt32x32_a32_wg1x1_dk16_s3_stk", 33, 200, 40, 3),            # 14 tiles of 3 K tiles, 5 streamed
+    ("mt32x32_a16_wg2x2_dk16_stk_tn", 64, 96, 50, 5),             # A^T, four waves, 6 tiles
+]
+
+
+@pytest.mark.parametrize("name,m,n,k,groups", STREAM_CASES)
+def test_stream_k_in_vm(name, m, n, k, groups):
+    """generated_gemm_streamk: the K iterations of the last partial round plus
+    one whole round of tiles are cut into `groups` equal runs, a tile cut at a
+    run boundary gets a head and a tail partial, and the later of the two
+    work-groups adds them.  Checked against float64, with every ticket re-armed,
+    and bit-identical whatever order the work-groups run in (the two-term sum
+    is commutative)."""
+    prog, cfg = program(name, "generated_gemm_streamk")
+    t0, t1 = cfg.tile_size
+    tiles = -(-m // t0) * -(-n // t1)
+    sk = catalog.stream_k_tiles(tiles, groups, k, mode=2)
+    assert groups <= sk <= tiles and (tiles - sk) % groups == 0
+    A, B, C, opA, opB = _split_operands(cfg, m, n, k, 8)
+    D, info = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m,
+                        stream_k=(groups, sk))
+    assert oracle.normwise_error(D, oracle.gemm_f64(opA, opB, C, 0.5, 1.5)) <= oracle.tolerance(k)
+    assert not info["tickets"].any()
+    rng = np.random.default_rng(1)
+    order = [(x, 0, 0) for x in range(groups)]
+    for o in (order[::-1], [order[i] for i in rng.permutation(groups)]):
+        D2, info2 = run_sgemm(prog, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, mnk=(m, n, k), ldd=m,
+                              stream_k=(groups, sk), order=o)
+        assert np.array_equal(D2, D) and not info2["tickets"].any()
+
+
+def test_stream_k_without_cuts_equals_the_plain_kernel():
+    """T = 2 G tiles with G stream-K tiles: every run is exactly one tile, so no
+    tile is cut and each is computed over its whole K like the plain kernel --
+    the same bits."""
+    name = "mt32x32_a32_wg1x1_dk16_s3_stk"
+    plain, cfg = program(name)
+    sk, _ = program(name, "generated_gemm_streamk")
+    A, B, C, _, _ = _split_operands(cfg, 128, 64, 83, 9)          # 8 tiles
+    D1, _ = run_sgemm(plain, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5)
+    D2, info = run_sgemm(sk, cfg.tile_size, cfg.num_workitems, A, B, C, 0.5, 1.5, stream_k=(4, 4))
+    assert np.array_equal(D1, D2) and not info["tickets"].any()
+
+
+def test_stream_k_plan_rule():
+    """The host rule (sgemm_set_stream_k): no stream-K until tiles exceed the
+    groups, auto mode only when the partial last round costs >= 3%."""
+    assert catalog.stream_k_tiles(512, 512, 4096) == 0           # one whole round
+    assert catalog.stream_k_tiles(722, 512, 4096) == 722 - 512 + 512
+    assert catalog.stream_k_tiles(1000, 512, 4096) == 0           # 2 rounds vs 1.95: under 3%
+    assert catalog.stream_k_tiles(1000, 512, 4096, mode=2) == 1000 - 512 + 0 if False else 488 + 512
+    assert catalog.stream_k_tiles(1024, 512, 4096, mode=2) == 512  # whole rounds, forced
+    assert catalog.stream_k_tiles(100, 512, 4096, mode=2) == 0     # fewer tiles than groups: split-K's case
+    assert catalog.stream_k_tiles(722, 512, 0) == 0 and catalog.stream_k_tiles(722, 512, 64, mode=0) == 0
+
+
 def test_split_k_with_one_range_equals_the_plain_kernel():
     name = "mt32x32_a32_wg1x1_dk16_s3_sk4"
     plain, cfg = program(name)
@@ -623,6 +684,22 @@ def test_s_load_widths_known_answer(nd, sfx):
     assert vm.s[30] == 0xDEADBEEF
 
 
+def test_readlane_and_writelane_ignore_exec():
+    """v_writelane_b32 / v_readlane_b32 (the compiler's way of parking scalar
+    registers in vector lanes): one lane written and read, selected by a
+    constant or an SGPR, whatever EXEC holds."""
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.v[5] = np.arange(64, dtype=np.uint32) + 100
+    vm.s[4], vm.s[6] = 0xCAFE, 37
+    vm.exec = 0   # no lane active: neither instruction looks at EXEC
+    vm.run("generated_gemm:\n v_writelane_b32 v5, s4, 3\n v_writelane_b32 v5, 0x77, s6\n"
+           " v_readlane_b32 s8, v5, 3\n v_readlane_b32 s9, v5, s6\n v_readlane_b32 s10, v5, 63\n s_endpgm\n")
+    want = np.arange(64, dtype=np.uint32) + 100
+    want[3], want[37] = 0xCAFE, 0x77
+    assert np.array_equal(vm.v[5], want)
+    assert (int(vm.s[8]), int(vm.s[9]), int(vm.s[10])) == (0xCAFE, 0x77, 163)
+
+
 def test_vm_atomics_and_lane_counts():
     vm = GcnVirtualMachine(104, 256, 64)
     mem = V.Memory(8192, "vmem")
@@ -664,6 +741,11 @@ def test_scalar_alu_wraps_and_sets_scc():
     vm.run("generated_gemm:\n s_add_u32 s3, s1, s2\n s_addc_u32 s4, 0, 0\n s_mul_hi_u32 s5, s1, s1\n"
            " s_endpgm\n")
     assert vm.s[3] == 1 and vm.s[4] == 1 and vm.s[5] == 0xFFFFFFFE
+    # and-not / or-not: s6 = 0x1234 & ~63, SCC set; s7 = 0 | ~0xFFFFFFFF = 0, SCC clear
+    vm.s[6], vm.s[8] = 0x1234, 0
+    vm.run("generated_gemm:\n s_andn2_b32 s6, s6, 63\n s_cselect_b32 s9, 1, 0\n s_orn2_b32 s7, s8, s1\n"
+           " s_cselect_b32 s10, 1, 0\n s_endpgm\n")
+    assert (vm.s[6], vm.s[9], vm.s[7], vm.s[10]) == (0x1200, 1, 0, 0)
 
 
 def test_vector_64bit_subtract_chains():

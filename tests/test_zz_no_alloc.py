@@ -77,6 +77,26 @@ def test_noalloc_without_split_and_repeated(kernels):
             assert np.array_equal(_d(kern, "launch_noalloc", bufs, m, n, k, 1.0, 0.0), first)
 
 
+def test_noalloc_stream_k_matches_launch(kernels):
+    """A stream-K launch (partials of 2 G tiles, G tickets) from the static
+    scratch: the same bits as from the handle's workspace, twice in a row."""
+    name = "mt128x64_a16_wg2x2_dk32_s3_occ2"
+    co, toml = catalog.paths(name)
+    with S.Kernel(co, toml) as ref_kern, S.Kernel(co, toml) as kern:
+        groups = kern.info.stream_k_groups
+        for i, (m, n, k) in enumerate(((128 * 30 - 5, 64 * 22 - 3, 333), (128 * 25, 64 * 23, 200))):
+            kern.set_stream_k(2)
+            ref_kern.set_stream_k(2)
+            sk = kern.stream_k_tiles(m, n, k)
+            _say(f"noalloc stream-K call {i + 1}: {name} {m}x{n}x{k}, {groups} groups, {sk} stream-K tiles")
+            assert sk > 0 and kern.workspace_size(m, n, k) <= S.SGEMM_NOALLOC_PARTIAL_BYTES + 4 * groups
+            A, B, C, bufs = _problem(m, n, k, 51 + i)
+            D = _d(kern, "launch_noalloc", bufs, m, n, k, 1.0, 0.5)
+            assert np.array_equal(D, _d(ref_kern, "launch", bufs, m, n, k, 1.0, 0.5))
+            err = oracle.normwise_error(D, oracle.cpu_gemm_mt(A, B, C, 1.0, 0.5, threads=16))
+            assert err <= oracle.tolerance(k), err
+
+
 def test_noalloc_rejects_more_than_its_scratch(kernels):
     """1024^2 in 64 x 64 tiles with 16 K ranges needs 256 * 16 * 16 KiB = 64 MiB
     of partials, twice the static scratch: an error, and D is untouched."""
