@@ -55,11 +55,13 @@ struct Part {
     uint32_t m, n;
     size_t a_off, b_off, c_off, d_off;
 };
-// The parts of an m x n x k launch of h (sgemm_set_edge_kernel): the whole
-// problem on h, or h on the tile-aligned interior plus the edge kernel on a
-// thin bottom strip (rows past the last whole tile row, every column) and a
-// thin right strip (columns past the last whole tile column, interior rows).
-// A strip is thin when it is at most a quarter of h's tile.  Returns 1..3.
+// The parts of an m x n x k launch of h (sgemm_set_edge_kernels), in launch
+// order on h's stream: the whole problem on h, or h on the tile-aligned
+// interior plus the row-strip kernel on a thin bottom strip (rows past the
+// last whole tile row, every column) and the column-strip kernel on a thin
+// right strip (columns past the last whole tile column, interior rows).  A
+// strip is thin when it is at most a quarter of h's tile, and is split off
+// only when that takes a round of work-groups off h's grid.  Returns 1..3.
 SGEMM_INTERNAL int decompose(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
                              uint32_t ldc, uint32_t ldd, Part out[3]);
 

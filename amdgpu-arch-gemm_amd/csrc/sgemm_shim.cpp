@@ -252,10 +252,13 @@ uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_
     const uint32_t ktiles = (k + (uint32_t)i.depth_k - 1) / (uint32_t)i.depth_k;
     uint64_t s = (uint32_t)i.split_k;
     if (s == 0) {
-        // Work-groups run in rounds of one per compute unit; a range of K/s
-        // per work-group makes the time ~ rounds(T * s) / s.  Pick the s with
-        // the fewest rounds per unit of K work (the smallest s among ties),
-        // keeping at least 4 K tiles per range.
+        // Work-groups run in rounds of one per compute unit; a work-group
+        // with a range of ceil(K tiles / s) K tiles costs that many K tiles
+        // plus kSplitRangeOverhead (pipeline fill, partial store, fix-up), so
+        // the time ~ rounds(T * s) * (ceil(K tiles / s) + overhead).  Pick the
+        // s with the least (the smallest s among ties), keeping at least 4 K
+        // tiles per range.
+        constexpr uint64_t kSplitRangeOverhead = 4;
         const uint64_t tiles = (uint64_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
                                ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
         const uint64_t cus = compute_units > 0 ? (uint64_t)compute_units : 1;
@@ -263,12 +266,12 @@ uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_
         if (tiles > 0 && tiles < cus) {
             uint64_t smax = (uint64_t)i.split_k_max;
             if (smax > ktiles / 4) smax = ktiles / 4;
-            uint64_t best_rounds = 1;  // rounds(T * s) / s compared as fractions
+            uint64_t best = (uint64_t)ktiles + kSplitRangeOverhead;  // s = 1: one round
             for (uint64_t c = 2; c <= smax; ++c) {
-                const uint64_t rounds = (tiles * c + cus - 1) / cus;
-                if (rounds * s < best_rounds * c) {
+                const uint64_t cost = (tiles * c + cus - 1) / cus * ((ktiles + c - 1) / c + kSplitRangeOverhead);
+                if (cost < best) {
                     s = c;
-                    best_rounds = rounds;
+                    best = cost;
                 }
             }
         }
@@ -350,7 +353,9 @@ struct sgemm_handle {
     int compute_units = 0;                    // of the device the module is loaded on
     int device = 0;                           // the device current at sgemm_open
     hipFunction_t function_streamk = nullptr; // null when the code object has none
-    sgemm_handle* edge = nullptr;             // small-tile kernel for thin edge strips (sgemm_set_edge_kernel)
+    sgemm_handle* edge_rows = nullptr;        // kernels for thin edge strips (sgemm_set_edge_kernels): the
+    sgemm_handle* edge_cols = nullptr;        // strip of rows past the last tile row, of columns past the last
+    int resident = 0;                         // work-groups of generated_gemm the device holds at once (0: unknown)
 };
 
 namespace sgemm_internal {
@@ -435,25 +440,41 @@ int decompose(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_
               uint32_t ldd, Part out[3]) {
     const sgemm_kernel_info& i = h->info;
     out[0] = Part{const_cast<sgemm_handle*>(h), m, n, 0, 0, 0, 0};
-    const sgemm_handle* e = h->edge;
-    if (!e || k == 0) return 1;
+    if (k == 0) return 1;
     const uint32_t tm = (uint32_t)i.tile_m, tn = (uint32_t)i.tile_n;
     uint32_t me = m % tm, ne = n % tn;
-    // thin strips only: at most a quarter of a tile, next to a non-empty interior
-    if (!(me && me * 4 <= tm && m > me)) me = 0;
-    if (!(ne && ne * 4 <= tn && n > ne)) ne = 0;
-    if (!me && !ne) return 1;
+    // thin strips only: at most a quarter of a tile, next to a non-empty
+    // interior, and only with a kernel attached for that strip
+    if (!(h->edge_rows && me && me * 4 <= tm && m > me)) me = 0;
+    if (!(h->edge_cols && ne && ne * 4 <= tn && n > ne)) ne = 0;
+    if ((!me && !ne) || h->resident <= 0) return 1;
+    // and only where they save h a round of work-groups: a strip costs a
+    // launch of its own (a memory-bound pass over A or B), the tiles it
+    // replaces cost nothing while they fit in a round the interior needs anyway
+    const uint64_t res = (uint64_t)h->resident;
+    auto rounds = [&](uint32_t rm, uint32_t rn) {
+        return ((uint64_t)((rm + tm - 1) / tm) * ((rn + tn - 1) / tn) + res - 1) / res;
+    };
+    const uint64_t both = rounds(m - me, n - ne);
+    if (rounds(m, n) <= both) return 1;
+    if (me && ne) {  // the fewest strips that reach the same rounds
+        if (rounds(m - me, n) <= both)
+            ne = 0;
+        else if (rounds(m, n - ne) <= both)
+            me = 0;
+    }
     const uint32_t mi = m - me, ni = n - ne;
     int count = 0;
     out[count++] = Part{const_cast<sgemm_handle*>(h), mi, ni, 0, 0, 0, 0};
-    sgemm_handle* eh = const_cast<sgemm_handle*>(e);
     if (me)  // rows [mi, m) of every column
-        out[count++] = Part{eh, me, n, i.trans_a ? (size_t)mi * lda : (size_t)mi, 0, (size_t)mi, (size_t)mi};
+        out[count++] = Part{h->edge_rows, me, n, i.trans_a ? (size_t)mi * lda : (size_t)mi, 0, (size_t)mi,
+                            (size_t)mi};
     if (ne)  // columns [ni, n) of rows [0, mi)
-        out[count++] = Part{eh, mi, ne, 0, i.trans_b ? (size_t)ni : (size_t)ni * ldb, (size_t)ni * ldc,
+        out[count++] = Part{h->edge_cols, mi, ne, 0, i.trans_b ? (size_t)ni : (size_t)ni * ldb, (size_t)ni * ldc,
                             (size_t)ni * ldd};
     return count;
 }
+
 
 hipStream_t stream(const sgemm_handle* h) { return h->stream; }
 
@@ -522,6 +543,13 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
         }
         h->device = dev;
         // optional stream-K kernel: G = resident work-groups per CU x CUs
+        int per_cu_main = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_main, h->function, h->info.workitems, 0) ==
+                hipSuccess && per_cu_main > 0 && h->compute_units > 0) {
+            h->resident = per_cu_main * h->compute_units;
+        } else {
+            (void)hipGetLastError();
+        }
         h->info.stream_k_groups = 0;
         if (hipModuleGetFunction(&h->function_streamk, h->module, "generated_gemm_streamk") == hipSuccess) {
             int per_cu = 0;
@@ -728,6 +756,9 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
     for (int q = 0; q < count; ++q) {
         const sgemm_internal::Part& pt = parts[q];
         if (pt.kh != h && (r = sgemm_check_shape(pt.kh, pt.m, pt.n, k, lda, ldb, ldc, ldd)) != SGEMM_OK) return r;
+    }
+    for (int q = 0; q < count; ++q) {
+        const sgemm_internal::Part& pt = parts[q];
         r = launch_part(pt.kh, h->stream, dA ? dA + pt.a_off : dA, dB ? dB + pt.b_off : dB, dC ? dC + pt.c_off : dC,
                         dD + pt.d_off, pt.m, pt.n, k, lda, ldb, ldc, ldd, alpha, beta);
         if (r != SGEMM_OK) return r;
@@ -735,20 +766,37 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
     return SGEMM_OK;
 }
 
-int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge) {
-    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_edge_kernel: null handle");
-    if (edge) {
-        if (edge == h || edge->edge) return fail(SGEMM_E_INVALID, "an edge kernel must be another handle without an edge");
-        if (edge->info.trans_a != h->info.trans_a || edge->info.trans_b != h->info.trans_b)
-            return fail(SGEMM_E_CONFIG, "the edge kernel's layout (trans_a/trans_b) differs from the main kernel's");
-        if (edge->info.tile_m > h->info.tile_m || edge->info.tile_n > h->info.tile_n)
-            return fail(SGEMM_E_CONFIG, "the edge kernel's tile %dx%d is larger than the main kernel's %dx%d",
-                        edge->info.tile_m, edge->info.tile_n, h->info.tile_m, h->info.tile_n);
-        if (edge->device != h->device) return fail(SGEMM_E_CONFIG, "the edge kernel is loaded on another device");
-    }
-    h->edge = edge;
+namespace {
+
+int check_edge(const sgemm_handle* h, const sgemm_handle* e, bool rows) {
+    if (!e) return SGEMM_OK;
+    if (e == h || e->edge_rows || e->edge_cols)
+        return fail(SGEMM_E_INVALID, "an edge kernel must be another handle without edge kernels");
+    if (e->info.trans_a != h->info.trans_a || e->info.trans_b != h->info.trans_b)
+        return fail(SGEMM_E_CONFIG, "the edge kernel's layout (trans_a/trans_b) differs from the main kernel's");
+    // a strip is at most a quarter of the main tile across, so an edge tile
+    // as wide across it as the main tile's can only be a mistaken handle
+    if (rows ? e->info.tile_m >= h->info.tile_m : e->info.tile_n >= h->info.tile_n)
+        return fail(SGEMM_E_CONFIG, "the %s edge kernel's tile %dx%d is not narrower across the strip than the main "
+                    "kernel's %dx%d", rows ? "row" : "column", e->info.tile_m, e->info.tile_n, h->info.tile_m,
+                    h->info.tile_n);
+    if (e->device != h->device) return fail(SGEMM_E_CONFIG, "the edge kernel is loaded on another device");
     return SGEMM_OK;
 }
+
+}  // namespace
+
+int sgemm_set_edge_kernels(sgemm_handle* h, sgemm_handle* rows, sgemm_handle* cols) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_edge_kernels: null handle");
+    int r = check_edge(h, rows, true);
+    if (r == SGEMM_OK) r = check_edge(h, cols, false);
+    if (r != SGEMM_OK) return r;
+    h->edge_rows = rows;
+    h->edge_cols = cols;
+    return SGEMM_OK;
+}
+
+int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge) { return sgemm_set_edge_kernels(h, edge, edge); }
 
 int sgemm_edge_interior(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* m_int, uint32_t* n_int) {
     if (!h || !m_int || !n_int) return fail(SGEMM_E_INVALID, "sgemm_edge_interior: null argument");

@@ -115,6 +115,13 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
                                      _opt(wgm=4, plr=3, xcd=8)),
     "mt32x32_a32_wg1x1_dk16_tt": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16, ta=True, tb=True), _opt()),
     "mt16x16_a16_wg1x1_dk16_nt": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16, tb=True), _opt(plr=3)),
+    # edge-strip kernels (sgemm_set_edge_kernels): 16 rows or 16 columns wide,
+    # split-K over the strip's few tiles.  A strip one element wide is a
+    # memory-bound pass over B (bottom) or A (right): at 4097^3, 67 MB each,
+    # 16.0 and 15.3 us with these (4.2 / 4.4 TB/s); 16 x 128 and 128 x 16 at
+    # depth 32 took 16.5 and 17.0, 16 x 256 and 256 x 16 21.3 and 20.5
+    "mt16x128_a16_wg1x4_dk64_s2": (_cfg(MFMA_16x16x4, (1, 4), (1, 2), 64, stages=1), _opt(plr=3, xcd=8, sk=0)),
+    "mt64x16_a16_wg4x1_dk64_s3": (_cfg(MFMA_16x16x4, (4, 1), (1, 1), 64, stages=2), _opt(plr=3, xcd=8, sk=0)),
     # the reference's one-wave VM configurations (test_vm.py:447-627)
     "mt32x32_a32_wg1x1_dk16": (_cfg(MFMA_32x32x2, (1, 1), (1, 1), 16), _opt()),
     "mt16x16_a16_wg1x1_dk16": (_cfg(MFMA_16x16x4, (1, 1), (1, 1), 16), _opt()),
@@ -154,21 +161,38 @@ CANDIDATES: Dict[str, Tuple[float, float]] = {
     "mt128x64_a16_wg2x2_dk32_s3_occ2": (0.940, 0.66e-6),
     "mt64x64_a16_wg1x4_dk32_s3": (0.913, 0.0),
 }
-# small-tile instance attached (sgemm_set_edge_kernel) to the large-tile ones
-# for thin edge strips: the 64 x 64 tile with split-K for the strips' few tiles
-EDGE_KERNEL: Dict[str, str] = {
-    "mt256x128_a32_wg2x2_dk16_s3_occ2": "mt64x64_a16_wg1x4_dk32_s3",
-    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": "mt64x64_a16_wg1x4_dk32_s3",
-    "mt256x256_a32_wg2x2_dk24_s3": "mt64x64_a16_wg1x4_dk32_s3",
-    "mt128x64_a16_wg2x2_dk32_s3_occ2": "mt64x64_a16_wg1x4_dk32_s3",
+# instances attached (sgemm_set_edge_kernels) to the large-tile ones for thin
+# edge strips: (rows, cols) = a 16-row tile for the strip of rows past the last
+# tile row and a 16-column tile for the strip of columns past the last tile
+# column, both with split-K for the strips' few tiles
+EDGE_PAIR = ("mt16x128_a16_wg1x4_dk64_s2", "mt64x16_a16_wg4x1_dk64_s3")
+EDGE_KERNEL: Dict[str, Tuple[str, str]] = {
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": EDGE_PAIR,
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": EDGE_PAIR,
+    "mt256x256_a32_wg2x2_dk24_s3": EDGE_PAIR,
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": EDGE_PAIR,
 }
 
 
-def edge_interior(name: str, m: int, n: int, k: int) -> Tuple[int, int]:
+# work-groups of generated_gemm resident per CU for the instances with edge
+# kernels (the compiler's occupancy; the host library queries it)
+RESIDENT_PER_CU: Dict[str, int] = {
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": 2,
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": 2,
+    "mt256x256_a32_wg2x2_dk24_s3": 1,
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": 2,
+}
+
+
+def edge_interior(name: str, m: int, n: int, k: int,
+                  compute_units: int = GFX950_COMPUTE_UNITS) -> Tuple[int, int]:
     """(m, n) of the interior the host library gives the instance itself when
-    its EDGE_KERNEL is attached (the rule of sgemm_set_edge_kernel: a strip of
-    at most a quarter of a tile next to a non-empty interior goes to the edge
-    kernel)."""
+    its EDGE_KERNEL pair is attached (the rule of sgemm_set_edge_kernels): a
+    strip of at most a quarter of a tile next to a non-empty interior goes to
+    an edge kernel when that takes a round of work-groups off the instance's
+    grid, and only the strips needed for that.  At 2500^3 in 128 x 64 tiles
+    the 4-column strip would not (800 and 780 tiles are both two rounds of
+    512): attached, it measured 253.0 us against 246.6 us without."""
     if name not in EDGE_KERNEL or k == 0:
         return m, n
     cfg, _ = SOLUTIONS[name]
@@ -178,6 +202,21 @@ def edge_interior(name: str, m: int, n: int, k: int) -> Tuple[int, int]:
         me = 0
     if not (ne and ne * 4 <= t1 and n > ne):
         ne = 0
+    if not me and not ne:
+        return m, n
+    res = RESIDENT_PER_CU[name] * compute_units
+
+    def rounds(rm, rn):
+        return -(-(-(-rm // t0) * -(-rn // t1)) // res)
+
+    both = rounds(m - me, n - ne)
+    if rounds(m, n) <= both:
+        return m, n
+    if me and ne:
+        if rounds(m - me, n) <= both:
+            ne = 0
+        elif rounds(m, n - ne) <= both:
+            me = 0
     return m - me, n - ne
 
 
@@ -234,13 +273,20 @@ def divides(name: str, m: int, n: int, k: int) -> bool:
     return m % t0 == 0 and n % t1 == 0 and vector_k(name, k)
 
 
+SPLIT_RANGE_OVERHEAD = 4  # K tiles
+
+
 def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> int:
     """K ranges the host library uses for an instance built with split_k = 0
     (the rule of sgemm_set_split_k): none when the tiles fill the compute
-    units, else the s <= min(MAX_SPLIT_K, K tiles / 4) with the fewest rounds
-    of work-groups per unit of K work, ceil(tiles * s / CUs) / s (smallest s
+    units, else the s <= min(MAX_SPLIT_K, K tiles / 4) with the least
+    ceil(tiles * s / CUs) * (ceil(K tiles / s) + SPLIT_RANGE_OVERHEAD): rounds
+    of work-groups times a range's K tiles plus its fixed cost (smallest s
     among ties); an instance built with a fixed split count uses that count.
-    Either way at most one range per K tile."""
+    Either way at most one range per K tile.  The fixed cost, 4 K tiles, is
+    the pipeline fill, partial store and fix-up of a range: it makes a thin
+    strip of 33 tiles (1 x 4097 x 4097 in 16 x 128 tiles) take 7 ranges,
+    17.7 us, where the rounds alone give 15 ranges, 19.2 us."""
     cfg, opt = SOLUTIONS[name]
     t0, t1 = cfg.tile_size
     tiles = -(-m // t0) * -(-n // t1)
@@ -252,11 +298,11 @@ def auto_split(name: str, m: int, n: int, k: int, compute_units: int = GFX950_CO
     elif tiles >= compute_units or tiles == 0:
         s = 1
     else:
-        s, best = 1, 1.0
+        s, best = 1, ktiles + SPLIT_RANGE_OVERHEAD
         for c in range(2, min(MAX_SPLIT_K, ktiles // 4) + 1):
-            rounds = -(-tiles * c // compute_units)
-            if rounds * s < best * c:
-                s, best = c, rounds
+            cost = -(-tiles * c // compute_units) * (-(-ktiles // c) + SPLIT_RANGE_OVERHEAD)
+            if cost < best:
+                s, best = c, cost
     return max(1, min(s, ktiles))
 
 
@@ -289,12 +335,12 @@ def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GF
     mi, ni = edge_interior(name, m, n, k)
     if (mi, ni) == (m, n):
         return predicted_launch_seconds(name, m, n, k, compute_units)
-    edge = EDGE_KERNEL[name]
+    rows, cols = EDGE_KERNEL[name]
     t = predicted_launch_seconds(name, mi, ni, k, compute_units)
     if mi < m:
-        t += predicted_launch_seconds(edge, m - mi, n, k, compute_units) + _LAUNCH_SECONDS
+        t += predicted_launch_seconds(rows, m - mi, n, k, compute_units) + _LAUNCH_SECONDS
     if ni < n:
-        t += predicted_launch_seconds(edge, mi, n - ni, k, compute_units) + _LAUNCH_SECONDS
+        t += predicted_launch_seconds(cols, mi, n - ni, k, compute_units) + _LAUNCH_SECONDS
     return t
 
 

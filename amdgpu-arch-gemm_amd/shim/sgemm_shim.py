@@ -67,6 +67,7 @@ SIGNATURES = {
     "sgemm_launch_splits": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
     "sgemm_set_stream_k": (_int, [_vp, _int]),
     "sgemm_set_edge_kernel": (_int, [_vp, _vp]),
+    "sgemm_set_edge_kernels": (_int, [_vp, _vp, _vp]),
     "sgemm_edge_interior": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
     "sgemm_stream_k_tiles": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
     "sgemm_malloc": (_int, [ctypes.POINTER(_vp), ctypes.c_size_t]),
@@ -265,10 +266,15 @@ class Kernel:
         self._refresh_info()
 
     def set_edge_kernel(self, edge: Optional["Kernel"]):
-        """Attaches a small-tile kernel for thin edge strips (None detaches); it must stay open while attached."""
-        _check("sgemm_set_edge_kernel", load_library().sgemm_set_edge_kernel(self.handle,
-                                                                            edge.handle if edge else None))
-        self.edge = edge
+        """One small-tile kernel for both thin edge strips (None detaches); it must stay open while attached."""
+        self.set_edge_kernels(edge, edge)
+
+    def set_edge_kernels(self, rows: Optional["Kernel"], cols: Optional["Kernel"]):
+        """Kernels for the thin strip of rows past the last tile row and of columns past the last tile
+        column (either may be None); they must stay open while attached."""
+        _check("sgemm_set_edge_kernels", load_library().sgemm_set_edge_kernels(
+            self.handle, rows.handle if rows else None, cols.handle if cols else None))
+        self.edges = (rows, cols)
 
     def edge_interior(self, m, n, k) -> Tuple[int, int]:
         """(m, n) of the part of an m x n x k launch this kernel runs itself."""

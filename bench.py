@@ -161,10 +161,10 @@ def main():
     A = S.fill_matrix(m, k, seed, 0, dist)
     B = S.fill_matrix(k, n, seed, 1, dist)
     kern = S.Kernel(co, toml)
-    edge = None
+    edges = []
     if name in catalog.EDGE_KERNEL and not args.no_edge:
-        edge = S.Kernel(*catalog.paths(catalog.EDGE_KERNEL[name]))
-        kern.set_edge_kernel(edge)
+        edges = [S.Kernel(*catalog.paths(e)) for e in catalog.EDGE_KERNEL[name]]
+        kern.set_edge_kernels(*edges)
     interior = kern.edge_interior(m, n, k)
     if interior != (m, n):
         log(f"edge strips: interior {interior[0]}x{interior[1]} on {name}, strips on {catalog.EDGE_KERNEL[name]}")
@@ -237,7 +237,7 @@ def main():
             "kernel": name,
             "split_k": splits,
             "stream_k_tiles": sk_tiles,
-            "edge_kernel": catalog.EDGE_KERNEL[name] if interior != (m, n) else None,
+            "edge_kernels": list(catalog.EDGE_KERNEL[name]) if interior != (m, n) else None,
             "pct_of_fp32_mfma_peak": round(100.0 * value / FP32_MFMA_PEAK_TFLOPS, 2),
             "device": info["name"],
             "peak_sclk_mhz": info["clock_khz"] / 1000.0,
@@ -262,8 +262,8 @@ def main():
     else:
         line["cpu_baseline"] = None
     kern.close()
-    if edge is not None:
-        edge.close()
+    for e in edges:
+        e.close()
     print(json.dumps(line), flush=True)
 
 

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 6
+#define SGEMM_SHIM_ABI_VERSION 7
 
 /* Most K ranges generated_gemm_splitk splits one output tile into. */
 #define SGEMM_MAX_SPLIT_K 16
@@ -118,9 +118,10 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
  * by later launches; 1 launches generated_gemm.  0 chooses per problem: with
  * T = ceil(m/MT0) * ceil(n/MT1) tiles and C compute units, no split when
  * T >= C; else the s in 1..min(split_k_max, ceil(k/depth_k) / 4) with the
- * fewest rounds of work-groups per unit of K work, ceil(T * s / C) / s (the
- * smallest s among ties), so a problem with few tiles and a deep K still
- * fills the GPU.
+ * least ceil(T * s / C) * (ceil(ceil(k/depth_k) / s) + 4) -- rounds of
+ * work-groups times the K tiles of a range plus 4 for each range's fixed cost
+ * -- (the smallest s among ties), so a problem with few tiles and a deep K
+ * still fills the GPU.
  * With s > 1 ranges, sgemm_launch runs generated_gemm_splitk over a grid of
  * (ceil(m/MT0), ceil(n/MT1), s') blocks, s' = min(s, ceil(k/depth_k)): every
  * block multiplies one range of whole K tiles and the last block of a tile
@@ -155,19 +156,28 @@ int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t 
  * generator_runner.cpp:127-131). */
 int sgemm_set_stream_k(sgemm_handle* h, int mode);
 
-/* Attaches `edge`, another loaded kernel with a smaller tile and the same
- * trans_a / trans_b, that later launches of h use for thin edge strips: when
- * m % MT0 (or n % MT1) is at most a quarter of h's tile, the launch runs h's
- * kernel on the tile-aligned interior and the edge kernel on the strip of
- * rows past the last whole tile row (every column) and the strip of columns
- * past the last whole tile column (interior rows), one after another on h's
- * stream, instead of paying a whole tile of MFMA work for each sliver (4097^3
- * in 256 x 128 tiles: 561 tiles, 49 of them one row or column wide).  The
- * strips use the edge kernel's own split-K / stream-K settings and workspace.
- * NULL detaches.  `edge` must stay open while attached; launches through h
- * must not overlap other work on `edge`'s workspace.  No counterpart in the
+/* Attaches two other loaded kernels with the same trans_a / trans_b that
+ * later launches of h use for thin edge strips: `rows` (tile_m below h's)
+ * for the strip of rows past the last whole tile row, every column, when
+ * m % MT0 is at most a quarter of h's tile height; `cols` (tile_n below h's)
+ * for the strip of columns past the last whole tile column, interior rows,
+ * when n % MT1 is at most a quarter of h's tile width -- and only when that
+ * takes a round of work-groups off h's grid (ceil(tiles / resident
+ * work-groups) falls; of the two strips, the fewest that reach the same
+ * rounds).  h's own kernel then runs only the tile-aligned interior, and the
+ * strips follow it on h's
+ * stream, instead of paying a whole tile of MFMA work for each
+ * sliver (4097^3 in 256 x 128 tiles: 561 tiles, 49 of them one row or one
+ * column wide).  The strips use their kernels' own split-K / stream-K
+ * settings and workspace.  Either may be NULL (that strip then stays with
+ * h); the same handle may serve both.
+ * The attached handles must stay open while attached, and must not run other
+ * work concurrently with launches through h.  No counterpart in the
  * reference, whose tuner skips shapes its tiles do not divide
  * (tuner/sgemm_tuner.py:97-100). */
+int sgemm_set_edge_kernels(sgemm_handle* h, sgemm_handle* rows, sgemm_handle* cols);
+
+/* sgemm_set_edge_kernels(h, edge, edge). */
 int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge);
 
 /* The interior (*m_int x *n_int) an m x n x k launch of h gives h's own
@@ -213,8 +223,8 @@ int sgemm_launch(sgemm_handle* h, const float* dA, const float* dB, const float*
  * partials and tickets from a fixed device array compiled into this library
  * (SGEMM_NOALLOC_PARTIAL_BYTES + 4 * SGEMM_NOALLOC_MAX_TILES bytes per device,
  * held until the process ends) instead of the handle's workspace, and clears
- * the tickets it uses with a kernel on the handle's stream.  A launch needing
- * more partial bytes or tiles than that returns SGEMM_E_SHAPE.  Every call on
+ * the tickets it uses with a kernel on the handle's stream.  A launch
+ * needing more partial bytes or tiles than that returns SGEMM_E_SHAPE.  Every call on
  * a device shares that device's array: calls that overlap on one device (two
  * streams, two handles, two threads) race and must be ordered by the caller. */
 int sgemm_launch_noalloc(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,

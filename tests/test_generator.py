@@ -283,7 +283,7 @@ MEASURED_BEST = [
     ((6144, 6144, 6144), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 151.3; 256x256: 110
     ((8192, 8192, 8192), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.6
     ((1536, 1536, 1536), "mt64x64_a16_wg1x4_dk32_s3"),           # 102.1; 128x64: 78
-    ((2500, 2500, 2500), "mt64x64_a16_wg1x4_dk32_s3"),           # 122.8 (not fitted on)
+    ((2500, 2500, 2500), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 126.7 with stream-K; 64x64: 120.5
     ((7000, 7000, 1000), "mt128x64_a16_wg2x2_dk32_s3_occ2"),     # 139.3 (not fitted on)
     ((4095, 4095, 4095), "mt256x128_a32_wg2x2_dk16_s3_occ2"),    # 152.4 (not fitted on)
     ((1792, 1792, 1792), "mt64x64_a16_wg1x4_dk32_s3"),           # 127.9 with stream-K; 128x64 occ2: 111.8

@@ -566,23 +566,29 @@ def test_stream_k(kernels, name, rounds, mode):
 
 
 # ---------------------------------------------------------------- edge strips
+E16 = catalog.EDGE_PAIR
+E64 = ("mt64x64_a16_wg1x4_dk32_s3", "mt64x64_a16_wg1x4_dk32_s3")
 EDGE_CASES = [
-    # (main, edge, m, n, k): thin strips below and right of the interior
-    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 3 + 5, 128 * 4 + 7, 100),
-    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 2 + 1, 128 * 5, 257),   # bottom only
-    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 256 * 2, 128 * 3 + 1, 64),    # right only
-    ("mt256x256_a32_wg2x2_dk24_s3", "mt64x64_a16_wg1x4_dk32_s3", 1025, 1025, 1025),
-    ("mt256x256_a32_wg2x2_dk16_s3_tn", "mt64x64_a16_wg2x2_dk32_s3_tn", 256 * 2 + 33, 256 + 3, 90),  # A^T
-    ("mt128x64_a16_wg2x2_dk32_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3", 128 * 3 + 2, 64 * 2 + 16, 77),
+    # (main, (rows edge, cols edge), m, n, k): thin strips below and right of
+    # the interior, on grids where they take a round of work-groups off the
+    # main kernel (the library's condition for using them)
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", E16, 4096 + 5, 4096 + 7, 100),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", E16, 4096 + 1, 4096, 257),        # bottom only
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", E16, 4096, 4096 + 1, 64),         # right only
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", E64, 4096 + 17, 4096 + 30, 333),  # one handle for both strips
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", E16, 4097, 4097, 300),            # the q4097 grid, shallow K
+    ("mt256x256_a32_wg2x2_dk24_s3", E16, 4097, 4097, 129),
+    ("mt256x256_a32_wg2x2_dk16_s3_tn", ("mt64x64_a16_wg2x2_dk32_s3_tn",) * 2, 4096 + 33, 4096 + 3, 90),  # A^T
+    ("mt128x64_a16_wg2x2_dk32_s3_occ2", E16, 128 * 16 + 2, 64 * 32 + 16, 77),
 ]
 
 
-@pytest.mark.parametrize("main,edge,m,n,k", EDGE_CASES)
-def test_edge_kernel_strips(kernels, main, edge, m, n, k):
-    """A launch with an attached edge kernel: the main kernel on the
-    tile-aligned interior, the edge kernel on the thin bottom and right strips.
-    D against the oracle with padded leading dimensions (rows past m of D
-    untouched), the library's interior is the catalog's rule, and
+@pytest.mark.parametrize("main,edges,m,n,k", EDGE_CASES)
+def test_edge_kernel_strips(kernels, main, edges, m, n, k):
+    """A launch with edge kernels attached: the main kernel on the
+    tile-aligned interior, the edge kernels on the thin bottom and right
+    strips.  D against the oracle with padded leading dimensions (rows past m
+    of D untouched), the library's interior is the catalog's rule, and
     sgemm_launch_noalloc gives the same bits."""
     cfg, _ = catalog.SOLUTIONS[main]
     ra, ca = (k, m) if cfg.trans_a else (m, k)
@@ -590,12 +596,16 @@ def test_edge_kernel_strips(kernels, main, edge, m, n, k):
     lda, ldb, ldc, ldd = ra + 3, rb + 1, m + 2, m + 5
     Af, Bf, Cf = S.fill_matrix(lda, ca, 41, 0), S.fill_matrix(ldb, cb, 41, 1), S.fill_matrix(ldc, n, 41, 2)
     dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
-    with _kernel(main) as kern, _kernel(edge) as ekern:
+    with _kernel(main) as kern, _kernel(edges[0]) as er, _kernel(edges[1]) as ec:
         assert kern.edge_interior(m, n, k) == (m, n)
-        kern.set_edge_kernel(ekern)
+        if edges[0] == edges[1]:
+            kern.set_edge_kernel(er)      # one handle serves both strips
+        else:
+            kern.set_edge_kernels(er, ec)
         mi, ni = kern.edge_interior(m, n, k)
-        _say(f"edge strips {main} + {edge} {m}x{n}x{k}: interior {mi}x{ni}")
-        assert (mi, ni) == catalog.edge_interior(main, m, n, k) if main in catalog.EDGE_KERNEL else (mi, ni) != (m, n)
+        _say(f"edge strips {main} + {edges} {m}x{n}x{k}: interior {mi}x{ni}")
+        if main in catalog.EDGE_KERNEL:
+            assert (mi, ni) == catalog.edge_interior(main, m, n, k)
         assert (mi, ni) != (m, n)
         outs = []
         for launch in ("launch", "launch_noalloc"):
@@ -607,20 +617,44 @@ def test_edge_kernel_strips(kernels, main, edge, m, n, k):
     Dfull = outs[0]
     opA = np.asfortranarray(Af[:ra, :ca].T if cfg.trans_a else Af[:m, :k])
     opB = np.asfortranarray(Bf[:rb, :cb].T if cfg.trans_b else Bf[:k, :n])
-    _check(Dfull[:m, :], oracle.cpu_gemm_mt(opA, opB, Cf[:m, :n], 1.5, -0.5, threads=16), k, f"{main}+{edge}")
+    _check(Dfull[:m, :], oracle.cpu_gemm_mt(opA, opB, Cf[:m, :n], 1.5, -0.5, threads=16), k, f"{main}+{edges}")
     assert np.all(Dfull[m:, :] == 9.5), "rows past m of D were written"
 
 
 def test_edge_kernel_errors(kernels):
     with _kernel("mt256x128_a32_wg2x2_dk16_s3_occ2") as kern, _kernel("mt64x64_a16_wg2x2_dk32_s3_tn") as tn, \
-            _kernel("mt256x256_a32_wg2x2_dk24_s3") as big:
+            _kernel("mt256x256_a32_wg2x2_dk24_s3") as big, _kernel(catalog.EDGE_PAIR[0]) as rows:
         with pytest.raises(S.SgemmError, match="layout"):
             kern.set_edge_kernel(tn)
-        with pytest.raises(S.SgemmError, match="larger"):
+        with pytest.raises(S.SgemmError, match="narrower"):
             kern.set_edge_kernel(big)
+        with pytest.raises(S.SgemmError, match="narrower"):
+            kern.set_edge_kernels(None, rows)    # 16 x 128 is as wide as the main tile: not a column strip kernel
         with pytest.raises(S.SgemmError):
             kern.set_edge_kernel(kern)
+        kern.set_edge_kernels(rows, None)
+        assert kern.edge_interior(4097, 4096, 64) == (4096, 4096)
+        assert kern.edge_interior(4097, 4097, 64) == (4097, 4097)   # 528 tiles without the row strip: no round saved
+        assert kern.edge_interior(513, 259, 64) == (513, 259)     # one round either way: no strip
         kern.set_edge_kernel(None)
+
+
+def test_edge_kernels_only_where_they_save_a_round(kernels):
+    """The library's strip rule is the catalog's: with the pair attached, a
+    thin strip goes to an edge kernel only when that takes a round of
+    work-groups off the main grid (2500^3 in 128 x 64 tiles: 800 and 780 tiles
+    are both two rounds of 512 resident work-groups, so no strip)."""
+    cus = S.device_info()["compute_units"]
+    for main in catalog.EDGE_KERNEL:
+        with _kernel(main) as kern, _kernel(catalog.EDGE_KERNEL[main][0]) as er, \
+                _kernel(catalog.EDGE_KERNEL[main][1]) as ec:
+            kern.set_edge_kernels(er, ec)
+            rng = np.random.default_rng(11)
+            shapes = [(2500, 2500, 2500), (4097, 4097, 4097), (8193, 8193, 64), (4095, 4095, 64), (1025, 1025, 64)]
+            shapes += [tuple(int(x) for x in rng.integers(1, 9000, size=2)) + (64,) for _ in range(60)]
+            for (m, n, k) in shapes:
+                assert kern.edge_interior(m, n, k) == catalog.edge_interior(main, m, n, k, cus), (main, m, n, k)
+    assert catalog.edge_interior("mt128x64_a16_wg2x2_dk32_s3_occ2", 2500, 2500, 2500, cus) == (2500, 2500)
 
 
 def test_stream_k_errors(kernels):

@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 6
+    assert lib.sgemm_abi_version() == 7
     assert ctypes.sizeof(S.KernelInfo) == 4 * 22  # 22 ints, as in sgemm_kernel_info
 
 
@@ -95,6 +95,7 @@ def test_null_arguments_are_rejected():
     assert lib.sgemm_set_stream_k(None, 1) == -1
     assert lib.sgemm_stream_k_tiles(None, 64, 64, 64, None) == -1
     assert lib.sgemm_set_edge_kernel(None, None) == -1
+    assert lib.sgemm_set_edge_kernels(None, None, None) == -1
     assert lib.sgemm_edge_interior(None, 64, 64, 64, None, None) == -1
 
 
