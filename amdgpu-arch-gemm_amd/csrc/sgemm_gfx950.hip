@@ -37,7 +37,13 @@
 //   A tile: [DK][MT0 + PAD_A]  -- one k per row, m contiguous; written straight
 //           from the column-major global rows (coalesced, conflict-free).
 //   B tile: [MT1][DK + PAD_B]  -- one n per row, k contiguous; written straight
-//           from the column-major global columns.
+//           from the column-major global columns.  In the NN/TN layouts the
+//           16-byte chunks of a row may be XOR-swizzled: chunk c of row n sits
+//           at chunk c ^ ((n >> SG_BSWZ_SHIFT) & SG_BSWZ_MASK) of that row, so
+//           that the ds_write_b128 of two rows per 8 lanes and the
+//           ds_read_b128 of 16 rows per cycle both hit distinct banks without
+//           a pad (gfx950 serves b128 writes 8 lanes x 32 banks per cycle,
+//           b128 reads 16 lanes x 64 banks, measured by profiler/lds_probe).
 //
 // K permutation.  An MFMA atom with atom_k = 2 (32x32x2) or 4 (16x16x4) feeds
 // lane group g = lane / atom_m one k value.  Any bijection between the k values
@@ -106,6 +112,12 @@
 #endif
 #ifndef SG_PAD_A
 #define SG_PAD_A 0
+#endif
+#ifndef SG_BSWZ_SHIFT
+#define SG_BSWZ_SHIFT 0
+#endif
+#ifndef SG_BSWZ_MASK
+#define SG_BSWZ_MASK 0
 #endif
 #ifndef SG_PAD_B
 #define SG_PAD_B 4
@@ -209,6 +221,16 @@ struct Geometry {
 };
 
 typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B> G;
+
+// B-tile chunk swizzle of row n (0: rows stored straight).  The XOR stays
+// inside a row when its chunk count is a multiple of MASK + 1, and a lane's
+// rows differ by multiples of the atom's N, which leave the swizzle alone
+// when atom N is a multiple of (MASK + 1) << SHIFT.
+__device__ __forceinline__ constexpr int bswz(int n) { return (n >> SG_BSWZ_SHIFT) & SG_BSWZ_MASK; }
+static_assert(SG_BSWZ_MASK == 0 || (SG_BSWZ_MASK & (SG_BSWZ_MASK + 1)) == 0, "swizzle mask is 2^b - 1");
+static_assert((SG_DK / 4) % (SG_BSWZ_MASK + 1) == 0, "swizzle leaves the B row");
+static_assert(G::atom::N % ((SG_BSWZ_MASK + 1) << SG_BSWZ_SHIFT) == 0, "swizzle varies across a lane's rows");
+static_assert(SG_BSWZ_MASK == 0 || !SG_TB, "the B swizzle is for the layouts with k contiguous in B");
 
 // Reads WT0 consecutive floats (the A operands of the WT0 interleaved atoms).
 template <int W> __device__ __forceinline__ void lds_read_row(const float* p, float (&out)[W]) {
@@ -451,7 +473,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         if constexpr (!TB) {  // c0: k / 4, c1: n
             const uint32_t cc = col0 + (uint32_t)c1 < n ? (uint32_t)c1 : 0u;
             b_off[i] = ((uint32_t)(c0 * 4) + cc * ldb) * 4u;
-            b_lds[i] = G::A_STAGE + c1 * G::B_LD + c0 * 4;
+            b_lds[i] = G::A_STAGE + c1 * G::B_LD + (c0 ^ sg::bswz(c1)) * 4;
         } else {              // c0: n / 4, c1: k
             const uint32_t cc = col0 + (uint32_t)(c0 * 4) < n ? (uint32_t)(c0 * 4) : 0u;
             b_off[i] = (cc + (uint32_t)c1 * ldb) * 4u;
@@ -636,7 +658,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const int r = lane % AT::M;  // row (A) / column (B) inside the atom
     const int g = lane / AT::M;  // k group
     const int a_rd = g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
-    const int b_rd = G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + g * KPL;
+    const int b_rd = G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + (SG_BSWZ_MASK ? 0 : g * KPL);
+    const int b_fr = sg::bswz(r);  // the swizzle of every B row this lane reads
 
     acc_t acc[WT0][WT1];
 #pragma unroll
@@ -657,7 +680,13 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         for (int j = 0; j < KPL; ++j) lds_read_row<WT0>(s + a_rd + (kb * KB + j) * G::A_LD, f.a[j]);
 #pragma unroll
         for (int jn = 0; jn < WT1; ++jn) {
-            const float* p = s + b_rd + jn * AT::N * G::B_LD + kb * KB;
+            const float* p;
+            if constexpr (SG_BSWZ_MASK == 0) {
+                p = s + b_rd + jn * AT::N * G::B_LD + kb * KB;
+            } else {
+                const int kc = g * KPL + kb * KB;  // first k of the read, inside one chunk
+                p = s + b_rd + jn * AT::N * G::B_LD + ((((kc >> 2) ^ b_fr) << 2) | (kc & 3));
+            }
             float tmp[KPL];
             lds_read_row<KPL>(p, tmp);
 #pragma unroll

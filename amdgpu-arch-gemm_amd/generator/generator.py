@@ -26,6 +26,7 @@ code object exports ``generated_gemm`` with the reference's 15-argument,
 from __future__ import annotations
 
 import argparse
+import functools
 import math
 import os
 import shutil
@@ -48,10 +49,19 @@ MAX_LDS_NUM_BYTES = 163840
 MAX_SPLIT_K = 16
 # Work-items per work-group accepted by the hardware.
 MAX_WORKITEMS = 1024
-# LDS geometry used by the pad solver: gfx950 serves a 16-byte-per-lane LDS
-# access in groups of lanes that together cover all banks once.
-LDS_NUM_BANKS = 64
+# How gfx950 serves one wave-wide LDS instruction, measured with
+# profiler/lds_probe (962 patterns: lane-pair tests, strided lanes and this
+# kernel's own accesses, every one reproduced by lds_access_cycles):
+# (write, bytes per lane) -> (banks of 4 bytes, lanes served per cycle).
+# Reads of 8 and 16 bytes see 64 banks (256 bytes a cycle), every other kind
+# 32 banks (128 bytes a cycle).
+LDS_SERVICE = {
+    (False, 4): (32, 32), (False, 8): (64, 32), (False, 16): (64, 16),
+    (True, 4): (32, 32), (True, 8): (32, 16), (True, 16): (32, 8),
+}
 LDS_BANK_BYTES = 4
+# pads (floats) and B-chunk swizzles the layout search tries
+LDS_PADS = (0, 4, 8, 12, 16)
 # hipcc flags for every kernel: packed FP32 VALU ops stay off.
 HIPCC_KERNEL_FLAGS = (
     "-O3",
@@ -218,25 +228,125 @@ class GemmOptimizations:
                 f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, split_k={self.split_k}, stream_k={self.stream_k})")
 
 
-def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int,
-                      num_banks: int = LDS_NUM_BANKS, bank_bytes: int = LDS_BANK_BYTES) -> int:
-    """Cycles one wave-wide LDS access takes under a simple bank model.
+def lds_lane_cycle(lane: int, access_bytes: int, write: bool = False) -> int:
+    """Cycle of a wave-wide LDS instruction in which gfx950 serves ``lane``:
+    consecutive groups of LDS_SERVICE's lanes per cycle, except ds_read_b128,
+    which serves each half-wave in two cycles and splits its eight quads (4
+    lanes each) by the parity of the quad index: {0, 3, 5, 6} then {1, 2, 4, 7}."""
+    _, per = LDS_SERVICE[(bool(write), access_bytes)]
+    if not write and access_bytes == 16:
+        quad = (lane >> 2) & 7
+        return (lane >> 5) * 2 + (bin(quad).count("1") & 1)
+    return lane // per
 
-    Lanes are served in groups whose combined width equals one pass over all
-    banks (``num_banks * bank_bytes / access_bytes`` lanes, at least one).  A
-    group costs as many cycles as the most-used bank in it; distinct dwords of
-    one bank conflict, the same dword is broadcast.
-    """
-    per_group = max(1, (num_banks * bank_bytes) // access_bytes)
+
+def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int, write: bool = False) -> int:
+    """Cycles one wave-wide LDS access takes: per cycle of lds_lane_cycle, as
+    many as the most-used bank holds distinct dwords (lanes that read or write
+    the same dword share its bank cycle)."""
+    banks, _ = LDS_SERVICE[(bool(write), access_bytes)]
+    groups: Dict[int, List[int]] = {}
+    for lane, addr in enumerate(byte_addrs):
+        groups.setdefault(lds_lane_cycle(lane, access_bytes, write), []).append(addr)
     cycles = 0
-    for g0 in range(0, len(byte_addrs), per_group):
+    for addrs in groups.values():
         words_per_bank: Dict[int, set] = {}
-        for addr in byte_addrs[g0:g0 + per_group]:
-            for w in range(access_bytes // bank_bytes):
-                word = addr // bank_bytes + w
-                words_per_bank.setdefault(word % num_banks, set()).add(word)
+        for addr in addrs:
+            for w in range(access_bytes // LDS_BANK_BYTES):
+                word = addr // LDS_BANK_BYTES + w
+                words_per_bank.setdefault(word % banks, set()).add(word)
         cycles += max(len(v) for v in words_per_bank.values())
     return cycles
+
+
+def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tiling: Sequence[int], depth_k: int,
+                      trans_a: bool, trans_b: bool, operand: str, pad: int, b_swizzle: Tuple[int, int] = (0, 0)):
+    """The wave-wide LDS instructions of one work-group per K tile for one
+    operand ("a" or "b") and layout, as (kind, wave, byte addresses, bytes per
+    lane, write, count) -- the address formulas of csrc/sgemm_gfx950.hip: the
+    tile writes of every wave, and each wave's operand reads (the waves' reads
+    differ by uniform offsets, so wave 0's pattern stands for all, counted
+    once per wave).  ``b_swizzle`` is the B-tile chunk swizzle (shift, mask)."""
+    am, an, _, ak = mfma
+    mt0 = am * wave_group[0] * wave_tiling[0]
+    mt1 = an * wave_group[1] * wave_tiling[1]
+    waves = wave_group[0] * wave_group[1]
+    nt = waves * 64
+    steps = depth_k // ak
+    kpl = 4 if steps >= 4 else (2 if steps >= 2 else 1)
+    kb_len = ak * kpl
+    nkb = depth_k // kb_len
+    shift, mask = b_swizzle
+    out = []
+
+    def writes(chunks, per_row, addr_of):
+        for i in range(-(-chunks // nt)):
+            for w in range(waves):
+                lanes = [ch for ch in (64 * w + l + i * nt for l in range(64)) if ch < chunks]
+                if lanes:
+                    for addrs, width in addr_of([(ch % per_row, ch // per_row) for ch in lanes]):
+                        out.append(("write", w, addrs, width, True, 1))
+
+    if operand == "a":
+        lda = mt0 + pad
+        if not trans_a:  # float4 along m into row k
+            writes(mt0 * depth_k // 4, mt0 // 4, lambda cc: [([c1 * lda * 4 + c0 * 16 for c0, c1 in cc], 16)])
+        else:  # float4 along k scattered down column m: four dword writes
+            writes(mt0 * depth_k // 4, depth_k // 4,
+                   lambda cc: [([((c0 * 4 + e) * lda + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
+        width = 4 * wave_tiling[0]
+        reads = [((l // am) * kpl * lda + (l % am) * wave_tiling[0]) * 4 for l in range(64)]
+        for part in range(max(1, width // 16)):  # 8 floats: two 16-byte reads
+            out.append(("read", 0, [x + 16 * part for x in reads], min(width, 16), False, waves * nkb * kpl))
+        return out
+    ldb = depth_k + pad
+
+    def chunk(n, c):
+        return c ^ ((n >> shift) & mask)
+
+    if not trans_b:  # float4 along k into row n, chunk swizzled
+        writes(mt1 * depth_k // 4, depth_k // 4,
+               lambda cc: [([(c1 * ldb + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
+    else:  # float4 along n scattered across rows: four dword writes
+        writes(mt1 * depth_k // 4, mt1 // 4,
+               lambda cc: [([((c0 * 4 + e) * ldb + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
+    for kb in range(nkb):
+        reads = []
+        for l in range(64):
+            n, kc = l % an, (l // an) * kpl + kb * kb_len
+            reads.append((n * ldb + chunk(n, kc >> 2) * 4 + (kc & 3)) * 4)
+        out.append(("read", 0, reads, 4 * kpl, False, waves * wave_tiling[1]))
+    return out
+
+
+def lds_tile_cycles(accesses) -> int:
+    """LDS cycles of lds_tile_accesses' instructions."""
+    return sum(count * lds_access_cycles(addrs, width, write) for _, _, addrs, width, write, count in accesses)
+
+
+@functools.lru_cache(maxsize=None)
+def _lds_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int], depth_k: int,
+                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int]:
+    """(pad A, pad B, B swizzle shift, B swizzle mask) with the fewest LDS
+    cycles per K tile (lds_tile_cycles); ties go to the smaller pad, then to
+    no swizzle.  Swizzles are tried for B when k is contiguous in it: masks
+    whose XOR stays inside a row's depth_k / 4 chunks and shifts that leave
+    every row a lane reads (atom-N apart) with one swizzle."""
+    geo = (mfma, wave_group, wave_tiling, depth_k, trans_a, trans_b)
+
+    def cost(operand, pad, swz=(0, 0)):
+        return lds_tile_cycles(lds_tile_accesses(*geo, operand, pad, swz))
+
+    pad_a = min(LDS_PADS, key=lambda p: (cost("a", p), p))
+    swizzles = [(0, 0)]
+    if not trans_b:
+        for mask in (1, 3, 7, 15):
+            for shift in range(5):
+                if (depth_k // 4) % (mask + 1) == 0 and mfma[1] % ((mask + 1) << shift) == 0:
+                    swizzles.append((shift, mask))
+    pad_b, swz = min(((p, sw) for p in LDS_PADS for sw in swizzles),
+                     key=lambda x: (cost("b", x[0], x[1]), x[0], x[1][1], x[1][0]))
+    return pad_a, pad_b, swz[0], swz[1]
 
 
 class GemmSolutionConfig:
@@ -354,64 +464,21 @@ class GemmSolutionConfig:
         return self.depth_k // self.mfma[3]
 
     # ------------------------------------------------------------------- LDS
-    def _a_read_addrs(self, pad: int) -> List[int]:
-        am = self.mfma[0]
-        wt0 = self.wave_tiling[0]
-        stride = self.tile_size[0] + pad
-        kpl = self.k_per_lane
-        return [((l // am) * kpl * stride + (l % am) * wt0) * 4 for l in range(64)]
-
-    def _b_read_addrs(self, pad: int) -> List[int]:
-        an = self.mfma[1]
-        stride = self.depth_k + pad
-        kpl = self.k_per_lane
-        return [((l % an) * stride + (l // an) * kpl) * 4 for l in range(64)]
-
-    def _a_write_addrs(self, pad: int) -> Tuple[List[int], int]:
-        """Byte addresses of one wave's A-tile LDS write and its width."""
-        stride = self.tile_size[0] + pad
-        if not self.trans_a:  # float4 along m into one row
-            per_row = self.tile_size[0] // 4
-            return [((t // per_row) * stride + (t % per_row) * 4) * 4 for t in range(64)], 16
-        per_m = self.depth_k // 4  # float4 along k scattered down a column, first dword shown
-        return [((t % per_m) * 4 * stride + t // per_m) * 4 for t in range(64)], 4
-
-    def _b_write_addrs(self, pad: int) -> Tuple[List[int], int]:
-        stride = self.depth_k + pad
-        if not self.trans_b:  # float4 along k into one row
-            per_col = self.depth_k // 4
-            return [((t // per_col) * stride + (t % per_col) * 4) * 4 for t in range(64)], 16
-        per_k = self.tile_size[1] // 4  # float4 along n scattered across rows
-        return [((t % per_k) * 4 * stride + t // per_k) * 4 for t in range(64)], 4
-
-    def _auto_lds_pad_a(self) -> int:
-        best, best_cost = 0, None
-        for pad in (0, 4, 8, 12, 16):
-            waddr, wbytes = self._a_write_addrs(pad)
-            writes = 1 if wbytes == 16 else 4
-            cost = (lds_access_cycles(self._a_read_addrs(pad), 4 * self.wave_tiling[0]) * self.k_per_lane
-                    + lds_access_cycles(waddr, wbytes) * writes)
-            if best_cost is None or cost < best_cost:
-                best, best_cost = pad, cost
-        return best
-
-    def _auto_lds_pad_b(self) -> int:
-        best, best_cost = 0, None
-        for pad in (0, 4, 8, 12, 16):
-            waddr, wbytes = self._b_write_addrs(pad)
-            writes = 1 if wbytes == 16 else 4
-            cost = (lds_access_cycles(self._b_read_addrs(pad), 4 * self.k_per_lane) * 4
-                    + lds_access_cycles(waddr, wbytes) * writes)
-            if best_cost is None or cost < best_cost:
-                best, best_cost = pad, cost
-        return best
+    @property
+    def lds_layout(self) -> Tuple[int, int, int, int]:
+        """(pad A, pad B, B swizzle shift, B swizzle mask): see _lds_layout."""
+        return _lds_layout(tuple(self.mfma), tuple(self.wave_group), tuple(self.wave_tiling), self.depth_k,
+                           self.trans_a, self.trans_b)
 
     @property
     def lds_pad_bytes(self) -> Tuple[int, int]:
-        return (
-            self._auto_lds_pad_a() * datatype_size(self.a_type),
-            self._auto_lds_pad_b() * datatype_size(self.b_type),
-        )
+        pad_a, pad_b, _, _ = self.lds_layout
+        return pad_a * datatype_size(self.a_type), pad_b * datatype_size(self.b_type)
+
+    @property
+    def lds_b_swizzle(self) -> Tuple[int, int]:
+        """(shift, mask) of the B-tile chunk swizzle (mask 0: none)."""
+        return self.lds_layout[2], self.lds_layout[3]
 
     @property
     def lds_offset_bytes(self) -> Tuple[int, int]:
@@ -573,6 +640,8 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_TB": int(config.trans_b),
         "SG_PAD_A": pad_a,
         "SG_PAD_B": pad_b,
+        "SG_BSWZ_SHIFT": config.lds_b_swizzle[0],
+        "SG_BSWZ_MASK": config.lds_b_swizzle[1],
         "SG_KERNEL_NAME": name,
     }
 

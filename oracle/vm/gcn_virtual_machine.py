@@ -865,6 +865,27 @@ _vop("v_bfe_u32", lambda a, o, w: ((a.astype(np.uint64) >> (o & 31).astype(np.ui
 _vop("v_bfi_b32", lambda m, a, b: (m & a) | (~m & b), 3)
 
 
+def _v_bitop3_b32(vm, ins, prog):
+    """gfx950 V_BITOP3_B32 D, S0, S1, S2 bitop3:T: bit i of D is bit
+    (S0_i << 2 | S1_i << 1 | S2_i) of the 8-bit truth table T -- the
+    convention under which S0, S1 and S2 alone are the tables 0xF0, 0xCC and
+    0xAA (LLVM's AMDGPU backend builds T that way)."""
+    unknown = set(ins.mods) - {"bitop3"}
+    if unknown:
+        raise NotImplementedError(f"modifiers {sorted(unknown)} of {ins}")
+    table = ins.mods.get("bitop3", 0)
+    a, b, c = (vm.rv32(o) for o in ins.ops[1:4])
+    out = np.zeros_like(a)
+    for idx in range(8):
+        if (table >> idx) & 1:
+            out |= (a if idx & 4 else ~a) & (b if idx & 2 else ~b) & (c if idx & 1 else ~c)
+    vm.wv32(ins.ops[0], out)
+
+
+for _suffix in ("", "_e64"):
+    _DISPATCH["v_bitop3_b32" + _suffix] = _v_bitop3_b32
+
+
 def _vop_carry(name, fn):
     """VOP2/VOP3b ops with a carry: vdst, [sdst,] src0, src1[, carry-in]."""
     def _impl(vm, ins, prog):

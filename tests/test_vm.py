@@ -700,6 +700,27 @@ def test_readlane_and_writelane_ignore_exec():
     assert (int(vm.s[8]), int(vm.s[9]), int(vm.s[10])) == (0xCAFE, 0x77, 163)
 
 
+def test_bitop3_truth_tables():
+    """v_bitop3_b32 (gfx950): bit i of the result is entry (S0_i, S1_i, S2_i)
+    of the truth table, S0 the high index bit: 0xF0/0xCC/0xAA select one
+    source, 0x96 is a three-way XOR, 0xE8 the majority, and the two tables the
+    compiler emits for the B-tile swizzle, 0x36 = (S0 | S2) ^ S1 and
+    0x6C = S1 ^ (S0 & S2)."""
+    rng = np.random.default_rng(5)
+    x, y, z = (rng.integers(0, 2 ** 32, 64, dtype=np.uint64).astype(np.uint32) for _ in range(3))
+    want = {0xF0: x, 0xCC: y, 0xAA: z, 0x96: x ^ y ^ z, 0xE8: (x & y) | (x & z) | (y & z),
+            0x36: (x | z) ^ y, 0x6C: y ^ (x & z), 0x00: np.zeros(64, np.uint32), 0xFF: np.full(64, 0xFFFFFFFF, np.uint32)}
+    for table, expect in want.items():
+        vm = GcnVirtualMachine(104, 256, 64)
+        vm.v[1], vm.v[2], vm.v[3] = x, y, z
+        vm.run(f"generated_gemm:\n v_bitop3_b32 v4, v1, v2, v3 bitop3:0x{table:x}\n s_endpgm\n")
+        assert np.array_equal(vm.v[4], expect), hex(table)
+    vm = GcnVirtualMachine(104, 256, 64)
+    vm.v[1], vm.v[2] = x, y
+    vm.run("generated_gemm:\n v_bitop3_b32 v4, v1, v2, 2 bitop3:0x36\n s_endpgm\n")   # inline constant
+    assert np.array_equal(vm.v[4], (x | np.uint32(2)) ^ y)
+
+
 def test_vm_atomics_and_lane_counts():
     vm = GcnVirtualMachine(104, 256, 64)
     mem = V.Memory(8192, "vmem")
