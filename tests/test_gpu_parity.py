@@ -741,6 +741,51 @@ def test_random_shapes_layouts_and_splits(kernels, name, m, n, k, pads, alpha, b
     assert np.all(Dfull[m:, :] == 9.5), "rows past m of D were written"
 
 
+def _selected_cases(count, seed):
+    """(m, n, k, stream-K mode or None, alpha, beta) on grids of hundreds to
+    thousands of tiles, where catalog.select's instance may stream its last
+    round or hand thin edges to the strip kernels."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        m, n = (int(x) for x in rng.integers(600, 4600, size=2))
+        k = int(rng.integers(1, 320))
+        mode = [None, 2][int(rng.integers(2))]
+        cases.append((m, n, k, mode, float(rng.choice([1.0, -0.5])), float(rng.choice([0.0, 0.75]))))
+    cases += [(4097, 4097, 64, None, 1.0, 0.0), (1800, 1800, 200, 2, 1.0, 0.5), (2500, 2500, 96, None, 2.0, 0.0)]
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,mode,alpha,beta", _selected_cases(int(os.environ.get("SGEMM_SELECTED_CASES", "16")),
+                                                                  int(os.environ.get("SGEMM_RANDOM_SEED", "2024"))))
+def test_random_selected_launches(kernels, m, n, k, mode, alpha, beta):
+    """What a caller of catalog.select gets on larger random grids: the
+    selected instance with its catalog edge kernels attached and its stream-K
+    setting (the .toml's, or mode 2: stream whenever tiles exceed the resident
+    work-groups), whole D against the oracle."""
+    name = catalog.select(m, n, k)
+    Af, Bf, Cf = S.fill_matrix(m, k, 17, 0), S.fill_matrix(k, n, 17, 1), S.fill_matrix(m, n, 17, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer(m * n * 4)
+    edges = [_kernel(e) for e in catalog.EDGE_KERNEL.get(name, ())]
+    try:
+        with _kernel(name) as kern:
+            if edges:
+                kern.set_edge_kernels(*edges)
+            if mode is not None and kern.info.stream_k_groups:
+                kern.set_stream_k(mode)
+            sk = kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0
+            _say(f"selected {name} {m}x{n}x{k} stream-K tiles {sk} interior {kern.edge_interior(m, n, k)} "
+                 f"alpha {alpha} beta {beta}")
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
+            kern.synchronize()
+    finally:
+        for e in edges:
+            e.close()
+    D = dD.download().reshape(n, m).T
+    _check(D, oracle.cpu_gemm_mt(Af, Bf, Cf, alpha, beta, threads=16), k, name)
+
+
 # ----------------------------------------------------------------- runner
 def _run(cmd, timeout=300):
     _say("+ " + " ".join(cmd))
