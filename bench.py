@@ -16,7 +16,8 @@ oracle/_ref) -- or this project's C restatement of it when that was not built --
 timed single-threaded on a column slice D[:, :s] of the same workload (the
 slice is itself a cpuGemm call with n = s, so per-output work and memory
 pattern are unchanged); s is calibrated to about 15 s of CPU time.  The slice
-is also compared with the GPU result (normwise error, 1e-5 * sqrt(K) bar).
+is also compared with the GPU result (normwise error, 1e-5 * sqrt(K) bar), and
+both float32 results with the float64 product of the same inputs.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -115,6 +116,8 @@ def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
     t, D = timed(cols)
     tflops = 2.0 * m * cols * k / t / 1e12
     err = oracle.normwise_error(D_gpu[:, :cols], D)
+    # both float32 results against the float64 product of the same inputs
+    D64 = A.astype(np.float64) @ B[:, :cols].astype(np.float64)
     return {
         "value": tflops,
         "unit": "TFLOP/s",
@@ -125,6 +128,7 @@ def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
         "sample": f"D[:, :{cols}] of the {m}x{n}x{k} workload (n={cols} columns), single thread, {t:.1f} s",
         "seconds": t,
     }, {"normwise_error": err, "tolerance": oracle.tolerance(k), "columns_checked": cols,
+        "gpu_vs_f64": oracle.normwise_error(D_gpu[:, :cols], D64), "cpu_vs_f64": oracle.normwise_error(D, D64),
         "pass": bool(err <= oracle.tolerance(k))}
 
 
