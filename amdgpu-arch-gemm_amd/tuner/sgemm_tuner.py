@@ -245,12 +245,18 @@ def spills(out: str, key: str) -> bool:
 
 # ----------------------------------------------------------- benchmarking
 class InProcessBench:
-    """Times candidates through the ctypes shim with inputs uploaded once."""
+    """Times candidates through the ctypes shim with inputs uploaded once.
 
-    def __init__(self, m, n, k, warmup, runs):
+    Each candidate first runs for ``warm_ms`` milliseconds of launches: the
+    engine clock falls within ~20 ms of idle (loading a candidate is enough)
+    and takes ~35 ms of load to come back, so without it every point is timed
+    on a ramping clock (1024^3 then measures ~12% low)."""
+
+    def __init__(self, m, n, k, warmup, runs, warm_ms=50.0):
         from shim import sgemm_shim as S
         self.S = S
         self.m, self.n, self.k, self.warmup, self.runs = m, n, k, warmup, runs
+        self.warm_ms = warm_ms
         A = S.fill_matrix(m, k, 1, 0)
         B = S.fill_matrix(k, n, 1, 1)
         self.dA, self.dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
@@ -258,8 +264,11 @@ class InProcessBench:
 
     def __call__(self, co, toml, timeout) -> Tuple[int, float]:
         with self.S.Kernel(co, toml) as kern:
-            ms = kern.time(self.dA, self.dB, None, self.dD, self.m, self.n, self.k, 1.0, 0.0,
-                           warmup=self.warmup, runs=self.runs) / self.runs
+            args = (self.dA, self.dB, None, self.dD, self.m, self.n, self.k, 1.0, 0.0)
+            t0 = time.perf_counter()
+            while (time.perf_counter() - t0) * 1e3 < self.warm_ms:
+                kern.time(*args, warmup=0, runs=5)
+            ms = kern.time(*args, warmup=self.warmup, runs=self.runs) / self.runs
         return 0, 2.0 * self.m * self.n * self.k / ms * 1e-6
 
 
@@ -425,6 +434,8 @@ def main(argv=None):
     ap.add_argument("--timeout", type=float, default=120.0)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--runs", type=int, default=50)
+    ap.add_argument("--warm-ms", type=float, default=50.0,
+                    help="--in-process: milliseconds of launches before timing each candidate (clock ramp)")
     ap.add_argument("--jobs", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--points-dir", default=None, help="compiled candidates (default <out>/points)")
     ap.add_argument("--all-shapes", action="store_true",
@@ -471,7 +482,7 @@ def main(argv=None):
         return 0
 
     if args.in_process:
-        bench = InProcessBench(m, n, k, args.warmup, args.runs)
+        bench = InProcessBench(m, n, k, args.warmup, args.runs, args.warm_ms)
     else:
         bench = RunnerBench(args.bench, m, n, k, args.warmup, args.runs)
 
