@@ -646,10 +646,24 @@ int sgemm_set_split_k(sgemm_handle* h, int splits) {
     return SGEMM_OK;
 }
 
+namespace {
+
+// m x n of h's own part of an m x n x k launch: the interior when edge
+// kernels take strips, else the whole problem.
+void own_part(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* pm, uint32_t* pn) {
+    sgemm_internal::Part parts[3];
+    sgemm_internal::decompose(h, m, n, k, m, k, m, m, parts);
+    *pm = parts[0].m;
+    *pn = parts[0].n;
+}
+
+}  // namespace
+
 int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes) {
     if (!h || !bytes) return fail(SGEMM_E_INVALID, "sgemm_workspace_size: null argument");
     *bytes = 0;
     if (m && n) {
+        own_part(h, m, n, k, &m, &n);
         const sgemm_internal::Plan p = sgemm_internal::plan(h, m, n, k);
         *bytes = p.partial_bytes ? p.partial_bytes + p.ticket_count * 4 : 0;
     }
@@ -667,12 +681,17 @@ int sgemm_set_stream_k(sgemm_handle* h, int mode) {
 
 int sgemm_stream_k_tiles(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* sk_tiles) {
     if (!h || !sk_tiles) return fail(SGEMM_E_INVALID, "sgemm_stream_k_tiles: null argument");
-    *sk_tiles = (m && n) ? (int)sgemm_internal::plan(h, m, n, k).sk_tiles : 0;
+    *sk_tiles = 0;
+    if (m && n) {
+        own_part(h, m, n, k, &m, &n);
+        *sk_tiles = (int)sgemm_internal::plan(h, m, n, k).sk_tiles;
+    }
     return SGEMM_OK;
 }
 
 int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits) {
     if (!h || !splits) return fail(SGEMM_E_INVALID, "sgemm_launch_splits: null argument");
+    if (m && n) own_part(h, m, n, k, &m, &n);
     *splits = (int)effective_splits(h->info, h->compute_units, m, n, k);
     return SGEMM_OK;
 }

@@ -133,12 +133,14 @@ int sgemm_check_shape(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k,
 int sgemm_set_split_k(sgemm_handle* h, int splits);
 
 /* Device bytes the handle's workspace needs for an m x n x k launch with its
- * current split and stream-K settings (0 when the launch needs none).  No
+ * current split and stream-K settings (0 when the launch needs none; h's own
+ * part: the interior when edge kernels take strips).  No
  * counterpart in the reference (its kernel needs no workspace). */
 int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, size_t* bytes);
 
-/* K ranges an m x n x k launch with the handle's current setting uses
- * (1: generated_gemm, no split).  No counterpart in the reference. */
+/* K ranges an m x n x k launch with the handle's current setting uses on
+ * h's own part (the interior when edge kernels take strips; 1:
+ * generated_gemm, no split).  No counterpart in the reference. */
 int sgemm_launch_splits(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* splits);
 
 /* Sets how unsplit launches treat a tile grid that leaves a partial last
@@ -186,7 +188,8 @@ int sgemm_set_edge_kernel(sgemm_handle* h, sgemm_handle* edge);
 int sgemm_edge_interior(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t* m_int, uint32_t* n_int);
 
 /* Tiles an m x n x k launch with the handle's current settings gives the
- * stream-K phase (0: the launch does not use generated_gemm_streamk).  No
+ * stream-K phase of h's own kernel (on the interior when edge kernels take
+ * strips; 0: the launch does not use generated_gemm_streamk).  No
  * counterpart in the reference. */
 int sgemm_stream_k_tiles(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, int* sk_tiles);
 

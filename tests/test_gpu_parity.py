@@ -606,6 +606,9 @@ def test_edge_kernel_strips(kernels, main, edges, m, n, k):
         _say(f"edge strips {main} + {edges} {m}x{n}x{k}: interior {mi}x{ni}")
         if main in catalog.EDGE_KERNEL:
             assert (mi, ni) == catalog.edge_interior(main, m, n, k)
+            # the query functions describe the main kernel's own part, the interior
+            cus = S.device_info()["compute_units"]
+            assert kern.launch_splits(m, n, k) == catalog.auto_split(main, mi, ni, k, cus)
         assert (mi, ni) != (m, n)
         outs = []
         for launch in ("launch", "launch_noalloc"):
