@@ -191,11 +191,12 @@ def summarise(res: Dict[str, Tuple[float, float]], pats: List[Pattern], cmd: str
             for _, _, addrs, width, write, count in kernel_accesses(name, operand, pad, swz):
                 key = _pattern_key(addrs, width, write)
                 groups = len({lds_lane_cycle(l, width, write) for l in range(64)})
-                meas += count * res[key][0]
+                meas = meas + count * res[key][0] if key in res and meas is not None else None
                 model += count * (lds_access_cycles(addrs, width, write) - groups)
                 base += count * groups
             desc = f"pad {pad}" + (f", swizzle {swz}" if swz[1] else "")
-            lines.append(f"| `{name}` | {operand.upper()} | {label}: {desc} | {meas:.0f} | {model:.0f} | {base:.0f} |")
+            shown = "n/a (beyond the probe's LDS)" if meas is None else f"{meas:.0f}"
+            lines.append(f"| `{name}` | {operand.upper()} | {label}: {desc} | {shown} | {model:.0f} | {base:.0f} |")
     return "\n".join(lines) + "\n"
 
 
