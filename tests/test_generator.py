@@ -158,6 +158,20 @@ def test_lds_model_closed_forms():
     assert g.lds_access_cycles([16 * i for i in range(64)], 16, True) == 8  # 128 B a cycle
 
 
+def test_committed_lds_measurements_match_the_model():
+    """Every kernel-access row of the committed probe summary: the conflict
+    cycles measured on the MI355X equal lds_access_cycles' count, and the
+    generator's chosen layout measured conflict-free for B."""
+    path = os.path.join(os.path.dirname(__file__), "..", "profiles", "lds_banks.md")
+    rows = [l.split("|") for l in open(path) if l.startswith("| `mt")]
+    assert len(rows) >= 40
+    for r in rows:
+        name, operand, layout, measured, model = (x.strip() for x in r[1:6])
+        assert measured == model, (name, operand, layout)
+        if layout.startswith("chosen") and operand == "B":
+            assert measured == "0", (name, layout)
+
+
 @pytest.mark.parametrize("name", ["mt256x128_a32_wg2x2_dk16_s3_occ2", "mt256x256_a32_wg2x2_dk24_s3",
                                   "mt128x64_a16_wg2x2_dk32_s3_occ2", "mt64x64_a16_wg1x4_dk32_s3",
                                   "mt64x16_a16_wg4x1_dk64_s3", "mt16x128_a16_wg1x4_dk64_s2"])
