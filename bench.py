@@ -17,7 +17,9 @@ timed single-threaded on a column slice D[:, :s] of the same workload (the
 slice is itself a cpuGemm call with n = s, so per-output work and memory
 pattern are unchanged); s is calibrated to about 15 s of CPU time.  The slice
 is also compared with the GPU result (normwise error, 1e-5 * sqrt(K) bar), and
-both float32 results with the float64 product of the same inputs.
+both float32 results with the float64 product of the same inputs.  A second,
+separately labelled CPU figure (cpu_baseline.parallel) runs the same loop over
+columns on up to 16 host threads (about 5 s).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -118,6 +120,21 @@ def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
     err = oracle.normwise_error(D_gpu[:, :cols], D)
     # both float32 results against the float64 product of the same inputs
     D64 = A.astype(np.float64) @ B[:, :cols].astype(np.float64)
+    # labelled separately: the same loop over columns on the host's cores (the
+    # box's share: at most 16), each output keeping its summation order, so
+    # the result is bitwise the single-thread one
+    threads = max(1, min(16, os.cpu_count() or 1))
+    cols_mt = int(min(n, max(threads, round(cols * threads * 5.0 / max(t, 1e-9)))))
+    Bm = np.asfortranarray(B[:, :cols_mt])
+    t0 = time.perf_counter()
+    D_mt = oracle.cpu_gemm_mt(A, Bm, None, 1.0, 0.0, threads=threads)
+    t_mt = time.perf_counter() - t0
+    overlap = min(cols, cols_mt)
+    parallel = {
+        "value": 2.0 * m * cols_mt * k / t_mt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"D[:, :{cols_mt}] of the same workload, columns over {threads} threads, {t_mt:.1f} s",
+        "bitwise_equal_to_single_thread": bool(np.array_equal(D_mt[:, :overlap], D[:, :overlap])),
+    }
     return {
         "value": tflops,
         "unit": "TFLOP/s",
@@ -127,6 +144,7 @@ def cpu_baseline(A, B, D_gpu, m, n, k, target_s: float):
         "kind": kind,
         "sample": f"D[:, :{cols}] of the {m}x{n}x{k} workload (n={cols} columns), single thread, {t:.1f} s",
         "seconds": t,
+        "parallel": parallel,
     }, {"normwise_error": err, "tolerance": oracle.tolerance(k), "columns_checked": cols,
         "gpu_vs_f64": oracle.normwise_error(D_gpu[:, :cols], D64), "cpu_vs_f64": oracle.normwise_error(D, D64),
         "pass": bool(err <= oracle.tolerance(k))}
