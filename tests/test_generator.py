@@ -371,6 +371,23 @@ def test_select_picks_the_measured_best(shape, name):
     assert catalog.select(*shape) == name
 
 
+def test_edge_interior_rule():
+    """Thin strips go to the edge kernels only when that takes a round of
+    work-groups off the main grid (and only the strips needed for it)."""
+    big, occ2, small = "mt256x256_a32_wg2x2_dk24_s3", "mt256x128_a32_wg2x2_dk16_s3_occ2", "mt128x64_a16_wg2x2_dk32_s3_occ2"
+    assert catalog.edge_interior(big, 4097, 4097, 4097) == (4096, 4096)      # 289 tiles -> 256: 2 rounds -> 1
+    assert catalog.edge_interior(big, 1025, 1025, 1025) == (1025, 1025)      # 25 tiles: one round either way
+    assert catalog.edge_interior(occ2, 4097, 4096, 64) == (4096, 4096)       # 544 -> 512 tiles of 512 slots
+    assert catalog.edge_interior(occ2, 4096 + 100, 4096, 64) == (4196, 4096)  # 100 rows: not a thin strip
+    assert catalog.edge_interior(small, 2500, 2500, 2500) == (2500, 2500)    # 800 and 780 tiles: two rounds each
+    assert catalog.edge_interior(small, 2050, 2064, 77) == (2048, 2048)      # 561 -> 512
+    assert catalog.edge_interior(big, 4097, 4097, 0) == (4097, 4097)         # k = 0: nothing to split off
+    # the strips' time joins the interior's in the model: 4097^3 on 256 x 256 is the interior plus two strips
+    t = catalog.predicted_seconds(big, 4097, 4097, 4097)
+    assert catalog.predicted_launch_seconds(big, 4096, 4096, 4097) < t < 1.1 * catalog.predicted_launch_seconds(
+        big, 4096, 4096, 4097)
+
+
 def test_time_model_counts_rounds_of_work_groups():
     """Wave quantisation: one more tile than the CUs hold costs a whole extra
     round, and splitting K fills a GPU that few tiles leave idle."""
