@@ -356,6 +356,7 @@ struct sgemm_handle {
     sgemm_handle* edge_rows = nullptr;        // kernels for thin edge strips (sgemm_set_edge_kernels): the
     sgemm_handle* edge_cols = nullptr;        // strip of rows past the last tile row, of columns past the last
     int resident = 0;                         // work-groups of generated_gemm the device holds at once (0: unknown)
+    hipStream_t own_stream = nullptr;         // created at sgemm_open; `stream` is it unless sgemm_set_stream
 };
 
 namespace sgemm_internal {
@@ -569,7 +570,8 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
             return fail(SGEMM_E_CONFIG, "split_k = %d but %s has no generated_gemm_splitk", info.split_k, co_path);
         }
     }
-    if (err == hipSuccess) err = hipStreamCreate(&h->stream);
+    if (err == hipSuccess) err = hipStreamCreate(&h->own_stream);
+    h->stream = h->own_stream;
     if (err == hipSuccess) err = hipEventCreate(&h->ev_start);
     if (err == hipSuccess) err = hipEventCreate(&h->ev_stop);
     if (err != hipSuccess) {
@@ -583,9 +585,10 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
 void sgemm_close(sgemm_handle* h) {
     if (!h) return;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->own_stream && h->own_stream != h->stream) (void)hipStreamSynchronize(h->own_stream);
     if (h->ev_start) (void)hipEventDestroy(h->ev_start);
     if (h->ev_stop) (void)hipEventDestroy(h->ev_stop);
-    if (h->stream) (void)hipStreamDestroy(h->stream);
+    if (h->own_stream) (void)hipStreamDestroy(h->own_stream);
     if (h->ws) (void)hipFree(h->ws);
     if (h->tickets) (void)hipFree(h->tickets);
     if (h->module) (void)hipModuleUnload(h->module);
@@ -876,6 +879,22 @@ int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const flo
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     return result;
+}
+
+int sgemm_set_stream(sgemm_handle* h, void* stream) {
+    if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_stream: null handle");
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : h->own_stream;
+    if (next != h->stream) {
+        // work already enqueued through h finishes before h moves on; not
+        // under capture (a capturing stream cannot be synchronized)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(h->stream, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(SGEMM_E_INVALID, "sgemm_set_stream: the handle's current stream is capturing");
+        HIP_TRY(hipStreamSynchronize(h->stream));
+        h->stream = next;
+    }
+    return SGEMM_OK;
 }
 
 int sgemm_synchronize(sgemm_handle* h) {

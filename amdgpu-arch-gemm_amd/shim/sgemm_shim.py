@@ -70,6 +70,7 @@ SIGNATURES = {
     "sgemm_set_edge_kernels": (_int, [_vp, _vp, _vp]),
     "sgemm_edge_interior": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32)]),
     "sgemm_stream_k_tiles": (_int, [_vp, _u32, _u32, _u32, ctypes.POINTER(_int)]),
+    "sgemm_set_stream": (_int, [_vp, _vp]),
     "sgemm_malloc": (_int, [ctypes.POINTER(_vp), ctypes.c_size_t]),
     "sgemm_free": (_int, [_vp]),
     "sgemm_memcpy_h2d": (_int, [_vp, _vp, ctypes.c_size_t]),
@@ -320,6 +321,10 @@ class Kernel:
             *self._args(a, b, c, d, m, n, k, lda, ldb, ldc, ldd, alpha, beta), runs,
             out.ctypes.data_as(ctypes.POINTER(_f32))))
         return out
+
+    def set_stream(self, stream: Optional[int]):
+        """Launch on a caller-owned hipStream_t (an integer handle; None: the handle's own stream)."""
+        _check("sgemm_set_stream", load_library().sgemm_set_stream(self.handle, stream or None))
 
     def synchronize(self):
         _check("sgemm_synchronize", load_library().sgemm_synchronize(self.handle))

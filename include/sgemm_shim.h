@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 7
+#define SGEMM_SHIM_ABI_VERSION 8
 
 /* Most K ranges generated_gemm_splitk splits one output tile into. */
 #define SGEMM_MAX_SPLIT_K 16
@@ -249,6 +249,17 @@ int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const flo
 
 /* Waits for all work of the handle's stream. */
 int sgemm_synchronize(sgemm_handle* h);
+
+/* Makes later launches, timings and synchronisations of h use `stream` (a
+ * hipStream_t of the handle's device, owned by the caller, who keeps it alive
+ * while h uses it) instead of the stream h created at sgemm_open; NULL goes
+ * back to that one.  Work already enqueued through h is waited for first, so
+ * the handle's launches stay ordered; the current stream must not be
+ * capturing then.  For callers that order the GEMM on their own stream (a
+ * framework's current stream, or one under HIP graph capture, where
+ * sgemm_launch_noalloc records no allocation).  No counterpart in the
+ * reference, which launches on the null stream (generator_runner.cpp:189). */
+int sgemm_set_stream(sgemm_handle* h, void* stream);
 
 /* Whole runner flow on host buffers with tight leading dimensions (lda = m
  * or k, ldb = k or n as the kernel's transposition says, ldc = ldd = m):

@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 7
+    assert lib.sgemm_abi_version() == 8
     assert ctypes.sizeof(S.KernelInfo) == 4 * 22  # 22 ints, as in sgemm_kernel_info
 
 
@@ -97,6 +97,7 @@ def test_null_arguments_are_rejected():
     assert lib.sgemm_set_edge_kernel(None, None) == -1
     assert lib.sgemm_set_edge_kernels(None, None, None) == -1
     assert lib.sgemm_edge_interior(None, 64, 64, 64, None, None) == -1
+    assert lib.sgemm_set_stream(None, None) == -1
 
 
 def test_runner_usage_error_exit_code():

@@ -4,8 +4,12 @@ It must give what sgemm_launch gives -- the same kernels with the same split
 count, so D is bit-identical -- on two calls in a row, the second with a
 smaller problem (the static scratch keeps the first call's partials and
 tickets), and must reject a launch whose partials exceed the scratch before
-launching anything.  Every call goes through the C-ABI (ctypes).
+launching anything.  Every call goes through the C-ABI (ctypes).  Captured
+into a HIP graph on a caller's stream (sgemm_set_stream) -- split-K,
+stream-K and edge-strip launches -- it must replay what an eager call gives.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -114,3 +118,90 @@ def test_noalloc_rejects_more_than_its_scratch(kernels):
             kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.0, beta=0.0)
         kern.synchronize()
         assert np.all(dD.download() == 3.0)
+
+
+# ------------------------------------------------------------ graph capture
+_vp = ctypes.c_void_p
+CAPTURE_MODE_GLOBAL = 0   # hipStreamCaptureModeGlobal: any unsafe call (an allocation) fails the capture
+
+
+def _ok(rc, what):
+    assert rc == 0, f"{what} failed: {rc}"
+
+
+def _col(x):
+    """The column-major bytes of a matrix (upload copies an array's memory order)."""
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float32).ravel(order="F"))
+
+
+GRAPH_CASES = [
+    # (main, edges or None, stream-K mode or None, m, n, k): split-K, stream-K and edge-strip launches
+    ("mt64x64_a16_wg1x4_dk32_s3", None, None, 256, 256, 8192),
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 2, 1792, 1792, 256),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", catalog.EDGE_PAIR, None, 4097, 4096, 64),
+]
+
+
+@pytest.mark.parametrize("main,edges,mode,m,n,k", GRAPH_CASES)
+def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, n, k):
+    _hip = ctypes.CDLL("libamdhip64.so")   # the HIP runtime the library itself links
+    stream = _vp()
+    _ok(_hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    graph, exe = _vp(), _vp()
+    opened = []
+    try:
+        kern = S.Kernel(*catalog.paths(main))
+        opened.append(kern)
+        if edges:
+            strips = [S.Kernel(*catalog.paths(e)) for e in edges]
+            opened += strips
+            kern.set_edge_kernels(*strips)
+        if mode is not None:
+            kern.set_stream_k(mode)
+        plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0,
+                kern.edge_interior(m, n, k))
+        _say(f"graph {main} {m}x{n}x{k}: splits, stream-K tiles, interior = {plan}")
+        assert plan[0] > 1 or plan[1] > 0 or plan[2] != (m, n), "the case must use the scratch or the strips"
+        dA, dB, dC, dD = S.DeviceBuffer(4 * m * k), S.DeviceBuffer(4 * k * n), S.DeviceBuffer(4 * m * n), \
+            S.DeviceBuffer(4 * m * n)
+        kern.set_stream(stream.value)
+        # one eager call first: it looks up the scratch's device address
+        dA.upload(_col(S.fill_matrix(m, k, 1, 0)))
+        dB.upload(_col(S.fill_matrix(k, n, 1, 1)))
+        dC.upload(_col(S.fill_matrix(m, n, 1, 2)))
+        kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
+        kern.synchronize()
+        _ok(_hip.hipStreamBeginCapture(stream, CAPTURE_MODE_GLOBAL), "hipStreamBeginCapture")
+        try:
+            kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
+        finally:
+            _ok(_hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        _ok(_hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+        for replay in range(3):
+            seed = 50 + replay
+            A, B, C = S.fill_matrix(m, k, seed, 0), S.fill_matrix(k, n, seed, 1), S.fill_matrix(m, n, seed, 2)
+            dA.upload(_col(A))
+            dB.upload(_col(B))
+            dC.upload(_col(C))
+            dD.upload(np.full((m, n), np.nan, dtype=np.float32))
+            _ok(_hip.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+            _ok(_hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+            D_graph = dD.download().reshape(n, m).T.copy()
+            dD.upload(np.full((m, n), np.nan, dtype=np.float32))
+            kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
+            kern.synchronize()
+            D_eager = dD.download().reshape(n, m).T.copy()
+            _say(f"  replay {replay}: checking")
+            assert np.array_equal(D_graph, D_eager), f"replay {replay} differs from the eager launch"
+            err = oracle.normwise_error(D_graph, oracle.cpu_gemm_mt(A, B, C, 1.5, -0.5, threads=16))
+            assert err <= oracle.tolerance(k), (replay, err)
+    finally:
+        if exe.value:
+            _hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            _hip.hipGraphDestroy(graph)
+        for kk in opened:
+            kk.set_stream(None)
+        for kk in reversed(opened):
+            kk.close()
+        _hip.hipStreamDestroy(stream)
