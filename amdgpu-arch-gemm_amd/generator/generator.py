@@ -824,7 +824,7 @@ def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimi
 def default_config() -> Tuple[GemmSolutionConfig, GemmOptimizations]:
     cfg = GemmSolutionConfig(DataType.FP32, DataType.FP32, DataType.FP32, DataType.FP32,
                              MFMA_32x32x2, (2, 2), (4, 2), 16, False, False, vmem_stage=2)
-    opt = GemmOptimizations(1, wgm=4, plr=3, gw=0, map_k_idx=0, xcd=8, occ=2)
+    opt = GemmOptimizations(1, wgm=4, plr=3, gw=1, map_k_idx=0, xcd=8, occ=2)
     return cfg, opt
 
 

@@ -330,6 +330,15 @@ def test_cli_writes_co_and_toml(tmp_path):
     assert d["name"] == "generated_gemm" and d["arch"] == "gfx950"
 
 
+def test_cli_default_is_the_catalog_headline_instance():
+    """The CLI's default code object is the instance the catalog runs at 4096^3."""
+    name = catalog.select(4096, 4096, 4096)
+    want_cfg, want_opt = catalog.SOLUTIONS[name]
+    got_cfg, got_opt = g.default_config()
+    assert got_cfg.to_dict() == want_cfg.to_dict(), name
+    assert got_opt.to_dict() == want_opt.to_dict(), name
+
+
 # ------------------------------------------------------------- catalog
 def test_select_prefers_tuned_and_divisible():
     for shape, name in catalog.PREFERRED:
