@@ -494,6 +494,66 @@ def test_split_and_plain_launches_interleave_on_one_handle(kernels):
             _check(D, ref, k, f"{name} splits {splits}")
 
 
+CONCURRENT_CASES = [
+    # (instance, stream-K mode or None, m, n, k): each launch keeps partials in its handle's workspace
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 512, 512, 16384),                  # split-K, 4 ranges
+    ("mt128x64_a16_wg2x2_dk32_s3_occ2", 2, 128 * 30 - 5, 64 * 22 - 3, 333),  # stream-K fix-up
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 256, 256, 4096),                   # same instance, another handle
+]
+
+
+def test_handles_launch_concurrently_on_their_own_streams(kernels):
+    """Handles launch on streams of their own (one handle on a caller's stream
+    through sgemm_set_stream), each with its own split-K / stream-K workspace:
+    launches of three handles issued back to back, with no synchronisation
+    between them (free to overlap on the GPU), must give the bits each gives
+    alone."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")   # the HIP runtime the library itself links
+    stream = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(stream)) == 0
+    kerns, probs = [], []
+    try:
+        for i, (name, mode, m, n, k) in enumerate(CONCURRENT_CASES):
+            kern = _kernel(name)
+            kerns.append(kern)
+            if mode is not None:
+                kern.set_stream_k(mode)
+            plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0)
+            _say(f"concurrent {i}: {name} {m}x{n}x{k}: K ranges, stream-K tiles = {plan}")
+            assert plan[0] > 1 or plan[1] > 0, "each case must use its workspace"
+            A, B, C = S.fill_matrix(m, k, 60 + i, 0), S.fill_matrix(k, n, 60 + i, 1), S.fill_matrix(m, n, 60 + i, 2)
+            bufs = [S.DeviceBuffer.from_array(x) for x in (A, B, C)] + [S.DeviceBuffer(4 * m * n)]
+            probs.append((A, B, C, bufs, m, n, k))
+        kerns[1].set_stream(stream.value)
+
+        def launch_all(sync_each):
+            outs = []
+            for kern, (_, _, _, (dA, dB, dC, dD), m, n, k) in zip(kerns, probs):
+                dD.upload(np.full((m, n), np.nan, dtype=np.float32))
+            for kern, (_, _, _, (dA, dB, dC, dD), m, n, k) in zip(kerns, probs):
+                for _ in range(3):
+                    kern.launch(dA, dB, dC, dD, m, n, k, alpha=0.75, beta=-1.25)
+                if sync_each:
+                    kern.synchronize()
+            for kern in kerns:
+                kern.synchronize()
+            for _, (_, _, _, (_, _, _, dD), m, n, _) in zip(kerns, probs):
+                outs.append(dD.download().reshape(n, m).T.copy())
+            return outs
+
+        alone = launch_all(sync_each=True)
+        together = launch_all(sync_each=False)
+        for i, (D1, D2, (A, B, C, _, m, n, k)) in enumerate(zip(alone, together, probs)):
+            assert np.array_equal(D1, D2), f"case {i}: concurrent launches changed the result"
+            _check(D2, oracle.cpu_gemm_mt(A, B, C, 0.75, -1.25, threads=16), k, f"concurrent case {i}")
+    finally:
+        for kern in kerns:
+            kern.set_stream(None)
+            kern.close()
+        hip.hipStreamDestroy(stream)
+
+
 def test_host_split_rule_matches_the_catalog(kernels):
     """The library's per-problem split count (sgemm_launch_splits) is the rule
     catalog.auto_split restates, on this device's compute-unit count."""
