@@ -905,13 +905,20 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // (atom_n columns of the wave's SM-row sub-tile) are scattered into a
     // column-major LDS chunk, then read back as float4 runs down each column,
     // so one store instruction writes whole columns (SM * 4 bytes each, full
-    // 128-byte lines) instead of 16 bytes in each of atom_n columns.
+    // 128-byte lines) instead of 16 bytes in each of atom_n columns.  Columns
+    // are unpadded and float4 run r of column c sits at run r ^ (c mod
+    // E_RUNS): the scatter's 16-byte writes (8 lanes a cycle, 8 columns at
+    // one row) and the read-back's 16-byte reads (a half-wave's quads
+    // {0,3,5,6} and {1,2,4,7} a cycle, down one to eight columns) then reach
+    // distinct banks.  A 4-float pad instead serves the writes but not the
+    // reads when a half-wave spans two or more columns (SM <= 64).
     constexpr int SM = AT::M * WT0;           // rows of a wave's sub-tile
-    constexpr int E_LD = SM + 4;              // LDS column stride (4-float pad: conflict-free scatter)
+    constexpr int E_LD = SM;                  // LDS column stride
     constexpr int E_CHUNK = AT::N * E_LD;     // floats of LDS per wave
     constexpr int E_RUNS = SM / 4;            // float4 runs per column
     constexpr int E_PER_LANE = AT::N * E_RUNS / 64;
     static_assert(AT::N * E_RUNS % 64 == 0, "a column group is a whole number of float4s per lane");
+    static_assert((E_RUNS & (E_RUNS - 1)) == 0, "the run swizzle stays inside a column");
     // SG_GW (the reference's global-write flavour, generator.py:2290-2508):
     // 1 stages through LDS as above when the chunks fit, 0 always stores
     // straight from the accumulators (no LDS, fewer live registers)
@@ -936,12 +943,31 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             const __amdgpu_buffer_rsrc_t rsc = sub_rsrc(beta != 0.0f ? c : d, beta != 0.0f ? ldc : ldd);
 #pragma unroll
             for (int jn = 0; jn < WT1; ++jn) {
+                // A lane's slots q..q+3 (q a multiple of 4) hold four
+                // consecutive rows of its column in both atoms, so below four
+                // rows per slot (WT0 < 4) QG slots share one 16-byte write:
+                // every write is whole float4 runs (8- and 4-byte writes
+                // would serve 16 and 32 lanes a cycle, more than the 8
+                // distinct runs a row of 8 columns offers).
+                constexpr int QG = WT0 >= 4 ? 1 : 4 / WT0;
+                static_assert(4 % QG == 0 && AT::ACC % QG == 0, "slot groups stay inside a run of four rows");
+                static_assert((WT0 * QG) % 4 == 0, "whole float4 runs per write");
+                const int ecol = lane % AT::N;
+                const int eswz = ecol & (E_RUNS - 1);
 #pragma unroll
-                for (int q = 0; q < AT::ACC; ++q) {
-                    float v[WT0];
+                for (int q = 0; q < AT::ACC; q += QG) {
+                    float v[WT0 * QG];
 #pragma unroll
-                    for (int i = 0; i < WT0; ++i) v[i] = alpha * acc[i][jn][q];
-                    store_row<WT0>(e + (lane % AT::N) * E_LD + AT::row(q, lane) * WT0, v);
+                    for (int g = 0; g < QG; ++g)
+#pragma unroll
+                        for (int i = 0; i < WT0; ++i) v[g * WT0 + i] = alpha * acc[i][jn][q + g];
+                    const int run0 = AT::row(q, lane) * WT0 / 4;
+#pragma unroll
+                    for (int h = 0; h < WT0 * QG / 4; ++h) {
+                        f32x4 t;
+                        t.x = v[4 * h]; t.y = v[4 * h + 1]; t.z = v[4 * h + 2]; t.w = v[4 * h + 3];
+                        *reinterpret_cast<f32x4*>(e + ecol * E_LD + ((run0 + h) ^ eswz) * 4) = t;
+                    }
                 }
                 // the wave's scattered writes are complete before any lane reads them back
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -963,7 +989,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 #pragma unroll
                     for (int b = 0; b < EB; ++b) {
                         const int idx = (p0 + b) * 64 + lane;
-                        v[b] = *reinterpret_cast<const f32x4*>(e + (idx / E_RUNS) * E_LD + (idx % E_RUNS) * 4);
+                        const int ec = idx / E_RUNS;
+                        v[b] = *reinterpret_cast<const f32x4*>(e + ec * E_LD + ((idx % E_RUNS) ^ (ec & (E_RUNS - 1))) * 4);
                     }
                     if (beta != 0.0f) {
                         f32x4 cv[EB];

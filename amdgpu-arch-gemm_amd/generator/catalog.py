@@ -67,6 +67,20 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     # 8192 x 8192 x 256), behind at K = 512 and at 4096^3
     "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": (_cfg(MFMA_32x32x2, (2, 2), (4, 2), 16, stages=2),
                                               _opt(wgm=4, plr=2, xcd=8, occ=2)),
+    # the same tile with eight waves of 64 x 64 (4 x 2), registers capped for
+    # four waves per SIMD: two work-groups, 16 waves per CU
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2": (_cfg(MFMA_32x32x2, (4, 2), (2, 2), 16, stages=2),
+                                              _opt(wgm=4, plr=2, xcd=8, occ=4)),
+    # eight waves (2 x 4 of 64 x 16) and a 64-deep K tile: two waves per SIMD
+    # take turns at its MFMAs, one 96 KiB work-group per CU.  At 16384 x 128 x
+    # 4096 (one tile per CU) 146.4 / 146.7 TFLOP/s in interleaved runs against
+    # 142.5 / 143.4 for the four-wave 128 x 64 instance; with the work-group
+    # remap and XCD mapping (wgm=4, xcd=8) it ran 144.2 / 143.8.  Only grids
+    # of exactly two rounds with N = 128 favour a remap (wgm=2, xcd=8:
+    # 131.8 against 121.0 at 32768 x 128 x 4096, the tiles sharing an A panel
+    # then run in one round); stream-K grids favour the plain order (20000 x
+    # 128 x 4096: 122.5 against 111.0)
+    "mt128x64_a16_wg2x4_dk64": (_cfg(MFMA_16x16x4, (2, 4), (4, 1), 64), _opt(plr=3, sk=0, stk=1)),
     "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
     # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
     "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
@@ -138,28 +152,38 @@ PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
     # before)
     ((4096, 4096, 4096), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
-    ((8192, 8192, 256), "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2"),
-    # 140.5-140.7 TFLOP/s in bench.py against 140.3-140.5 without occ=2
-    ((16384, 128, 4096), "mt128x64_a16_wg2x2_dk32_s3_occ2"),
+    # eight 64 x 64 waves, two work-groups per CU: 135.9 / 136.0 TFLOP/s in
+    # bench.py against 134.3 / 134.4 for the four-wave 256 x 128 plr=2 instance
+    ((8192, 8192, 256), "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2"),
+    # 144.2 / 144.2 TFLOP/s in bench.py against 141.2 / 141.2 for the
+    # four-wave 128 x 64 occ=2 instance
+    ((16384, 128, 4096), "mt128x64_a16_wg2x4_dk64"),
     # few output tiles and a deep K (bench.py --workload deepk): the split-K kernel
     ((512, 512, 16384), "mt64x64_a16_wg1x4_dk32_s3"),
 ]
 # Instances select() chooses among for other shapes: (fraction of the FP32
-# MFMA peak the K loop reaches, fixed seconds per tile), fitted by least
-# squares on log time to 41 shapes from 768^3 to 16384 x 8192 x 256 (MI355X,
-# interleaved runs; rms error 4.8%).  The plr=2 twin of the 256 x 128 instance
-# pays a smaller fixed cost for a slower loop: it wins below K ~ 480.  The
-# 64 x 64 one also carries the split-K kernel: against
-# mt128x64_a16_wg2x2_dk16_s2 it measured 125.6 / 127.5 / 114.8 TFLOP/s at
-# 512^2 x 16384, 1024 x 512 x 8192 and 256^2 x 65536 (host-chosen split
-# counts), against 109.0 / 110.5 / 59.0.
-CANDIDATES: Dict[str, Tuple[float, float]] = {
-    "mt256x256_a32_wg2x2_dk24_s3": (0.981, 0.0),
-    "mt256x128_a32_wg2x2_dk16_s3_occ2": (0.985, 2.33e-6),
-    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": (0.961, 1.02e-6),
-    "mt128x64_a16_wg2x2_dk32_s3": (0.924, 0.0),
-    "mt128x64_a16_wg2x2_dk32_s3_occ2": (0.940, 0.66e-6),
-    "mt64x64_a16_wg1x4_dk32_s3": (0.913, 0.0),
+# MFMA peak the K loop reaches when the grid gives a CU more than one
+# work-group, fixed seconds per tile, the fraction when each CU holds one
+# work-group), fitted per instance by least squares on log time to 41 shapes
+# from 1024^3 to 16384^2 x 256 timed interleaved on MI355X (rms error 1-7%
+# per instance).  One work-group per CU is the four-wave instances' weak spot
+# (0.77-0.83 for 128 x 64 and 64 x 64 against 0.93-0.95 on fuller grids), not
+# the eight-wave ones', whose two waves per SIMD hide each other's waits: at
+# 8192 x 256 x 4096 the eight-wave 128 x 64 runs 145 TFLOP/s against 132 for
+# the four-wave occ=2 one.  The plr=2 twin of the 256 x 128 instance pays a
+# smaller fixed cost for a slower loop: it wins at short K.  The 64 x 64 one
+# also carries the split-K kernel: against mt128x64_a16_wg2x2_dk16_s2 it
+# measured 125.6 / 127.5 / 114.8 TFLOP/s at 512^2 x 16384, 1024 x 512 x 8192
+# and 256^2 x 65536 (host-chosen split counts), against 109.0 / 110.5 / 59.0.
+CANDIDATES: Dict[str, Tuple[float, float, float]] = {
+    "mt256x256_a32_wg2x2_dk24_s3": (0.980, 5.00e-6, 0.985),
+    "mt256x128_a32_wg2x2_dk16_s3_occ2": (0.990, 2.50e-6, 0.980),
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": (0.945, 0.25e-6, 0.880),
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2": (0.965, 0.50e-6, 0.930),
+    "mt128x64_a16_wg2x2_dk32_s3": (0.945, 0.25e-6, 0.805),
+    "mt128x64_a16_wg2x2_dk32_s3_occ2": (0.950, 0.75e-6, 0.830),
+    "mt128x64_a16_wg2x4_dk64": (0.935, 1.00e-6, 0.910),
+    "mt64x64_a16_wg1x4_dk32_s3": (0.925, 0.00e-6, 0.770),
 }
 # instances attached (sgemm_set_edge_kernels) to the large-tile ones for thin
 # edge strips: (rows, cols) = a 16-row tile for the strip of rows past the last
@@ -171,16 +195,22 @@ EDGE_KERNEL: Dict[str, Tuple[str, str]] = {
     "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": EDGE_PAIR,
     "mt256x256_a32_wg2x2_dk24_s3": EDGE_PAIR,
     "mt128x64_a16_wg2x2_dk32_s3_occ2": EDGE_PAIR,
+    "mt128x64_a16_wg2x4_dk64": EDGE_PAIR,
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2": EDGE_PAIR,
 }
 
 
 # work-groups of generated_gemm resident per CU for the instances with edge
-# kernels (the compiler's occupancy; the host library queries it)
+# kernels and the time model's candidates (the compiler's occupancy; the host
+# library queries it): an occ=N instance holds N four-wave work-groups or
+# N / 2 eight-wave ones
 RESIDENT_PER_CU: Dict[str, int] = {
     "mt256x128_a32_wg2x2_dk16_s3_occ2": 2,
     "mt256x128_a32_wg2x2_dk16_s3_occ2_plr2": 2,
     "mt256x256_a32_wg2x2_dk24_s3": 1,
     "mt128x64_a16_wg2x2_dk32_s3_occ2": 2,
+    "mt128x64_a16_wg2x4_dk64": 1,
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2": 2,
 }
 
 
@@ -225,6 +255,7 @@ def edge_interior(name: str, m: int, n: int, k: int,
 STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
     "mt64x64_a16_wg1x4_dk32_s3": 3,
     "mt128x64_a16_wg2x2_dk32_s3_occ2": 2,
+    "mt128x64_a16_wg2x4_dk64": 1,
 }
 # rate of the streamed tiles relative to whole tiles: interleaved runs at
 # 1792^2..4864^2 x 4096 and 3000^3 measured 0.89-0.92 of the model's whole-tile
@@ -344,13 +375,21 @@ def predicted_seconds(name: str, m: int, n: int, k: int, compute_units: int = GF
     return t
 
 
+def _loop_efficiency(name: str, work_groups: int, compute_units: int) -> float:
+    """The K loop's fraction of the MFMA peak: the full rate once the grid
+    gives each CU more than one work-group, the lower one-work-group rate
+    otherwise (nothing beside it hides its waits)."""
+    eff, _, eff_alone = CANDIDATES.get(name, (0.9, 0.0, 0.9))
+    return eff_alone if work_groups <= compute_units else eff
+
+
 def predicted_launch_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
     """Time model behind select(): the CU with the most work-groups sets the
     time (rounds of tiles x K splits over the CUs, each work-group a K loop at
     the instance's MFMA efficiency plus its fixed cost and its epilogue's
     stores), and a split
     launch adds its partials' writes and the last work-group's reads.  Two
-    work-groups per CU (occ=2) hide half of each epilogue behind the other's
+    work-groups per CU (RESIDENT_PER_CU) hide half of each epilogue behind the other's
     K loop.  Wave quantisation is the point: 3000^3 in 256 x 128 tiles is 288
     work-groups, two rounds on 32 CUs, at half the speed of 64 x 64 tiles.  An
     instance with a stream-K kernel that the host would use on this grid
@@ -364,15 +403,16 @@ def predicted_launch_seconds(name: str, m: int, n: int, k: int, compute_units: i
     ktiles = -(-max(k, 1) // dk)
     k_range = -(-ktiles // splits) * dk
     rounds = -(-(tiles * splits) // compute_units)
-    occ = max(opt.occ, 1)
+    occ = RESIDENT_PER_CU.get(name, max(opt.occ, 1))  # work-groups per CU
     tile_bytes = t0 * t1 * 4
-    eff, fixed = CANDIDATES.get(name, (0.9, 0.0))
+    eff = _loop_efficiency(name, tiles * splits, compute_units)
+    fixed = CANDIDATES.get(name, (0.9, 0.0, 0.9))[1]
     loop = 2.0 * t0 * t1 * k_range / (_CU_FLOPS * eff) + fixed
     epilogue = tile_bytes / _CU_WRITE_BYTES_PER_S
     reduce = 2.0 * splits * tile_bytes / _CU_WRITE_BYTES_PER_S if splits > 1 else 0.0
     sk = 0
     if splits == 1 and opt.stream_k:
-        groups = compute_units * STREAM_K_GROUPS_PER_CU.get(name, max(opt.occ, 1))
+        groups = compute_units * STREAM_K_GROUPS_PER_CU.get(name, occ)
         sk = stream_k_tiles(tiles, groups, k, 1, dk, opt.stream_k_rounds)
     if sk:
         # stream-K: no partial last round; the streamed tiles run at a lower

@@ -319,6 +319,49 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
     return out
 
 
+def lds_epilogue_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tiling: Sequence[int],
+                          pad: int = 0, swizzle: bool = True, grouped: bool = True):
+    """The staged epilogue's LDS instructions of one work-group, in the format
+    of lds_tile_accesses -- the address formulas of csrc/sgemm_gfx950.hip: per
+    column group of a wave's sub-tile, the accumulator scatter into the wave's
+    column-major chunk (column stride SM + ``pad`` floats, SM the sub-tile's
+    rows) and the read-back of float4 runs down each column.  A lane's rows
+    come in groups of four: ``grouped`` writes 4 / WT0 slots with one 16-byte
+    write when the wave tile is under four atoms tall (else one write per
+    slot); ``swizzle`` stores float4 run r of column c at run r ^ (c mod
+    SM / 4).  The defaults are the kernel's layout.  The waves' chunks differ
+    by uniform offsets: wave 0's pattern, counted once per wave and column
+    group."""
+    am, an = mfma[0], mfma[1]
+    wt0, wt1 = wave_tiling
+    waves = wave_group[0] * wave_group[1]
+    acc = am * an // 64
+    sm = am * wt0
+    e_ld = sm + pad
+    e_runs = sm // 4
+    qg = 1 if (wt0 >= 4 or not grouped) else 4 // wt0
+
+    def row(q, lane):
+        return (q & 3) + 8 * (q >> 2) + 4 * (lane >> 5) if am == 32 else q + 4 * (lane >> 4)
+
+    def at(col, pos):  # byte address of float `pos` of column `col`
+        run = pos // 4
+        if swizzle:
+            run ^= col % e_runs
+        return (col * e_ld + run * 4 + pos % 4) * 4
+
+    out = []
+    for q in range(0, acc, qg):
+        width = 4 * wt0 * qg
+        for part in range(max(1, width // 16)):
+            addrs = [at(lane % an, row(q, lane) * wt0 + 4 * part) for lane in range(64)]
+            out.append(("epilogue write", 0, addrs, min(width, 16), True, waves * wt1))
+    for p in range(an * e_runs // 64):
+        idx = [p * 64 + lane for lane in range(64)]
+        out.append(("epilogue read", 0, [at(i // e_runs, (i % e_runs) * 4) for i in idx], 16, False, waves * wt1))
+    return out
+
+
 def lds_tile_cycles(accesses) -> int:
     """LDS cycles of lds_tile_accesses' instructions."""
     return sum(count * lds_access_cycles(addrs, width, write) for _, _, addrs, width, write, count in accesses)

@@ -38,7 +38,7 @@ ROOT = os.path.dirname(PKG)
 sys.path.insert(0, PKG)
 
 from generator import catalog  # noqa: E402
-from generator.generator import lds_access_cycles, lds_lane_cycle, lds_tile_accesses  # noqa: E402
+from generator.generator import lds_access_cycles, lds_epilogue_accesses, lds_lane_cycle, lds_tile_accesses  # noqa: E402
 
 PROBE = os.path.join(HERE, "lds_probe")
 LDS_BYTES = 64 * 1024
@@ -48,6 +48,8 @@ PADS = (0, 4, 8, 12, 16)
 # instances whose kernel accesses are measured
 INSTANCES = (
     "mt256x128_a32_wg2x2_dk16_s3_occ2",
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2",
+    "mt128x64_a16_wg2x4_dk64",
     "mt256x256_a32_wg2x2_dk24_s3",
     "mt256x256_a32_wg2x2_dk16_s3",
     "mt128x64_a16_wg2x2_dk32_s3_occ2",
@@ -100,18 +102,38 @@ def kernel_accesses(name: str, operand: str, pad: int, swz: Tuple[int, int]):
                              operand, pad, swz)
 
 
+# staged-epilogue layouts measured per instance: (label, column pad in floats,
+# run swizzle, 16-byte grouped writes)
+EPILOGUE_LAYOUTS = (
+    ("one write per slot, pad 4", 4, False, False),
+    ("grouped writes, pad 4", 4, False, True),
+    ("kernel: grouped writes, run ^ column, pad 0", 0, True, True),
+)
+
+
+def epilogue_accesses(name: str, pad: int, swizzle: bool, grouped: bool):
+    cfg, _ = catalog.SOLUTIONS[name]
+    return lds_epilogue_accesses(cfg.mfma, cfg.wave_group, cfg.wave_tiling, pad, swizzle, grouped)
+
+
 def kernel_patterns() -> List[Pattern]:
     """Every distinct wave-wide access of each measured layout (the waves'
     operand reads differ by uniform offsets; their tile writes are listed per
     wave), named by its address pattern so that layouts share dispatches."""
     out, seen = [], set()
+
+    def add(accesses):
+        for kind, wave, addrs, width, write, _ in accesses:
+            key = _pattern_key(addrs, width, write)
+            if key not in seen and max(addrs) + width <= LDS_BYTES:
+                seen.add(key)
+                out.append((key, "w" if write else "r", width, list(addrs)))
+
     for name in INSTANCES:
         for _, operand, pad, swz in kernel_layouts(name):
-            for kind, wave, addrs, width, write, _ in kernel_accesses(name, operand, pad, swz):
-                key = _pattern_key(addrs, width, write)
-                if key not in seen and max(addrs) + width <= LDS_BYTES:
-                    seen.add(key)
-                    out.append((key, "w" if write else "r", width, list(addrs)))
+            add(kernel_accesses(name, operand, pad, swz))
+        for _, pad, swizzle, grouped in EPILOGUE_LAYOUTS:
+            add(epilogue_accesses(name, pad, swizzle, grouped))
     return out
 
 
@@ -197,6 +219,21 @@ def summarise(res: Dict[str, Tuple[float, float]], pats: List[Pattern], cmd: str
             desc = f"pad {pad}" + (f", swizzle {swz}" if swz[1] else "")
             shown = "n/a (beyond the probe's LDS)" if meas is None else f"{meas:.0f}"
             lines.append(f"| `{name}` | {operand.upper()} | {label}: {desc} | {shown} | {model:.0f} | {base:.0f} |")
+    lines += ["", "## The staged epilogue per layout", "",
+              "LDS conflict cycles of one work-group's epilogue (every wave's accumulator scatter and float4 "
+              "read-back, `generator.lds_epilogue_accesses`), measured and modelled as above.", "",
+              "| instance | layout | measured | model | conflict-free cycles |", "|---|---|---|---|---|"]
+    for name in INSTANCES:
+        for label, pad, swizzle, grouped in EPILOGUE_LAYOUTS:
+            meas = model = base = 0.0
+            for _, _, addrs, width, write, count in epilogue_accesses(name, pad, swizzle, grouped):
+                key = _pattern_key(addrs, width, write)
+                groups = len({lds_lane_cycle(l, width, write) for l in range(64)})
+                meas = meas + count * res[key][0] if key in res and meas is not None else None
+                model += count * (lds_access_cycles(addrs, width, write) - groups)
+                base += count * groups
+            shown = "n/a (beyond the probe's LDS)" if meas is None else f"{meas:.0f}"
+            lines.append(f"| `{name}` | {label} | {shown} | {model:.0f} | {base:.0f} |")
     return "\n".join(lines) + "\n"
 
 

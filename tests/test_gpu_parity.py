@@ -720,6 +720,20 @@ def test_edge_kernels_only_where_they_save_a_round(kernels):
     assert catalog.edge_interior("mt128x64_a16_wg2x2_dk32_s3_occ2", 2500, 2500, 2500, cus) == (2500, 2500)
 
 
+def test_catalog_occupancy_tables_match_the_library(kernels):
+    """The stream-K groups the catalog's time model assumes are the ones the
+    library queries from the runtime (occupancy of generated_gemm_streamk x
+    CUs); every stream-K instance the model considers is listed."""
+    cus = S.device_info()["compute_units"]
+    for name, per_cu in catalog.STREAM_K_GROUPS_PER_CU.items():
+        with _kernel(name) as kern:
+            _say(f"stream-K groups {name}: {kern.info.stream_k_groups}")
+            assert kern.info.stream_k_groups == per_cu * cus, name
+    for name in catalog.CANDIDATES:
+        _, opt = catalog.SOLUTIONS[name]
+        assert not opt.stream_k or name in catalog.STREAM_K_GROUPS_PER_CU, name
+
+
 def test_stream_k_errors(kernels):
     with _kernel("mt256x128_a32_wg2x2_dk16_s3_occ2") as kern:
         assert kern.info.stream_k_groups == 0
