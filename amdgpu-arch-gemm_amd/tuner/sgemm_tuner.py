@@ -83,7 +83,7 @@ GFX950_WAVE_GROUPS = [(2, 2), (4, 1)]
 # --space gfx950-wide: also 32-wide tiles and every wave group of the reference
 GFX950_WIDE_MACRO_TILES = [(a, b) for a in (32, 64, 128, 256) for b in (32, 64, 128, 256)]
 GFX950_WIDE_WAVE_GROUPS = SUPPORTED_WAVE_GROUPS + [(4, 1), (1, 4)]
-GFX950_DEPTH_K = [16, 24, 32]
+GFX950_DEPTH_K = [16, 24, 32, 64]
 GFX950_VMEM_STAGES = [1, 2]
 GFX950_WGM = [1, 4, 8]
 GFX950_XCD = [0, 8]
@@ -443,7 +443,8 @@ def main(argv=None):
     ap.add_argument("--split-k", default="1",
                     help="comma-separated split-K values for stage 2 (0 = chosen per problem; default 1: no split)")
     ap.add_argument("--occ", default="0,2",
-                    help="comma-separated occupancy targets for stage 2 (0 = compiler's choice; 2 = two waves per SIMD)")
+                    help="comma-separated occupancy targets (waves per SIMD) for stages 1 and 2 (0 = compiler's "
+                         "choice; 2 / 4 = registers capped for two / four)")
     ap.add_argument("--gw", default="1",
                     help="comma-separated epilogue flavours for stage 2 (1 = staged through LDS, 0 = direct stores)")
     ap.add_argument("--tiles", default=None,

@@ -162,3 +162,23 @@ def test_compile_only_builds_stage1_with_split_and_occupancy_knobs(tmp_path):
     keys = {T.point_key(*p) for p in T.knob_points(cfg, split_ks=(1, 0), occs=(0, 2))}
     assert any(k.endswith("_occ2_sk0") for k in keys) and any(k.endswith("_occ2") for k in keys)
     assert sum(1 for k in keys if k.endswith("_sk0")) * 2 == len(keys)
+
+
+@pytest.mark.parametrize("name,occs,depths", [
+    ("mt128x64_a16_wg2x4_dk64", (0,), (32, 64)),              # cfg5's instance
+    ("mt256x128_a32_wg4x2_dk16_s3_occ4_plr2", (0, 2, 4), (16,)),  # cfg4's instance
+])
+def test_wide_space_reaches_the_eight_wave_instances(name, occs, depths):
+    """With --space gfx950-wide, --occ and --stage1-depths covering them, the
+    tuner's stage 1 holds the geometry of the catalog's eight-wave instances
+    and stage 2 around it holds the instance's exact knobs."""
+    from generator import catalog
+    cfg, opt = catalog.SOLUTIONS[name]
+    geo = (tuple(cfg.mfma), tuple(cfg.wave_group), tuple(cfg.wave_tiling))
+    stage1 = [c for c, o in T.geometry_points(T.DEFAULT_KNOBS, wide=True, occs=occs, depths=depths,
+                                              tiles=[tuple(cfg.tile_size)])
+              if (tuple(c.mfma), tuple(c.wave_group), tuple(c.wave_tiling)) == geo and o.occ == opt.occ]
+    assert stage1, name
+    keys = {T.point_key(c, o) for c, o in T.knob_points(stage1[0], split_ks=(opt.split_k,), occs=(opt.occ,),
+                                                          gws=(opt.gw,))}
+    assert T.point_key(cfg, opt) in keys, name
