@@ -386,8 +386,8 @@ def _loop_efficiency(name: str, work_groups: int, compute_units: int) -> float:
 def predicted_launch_seconds(name: str, m: int, n: int, k: int, compute_units: int = GFX950_COMPUTE_UNITS) -> float:
     """Time model behind select(): the CU with the most work-groups sets the
     time (rounds of tiles x K splits over the CUs, each work-group a K loop at
-    the instance's MFMA efficiency plus its fixed cost and its epilogue's
-    stores), and a split
+    the instance's MFMA efficiency (_loop_efficiency) plus its fixed cost and
+    its epilogue's stores), and a split
     launch adds its partials' writes and the last work-group's reads.  Two
     work-groups per CU (RESIDENT_PER_CU) hide half of each epilogue behind the other's
     K loop.  Wave quantisation is the point: 3000^3 in 256 x 128 tiles is 288
