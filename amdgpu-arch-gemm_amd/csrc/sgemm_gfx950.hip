@@ -448,12 +448,41 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // element (row, kk) of op(A) is a[row + kk*lda] (NN) or a[kk + row*lda] (T)
     const float* a_tile = TA ? a + (size_t)row0 * lda : a + row0;
     const float* b_tile = TB ? b + col0 : b + (size_t)col0 * ldb;
+    // Chunk ch of a K tile -> (c0, c1), its float4 position along the
+    // operand's contiguous dimension and across it.  Along-row chunks (A, B)
+    // go contiguous dimension first.  The transposed operands' chunks are
+    // scattered with four ds_write_b32 down LDS columns, so their order sets
+    // the banks 32 lanes hit at once: A^T takes pairs of k chunks, then m (32
+    // rows of m at one k pair); B^T takes 16 k, then n chunks (16 columns of
+    // k at two row groups four rows apart).  Both keep 32 or 64 contiguous
+    // bytes per lane group in global memory.
+    auto a_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
+        if constexpr (TA && A_C0 % 2 == 0) {
+            c0 = (ch & 1) + 2 * ((ch >> 1) / MT0);
+            c1 = (ch >> 1) % MT0;
+        } else {
+            c0 = ch % A_C0;
+            c1 = ch / A_C0;
+        }
+    };
+    auto b_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
+        if constexpr (TB) {
+            constexpr int KG = DK % 16 == 0 ? 16 : DK;
+            const int rest = ch / KG;
+            c0 = rest % B_C0;
+            c1 = ch % KG + KG * (rest / B_C0);
+        } else {
+            c0 = ch % B_C0;
+            c1 = ch / B_C0;
+        }
+    };
     uint32_t a_off[G::LA], b_off[G::LB];  // bytes from the K tile's first element
     int a_lds[G::LA], b_lds[G::LB];
 #pragma unroll
     for (int i = 0; i < G::LA; ++i) {
         const int ch = tid + i * NT;
-        const int c0 = ch % A_C0, c1 = ch / A_C0;
+        int c0, c1;
+        a_chunk(ch, c0, c1);
         // a chunk of rows wholly past m reads the tile's first row instead
         if constexpr (!TA) {  // c0: m / 4, c1: k
             const uint32_t r = row0 + (uint32_t)(c0 * 4) < m ? (uint32_t)(c0 * 4) : 0u;
@@ -468,7 +497,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 #pragma unroll
     for (int i = 0; i < G::LB; ++i) {
         const int ch = tid + i * NT;
-        const int c0 = ch % B_C0, c1 = ch / B_C0;
+        int c0, c1;
+        b_chunk(ch, c0, c1);
         // a chunk of columns wholly past n reads the tile's first column instead
         if constexpr (!TB) {  // c0: k / 4, c1: n
             const uint32_t cc = col0 + (uint32_t)c1 < n ? (uint32_t)c1 : 0u;
@@ -574,7 +604,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
                     if constexpr (decltype(head)::on) {
                         // k inside the tile of the chunk's first element: c1 (A), 4 * c0 (A^T)
-                        const int kk = TA ? (ch % A_C0) * 4 : ch / A_C0;
+                        int c0, c1;
+                        a_chunk(ch, c0, c1);
+                        const int kk = TA ? c0 * 4 : c1;
                         ra[set][i] = head_load(rsa, a_off[i], kk, TA, TA ? 4u : lda * 4u);
                     } else {
                         ra[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)a_off[i], 0, 0));
@@ -587,7 +619,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
                     if constexpr (decltype(head)::on) {
                         // k inside the tile of the chunk's first element: 4 * c0 (B), c1 (B^T)
-                        const int kk = TB ? ch / B_C0 : (ch % B_C0) * 4;
+                        int c0, c1;
+                        b_chunk(ch, c0, c1);
+                        const int kk = TB ? c1 : c0 * 4;
                         rb[set][i] = head_load(rsb, b_off[i], kk, !TB, TB ? ldb * 4u : 4u);
                     } else {
                         rb[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)b_off[i], 0, 0));
@@ -600,7 +634,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             for (int i = 0; i < G::LA; ++i) {
                 const int ch = tid + i * NT;
                 if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
-                    const int c0 = ch % A_C0, c1 = ch / A_C0;
+                    int c0, c1;
+                    a_chunk(ch, c0, c1);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t row = row0 + (TA ? (uint32_t)c1 : (uint32_t)(c0 * 4 + e));
@@ -616,7 +651,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             for (int i = 0; i < G::LB; ++i) {
                 const int ch = tid + i * NT;
                 if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
-                    const int c0 = ch % B_C0, c1 = ch / B_C0;
+                    int c0, c1;
+                    b_chunk(ch, c0, c1);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint32_t col = col0 + (TB ? (uint32_t)(c0 * 4 + e) : (uint32_t)c1);

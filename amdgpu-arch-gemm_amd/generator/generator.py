@@ -279,20 +279,27 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
     shift, mask = b_swizzle
     out = []
 
-    def writes(chunks, per_row, addr_of):
+    def writes(chunks, order, addr_of):
         for i in range(-(-chunks // nt)):
             for w in range(waves):
                 lanes = [ch for ch in (64 * w + l + i * nt for l in range(64)) if ch < chunks]
                 if lanes:
-                    for addrs, width in addr_of([(ch % per_row, ch // per_row) for ch in lanes]):
+                    for addrs, width in addr_of([order(ch) for ch in lanes]):
                         out.append(("write", w, addrs, width, True, 1))
+
+    def rows_first(per_row):  # chunk -> (position along the row, row): the along-row operands
+        return lambda ch: (ch % per_row, ch // per_row)
 
     if operand == "a":
         lda = mt0 + pad
         if not trans_a:  # float4 along m into row k
-            writes(mt0 * depth_k // 4, mt0 // 4, lambda cc: [([c1 * lda * 4 + c0 * 16 for c0, c1 in cc], 16)])
-        else:  # float4 along k scattered down column m: four dword writes
-            writes(mt0 * depth_k // 4, depth_k // 4,
+            writes(mt0 * depth_k // 4, rows_first(mt0 // 4),
+                   lambda cc: [([c1 * lda * 4 + c0 * 16 for c0, c1 in cc], 16)])
+        else:  # float4 along k scattered down column m: four dword writes, k-chunk pairs then m
+            a_c0 = depth_k // 4
+            order = ((lambda ch: ((ch & 1) + 2 * ((ch >> 1) // mt0), (ch >> 1) % mt0)) if a_c0 % 2 == 0
+                     else rows_first(a_c0))
+            writes(mt0 * depth_k // 4, order,
                    lambda cc: [([((c0 * 4 + e) * lda + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
         width = 4 * wave_tiling[0]
         reads = [((l // am) * kpl * lda + (l % am) * wave_tiling[0]) * 4 for l in range(64)]
@@ -305,10 +312,12 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
         return c ^ ((n >> shift) & mask)
 
     if not trans_b:  # float4 along k into row n, chunk swizzled
-        writes(mt1 * depth_k // 4, depth_k // 4,
+        writes(mt1 * depth_k // 4, rows_first(depth_k // 4),
                lambda cc: [([(c1 * ldb + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
-    else:  # float4 along n scattered across rows: four dword writes
-        writes(mt1 * depth_k // 4, mt1 // 4,
+    else:  # float4 along n scattered across rows: four dword writes, 16 k then n chunks
+        kg = 16 if depth_k % 16 == 0 else depth_k
+        b_c0 = mt1 // 4
+        writes(mt1 * depth_k // 4, lambda ch: ((ch // kg) % b_c0, ch % kg + kg * ((ch // kg) // b_c0)),
                lambda cc: [([((c0 * 4 + e) * ldb + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
     for kb in range(nkb):
         reads = []
