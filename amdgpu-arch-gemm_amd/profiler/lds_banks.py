@@ -56,6 +56,8 @@ INSTANCES = (
     "mt64x64_a16_wg1x4_dk32_s3",
     "mt16x128_a16_wg1x4_dk64_s2",
     "mt64x16_a16_wg4x1_dk64_s3",
+    "mt256x256_a32_wg2x2_dk16_s3_tn",
+    "mt256x256_a32_wg2x2_dk16_s3_nt",
 )
 
 Pattern = Tuple[str, str, int, List[int]]  # name, r|w, bytes per lane, 64 byte addresses
