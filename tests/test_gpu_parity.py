@@ -432,6 +432,8 @@ SPLIT_CASES = [
     ("mt128x64_a16_wg2x2_dk16_s2", 512, 512, 16384, 0),      # few tiles, deep K: 16 ranges
     ("mt64x64_a16_wg1x4_dk32_s3", 256, 256, 65536, 0),       # 16 tiles: 16 ranges
     ("mt64x64_a16_wg1x4_dk32_s3", 1024, 1024, 1024, 0),      # 256 tiles: no split
+    ("mt128x64_a16_wg2x4_dk64", 4096, 128, 8192, 0),         # eight waves, 64 tiles: 4 ranges
+    ("mt128x64_a16_wg2x4_dk64", 1000, 333, 5000, 3),         # eight waves, edge tiles, a K remainder
 ]
 
 
@@ -570,7 +572,7 @@ def test_host_split_rule_matches_the_catalog(kernels):
 
 # ---------------------------------------------------------------- stream-K
 STREAM_INSTANCES = ["mt32x32_a32_wg1x1_dk16_s3_stk", "mt32x32_a16_wg2x2_dk16_stk_tn", "mt64x64_a16_wg1x4_dk32_s3",
-                    "mt128x64_a16_wg2x2_dk32_s3_occ2"]
+                    "mt128x64_a16_wg2x2_dk32_s3_occ2", "mt128x64_a16_wg2x4_dk64"]
 
 
 def _stream_shape(cfg, groups, rounds, seed):
