@@ -122,6 +122,12 @@
 #ifndef SG_PAD_B
 #define SG_PAD_B 4
 #endif
+#ifndef SG_ASWZ_SHIFT
+#define SG_ASWZ_SHIFT 0
+#endif
+#ifndef SG_ASWZ_MASK
+#define SG_ASWZ_MASK 0
+#endif
 #ifndef SG_TA
 #define SG_TA 0
 #endif
@@ -189,7 +195,7 @@ template <> struct Atom<16> {
     __device__ static __forceinline__ int row(int q, int lane) { return q + 4 * (lane >> 4); }
 };
 
-template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B>
+template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA>
 struct Geometry {
     typedef Atom<AM> atom;
     static constexpr int NT = WG0 * WG1 * 64;
@@ -198,9 +204,11 @@ struct Geometry {
     // k values a lane reads per LDS read of B (and MFMA steps per k block)
     static constexpr int KPL = (DK / atom::K >= 4) ? 4 : ((DK / atom::K >= 2) ? 2 : 1);
     static constexpr int KB = atom::K * KPL;
-    static constexpr int A_LD = MT0 + PAD_A;  // LDS row stride of the A tile (floats)
+    // A tile: [DK][MT0 + PAD_A] (m contiguous), or for A^T [MT0][DK + PAD_A]
+    // (k contiguous, like B); B tile: [MT1][DK + PAD_B]
+    static constexpr int A_LD = TA ? DK + PAD_A : MT0 + PAD_A;  // LDS row stride of the A tile (floats)
     static constexpr int B_LD = DK + PAD_B;   // LDS row stride of the B tile (floats)
-    static constexpr int A_STAGE = DK * A_LD;
+    static constexpr int A_STAGE = TA ? MT0 * A_LD : DK * A_LD;
     static constexpr int B_STAGE = MT1 * B_LD;
     static constexpr int STAGE = A_STAGE + B_STAGE;
     static constexpr int LDS_FLOATS = NBUF * STAGE;
@@ -220,7 +228,7 @@ struct Geometry {
     static_assert(LDS_FLOATS * 4 <= 163840, "LDS tile exceeds the 160 KiB of a gfx950 CU");
 };
 
-typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B> G;
+typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0> G;
 
 // B-tile chunk swizzle of row n (0: rows stored straight).  The XOR stays
 // inside a row when its chunk count is a multiple of MASK + 1, and a lane's
@@ -231,6 +239,18 @@ static_assert(SG_BSWZ_MASK == 0 || (SG_BSWZ_MASK & (SG_BSWZ_MASK + 1)) == 0, "sw
 static_assert((SG_DK / 4) % (SG_BSWZ_MASK + 1) == 0, "swizzle leaves the B row");
 static_assert(G::atom::N % ((SG_BSWZ_MASK + 1) << SG_BSWZ_SHIFT) == 0, "swizzle varies across a lane's rows");
 static_assert(SG_BSWZ_MASK == 0 || !SG_TB, "the B swizzle is for the layouts with k contiguous in B");
+
+// A^T-tile chunk swizzle of row m, the same scheme: a lane reads rows
+// wm * SM + r * WT0 + i (SM = atom M * WT0, i < WT0 the atom), which share
+// one swizzle when SHIFT >= log2(WT0) and SM is a multiple of
+// (MASK + 1) << SHIFT.
+__device__ __forceinline__ constexpr int aswz(int m) { return (m >> SG_ASWZ_SHIFT) & SG_ASWZ_MASK; }
+static_assert(SG_ASWZ_MASK == 0 || (SG_ASWZ_MASK & (SG_ASWZ_MASK + 1)) == 0, "swizzle mask is 2^b - 1");
+static_assert((SG_DK / 4) % (SG_ASWZ_MASK + 1) == 0, "swizzle leaves the A^T row");
+static_assert(SG_ASWZ_MASK == 0 || ((1 << SG_ASWZ_SHIFT) >= SG_WT0 &&
+                                    (G::atom::M * SG_WT0) % ((SG_ASWZ_MASK + 1) << SG_ASWZ_SHIFT) == 0),
+              "swizzle varies across a lane's rows");
+static_assert(SG_ASWZ_MASK == 0 || SG_TA, "the A swizzle is for the layout with k contiguous in A^T");
 
 // Reads WT0 consecutive floats (the A operands of the WT0 interleaved atoms).
 template <int W> __device__ __forceinline__ void lds_read_row(const float* p, float (&out)[W]) {
@@ -449,17 +469,21 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const float* a_tile = TA ? a + (size_t)row0 * lda : a + row0;
     const float* b_tile = TB ? b + col0 : b + (size_t)col0 * ldb;
     // Chunk ch of a K tile -> (c0, c1), its float4 position along the
-    // operand's contiguous dimension and across it.  Along-row chunks (A, B)
-    // go contiguous dimension first.  The transposed operands' chunks are
+    // operand's contiguous dimension and across it.  Chunks that lie along an
+    // LDS row (A, A^T, B) go contiguous dimension first (A^T at depth 16 with
+    // its rows reordered, below).  B^T's chunks are
     // scattered with four ds_write_b32 down LDS columns, so their order sets
-    // the banks 32 lanes hit at once: A^T takes pairs of k chunks, then m (32
-    // rows of m at one k pair); B^T takes 16 k, then n chunks (16 columns of
-    // k at two row groups four rows apart).  Both keep 32 or 64 contiguous
-    // bytes per lane group in global memory.
+    // the banks 32 lanes hit at once: 16 k, then n chunks (16 columns of k at
+    // two row groups four rows apart), which keeps 64 contiguous bytes per
+    // lane group in global memory.
     auto a_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
-        if constexpr (TA && A_C0 % 2 == 0) {
-            c0 = (ch & 1) + 2 * ((ch >> 1) / MT0);
-            c1 = (ch >> 1) % MT0;
+        if constexpr (TA && A_C0 == 4) {
+            // an 8-lane write cycle covers two A^T rows: take them four rows
+            // apart (row order 0, 4, 1, 5, 2, 6, 3, 7 in each group of eight),
+            // whose banks a 4- or 12-float pad keeps apart
+            const int j = ch >> 2;
+            c0 = ch & 3;
+            c1 = (j & ~7) | ((j & 1) << 2) | ((j >> 1) & 3);
         } else {
             c0 = ch % A_C0;
             c1 = ch / A_C0;
@@ -491,7 +515,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         } else {              // c0: k / 4, c1: m
             const uint32_t r = row0 + (uint32_t)c1 < m ? (uint32_t)c1 : 0u;
             a_off[i] = ((uint32_t)(c0 * 4) + r * lda) * 4u;
-            a_lds[i] = (c0 * 4) * G::A_LD + c1;
+            a_lds[i] = c1 * G::A_LD + (c0 ^ sg::aswz(c1)) * 4;
         }
     }
 #pragma unroll
@@ -671,12 +695,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 #pragma unroll
         for (int i = 0; i < G::LA; ++i)
             if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS) {
-                if constexpr (!TA) {
-                    *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[set][i];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) s[a_lds[i] + e * G::A_LD] = ra[set][i][e];
-                }
+                *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[set][i];  // a row of A or of A^T
             }
 #pragma unroll
         for (int i = 0; i < G::LB; ++i)
@@ -693,7 +712,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // ---- LDS -> MFMA operand addresses ----
     const int r = lane % AT::M;  // row (A) / column (B) inside the atom
     const int g = lane / AT::M;  // k group
-    const int a_rd = g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
+    // A: row k = g * KPL + ..., WT0 consecutive m (the interleaved atoms);
+    // A^T: rows m = wm * SM + r * WT0 + i, KPL consecutive k each
+    const int a_rd = TA ? (wm * (AT::M * WT0) + r * WT0) * G::A_LD + (SG_ASWZ_MASK ? 0 : g * KPL)
+                        : g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
+    const int a_fr = sg::aswz(wm * (AT::M * WT0) + r * WT0);  // the swizzle of every A^T row this lane reads
     const int b_rd = G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + (SG_BSWZ_MASK ? 0 : g * KPL);
     const int b_fr = sg::bswz(r);  // the swizzle of every B row this lane reads
 
@@ -712,8 +735,25 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         float b[WT1][KPL];
     };
     auto load_frag = [&](const float* s, int kb, Frag& f) __attribute__((always_inline)) {
+        if constexpr (!TA) {
 #pragma unroll
-        for (int j = 0; j < KPL; ++j) lds_read_row<WT0>(s + a_rd + (kb * KB + j) * G::A_LD, f.a[j]);
+            for (int j = 0; j < KPL; ++j) lds_read_row<WT0>(s + a_rd + (kb * KB + j) * G::A_LD, f.a[j]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < WT0; ++i) {
+                const float* p;
+                if constexpr (SG_ASWZ_MASK == 0) {
+                    p = s + a_rd + i * G::A_LD + kb * KB;
+                } else {
+                    const int kc = g * KPL + kb * KB;  // first k of the read, inside one chunk
+                    p = s + a_rd + i * G::A_LD + ((((kc >> 2) ^ a_fr) << 2) | (kc & 3));
+                }
+                float tmp[KPL];
+                lds_read_row<KPL>(p, tmp);
+#pragma unroll
+                for (int j = 0; j < KPL; ++j) f.a[j][i] = tmp[j];
+            }
+        }
 #pragma unroll
         for (int jn = 0; jn < WT1; ++jn) {
             const float* p;

@@ -266,7 +266,9 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
     lane, write, count) -- the address formulas of csrc/sgemm_gfx950.hip: the
     tile writes of every wave, and each wave's operand reads (the waves' reads
     differ by uniform offsets, so wave 0's pattern stands for all, counted
-    once per wave).  ``b_swizzle`` is the B-tile chunk swizzle (shift, mask)."""
+    once per wave).  ``b_swizzle`` is the chunk swizzle (shift, mask) of the
+    operand's k-contiguous rows: B's, or A^T's (whose tile is [MT0][DK + pad],
+    k contiguous, where A's is [DK][MT0 + pad])."""
     am, an, _, ak = mfma
     mt0 = am * wave_group[0] * wave_tiling[0]
     mt1 = an * wave_group[1] * wave_tiling[1]
@@ -290,26 +292,37 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
     def rows_first(per_row):  # chunk -> (position along the row, row): the along-row operands
         return lambda ch: (ch % per_row, ch // per_row)
 
-    if operand == "a":
+    def chunk(row, c):  # the chunk swizzle of a k-contiguous row (B, A^T)
+        return c ^ ((row >> shift) & mask)
+
+    if operand == "a" and not trans_a:
         lda = mt0 + pad
-        if not trans_a:  # float4 along m into row k
-            writes(mt0 * depth_k // 4, rows_first(mt0 // 4),
-                   lambda cc: [([c1 * lda * 4 + c0 * 16 for c0, c1 in cc], 16)])
-        else:  # float4 along k scattered down column m: four dword writes, k-chunk pairs then m
-            a_c0 = depth_k // 4
-            order = ((lambda ch: ((ch & 1) + 2 * ((ch >> 1) // mt0), (ch >> 1) % mt0)) if a_c0 % 2 == 0
-                     else rows_first(a_c0))
-            writes(mt0 * depth_k // 4, order,
-                   lambda cc: [([((c0 * 4 + e) * lda + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
+        # float4 along m into row k
+        writes(mt0 * depth_k // 4, rows_first(mt0 // 4), lambda cc: [([c1 * lda * 4 + c0 * 16 for c0, c1 in cc], 16)])
         width = 4 * wave_tiling[0]
         reads = [((l // am) * kpl * lda + (l % am) * wave_tiling[0]) * 4 for l in range(64)]
         for part in range(max(1, width // 16)):  # 8 floats: two 16-byte reads
             out.append(("read", 0, [x + 16 * part for x in reads], min(width, 16), False, waves * nkb * kpl))
         return out
+    if operand == "a":
+        # A^T: rows of m with k contiguous, chunk swizzled like B; a lane of
+        # atom i reads row r * WT0 + i (the interleaved atoms), KPL k at once
+        lda = depth_k + pad
+        wt0 = wave_tiling[0]
+        # at depth 16 an 8-lane write cycle covers two rows: they are taken
+        # four rows apart (order 0, 4, 1, 5, 2, 6, 3, 7 in each group of eight)
+        order = ((lambda ch: (ch & 3, ((ch >> 2) & ~7) | (((ch >> 2) & 1) << 2) | (((ch >> 2) >> 1) & 3)))
+                 if depth_k // 4 == 4 else rows_first(depth_k // 4))
+        writes(mt0 * depth_k // 4, order, lambda cc: [([(c1 * lda + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
+        for kb in range(nkb):
+            for i in range(wt0):
+                reads = []
+                for l in range(64):
+                    row, kc = (l % am) * wt0 + i, (l // am) * kpl + kb * kb_len
+                    reads.append((row * lda + chunk(row, kc >> 2) * 4 + (kc & 3)) * 4)
+                out.append(("read", 0, reads, 4 * kpl, False, waves))
+        return out
     ldb = depth_k + pad
-
-    def chunk(n, c):
-        return c ^ ((n >> shift) & mask)
 
     if not trans_b:  # float4 along k into row n, chunk swizzled
         writes(mt1 * depth_k // 4, rows_first(depth_k // 4),
@@ -378,27 +391,39 @@ def lds_tile_cycles(accesses) -> int:
 
 @functools.lru_cache(maxsize=None)
 def _lds_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int], depth_k: int,
-                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int]:
-    """(pad A, pad B, B swizzle shift, B swizzle mask) with the fewest LDS
-    cycles per K tile (lds_tile_cycles); ties go to the smaller pad, then to
-    no swizzle.  Swizzles are tried for B when k is contiguous in it: masks
-    whose XOR stays inside a row's depth_k / 4 chunks and shifts that leave
-    every row a lane reads (atom-N apart) with one swizzle."""
+                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int, int, int]:
+    """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
+    A^T swizzle mask) with the fewest LDS cycles per K tile
+    (lds_tile_cycles); ties go to the smaller pad, then to no swizzle.
+    Swizzles are tried for the operands whose tile rows are k contiguous (B,
+    A^T): masks whose XOR stays inside a row's depth_k / 4 chunks and shifts
+    that give every row a lane reads one swizzle (B rows atom-N apart; A^T
+    rows r * WT0 + i of the interleaved atoms, atom-M * WT0 apart)."""
     geo = (mfma, wave_group, wave_tiling, depth_k, trans_a, trans_b)
 
     def cost(operand, pad, swz=(0, 0)):
         return lds_tile_cycles(lds_tile_accesses(*geo, operand, pad, swz))
 
-    pad_a = min(LDS_PADS, key=lambda p: (cost("a", p), p))
-    swizzles = [(0, 0)]
+    def best(operand, swizzles):
+        return min(((p, sw) for p in LDS_PADS for sw in swizzles),
+                   key=lambda x: (cost(operand, x[0], x[1]), x[0], x[1][1], x[1][0]))
+
+    a_swizzles = [(0, 0)]
+    if trans_a:
+        wt0, rows = wave_tiling[0], mfma[0] * wave_tiling[0]
+        for mask in (1, 3, 7, 15):
+            for shift in range(8):
+                if (depth_k // 4) % (mask + 1) == 0 and (1 << shift) >= wt0 and rows % ((mask + 1) << shift) == 0:
+                    a_swizzles.append((shift, mask))
+    b_swizzles = [(0, 0)]
     if not trans_b:
         for mask in (1, 3, 7, 15):
             for shift in range(5):
                 if (depth_k // 4) % (mask + 1) == 0 and mfma[1] % ((mask + 1) << shift) == 0:
-                    swizzles.append((shift, mask))
-    pad_b, swz = min(((p, sw) for p in LDS_PADS for sw in swizzles),
-                     key=lambda x: (cost("b", x[0], x[1]), x[0], x[1][1], x[1][0]))
-    return pad_a, pad_b, swz[0], swz[1]
+                    b_swizzles.append((shift, mask))
+    pad_a, a_swz = best("a", a_swizzles)
+    pad_b, b_swz = best("b", b_swizzles)
+    return pad_a, pad_b, b_swz[0], b_swz[1], a_swz[0], a_swz[1]
 
 
 class GemmSolutionConfig:
@@ -517,14 +542,15 @@ class GemmSolutionConfig:
 
     # ------------------------------------------------------------------- LDS
     @property
-    def lds_layout(self) -> Tuple[int, int, int, int]:
-        """(pad A, pad B, B swizzle shift, B swizzle mask): see _lds_layout."""
+    def lds_layout(self) -> Tuple[int, int, int, int, int, int]:
+        """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
+        A^T swizzle mask): see _lds_layout."""
         return _lds_layout(tuple(self.mfma), tuple(self.wave_group), tuple(self.wave_tiling), self.depth_k,
                            self.trans_a, self.trans_b)
 
     @property
     def lds_pad_bytes(self) -> Tuple[int, int]:
-        pad_a, pad_b, _, _ = self.lds_layout
+        pad_a, pad_b = self.lds_layout[:2]
         return pad_a * datatype_size(self.a_type), pad_b * datatype_size(self.b_type)
 
     @property
@@ -533,17 +559,26 @@ class GemmSolutionConfig:
         return self.lds_layout[2], self.lds_layout[3]
 
     @property
-    def lds_offset_bytes(self) -> Tuple[int, int]:
+    def lds_a_swizzle(self) -> Tuple[int, int]:
+        """(shift, mask) of the A^T-tile chunk swizzle (mask 0: none)."""
+        return self.lds_layout[4], self.lds_layout[5]
+
+    def _lds_a_stage_bytes(self) -> int:
         pad_a = self.lds_pad_bytes[0] // datatype_size(self.a_type)
-        return 0, (self.tile_size[0] + pad_a) * self.depth_k * datatype_size(self.a_type)
+        if self.trans_a:  # [MT0][DK + padA]
+            return self.tile_size[0] * (self.depth_k + pad_a) * datatype_size(self.a_type)
+        return (self.tile_size[0] + pad_a) * self.depth_k * datatype_size(self.a_type)  # [DK][MT0 + padA]
+
+    @property
+    def lds_offset_bytes(self) -> Tuple[int, int]:
+        return 0, self._lds_a_stage_bytes()
 
     @property
     def lds_swap_offset_bytes(self) -> int:
-        """Bytes of one LDS stage: A [DK][MT0 + padA] then B [MT1][DK + padB]."""
-        pad_a = self.lds_pad_bytes[0] // datatype_size(self.a_type)
+        """Bytes of one LDS stage: A [DK][MT0 + padA] (A^T: [MT0][DK + padA])
+        then B [MT1][DK + padB]."""
         pad_b = self.lds_pad_bytes[1] // datatype_size(self.b_type)
-        return ((self.tile_size[0] + pad_a) * self.depth_k * datatype_size(self.a_type)
-                + self.tile_size[1] * (self.depth_k + pad_b) * datatype_size(self.b_type))
+        return self._lds_a_stage_bytes() + self.tile_size[1] * (self.depth_k + pad_b) * datatype_size(self.b_type)
 
     @property
     def lds_usage_bytes(self) -> int:
@@ -694,6 +729,8 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_PAD_B": pad_b,
         "SG_BSWZ_SHIFT": config.lds_b_swizzle[0],
         "SG_BSWZ_MASK": config.lds_b_swizzle[1],
+        "SG_ASWZ_SHIFT": config.lds_a_swizzle[0],
+        "SG_ASWZ_MASK": config.lds_a_swizzle[1],
         "SG_KERNEL_NAME": name,
     }
 

@@ -92,9 +92,9 @@ def kernel_layouts(name: str):
     """(label, operand, pad, swizzle) of the layouts measured for an instance:
     each pad without a swizzle, and the generator's choice."""
     cfg, _ = catalog.SOLUTIONS[name]
-    pad_a, pad_b, shift, mask = cfg.lds_layout
+    pad_a, pad_b, shift, mask, a_shift, a_mask = cfg.lds_layout
     out = [(f"pad{p}", op, p, (0, 0)) for op in ("a", "b") for p in PADS]
-    out += [("chosen", "a", pad_a, (0, 0)), ("chosen", "b", pad_b, (shift, mask))]
+    out += [("chosen", "a", pad_a, (a_shift, a_mask)), ("chosen", "b", pad_b, (shift, mask))]
     return out
 
 

@@ -187,15 +187,16 @@ def test_committed_lds_measurements_match_the_model():
 @pytest.mark.parametrize("name", ["mt256x256_a32_wg2x2_dk16_s3_nt", "mt256x256_a32_wg2x2_dk16_s3_tt",
                                   "mt256x256_a32_wg2x2_dk16_s3_tn", "mt32x32_a32_wg1x1_dk16_tt"])
 def test_transposed_scatter_is_conflict_free(name):
-    """A transposed operand's float4 chunks are scattered down LDS columns with
-    four ds_write_b32; with B^T's chunks taken 16 k at a time and A^T's in k
-    pairs, every write and read of these instances' chosen layouts takes one
-    cycle per lane group (B^T's first order, n chunks fastest, cost 16 cycles
-    per write group at 256 x 256: 15% of the NT kernel's speed)."""
+    """B^T's float4 chunks are scattered down LDS columns with four
+    ds_write_b32, taken 16 k at a time; A^T's tile is stored k contiguous, as
+    B's is, with its own chunk swizzle.  Every write and read of these
+    instances' chosen layouts takes one cycle per lane group (B^T's first
+    order, n chunks fastest, cost 16 cycles per write group at 256 x 256: 15%
+    of the NT kernel's speed)."""
     c, _ = catalog.SOLUTIONS[name]
-    pa, pb, sh, mk = c.lds_layout
+    pa, pb, sh, mk, ash, amk = c.lds_layout
     geo = (c.mfma, c.wave_group, c.wave_tiling, c.depth_k, c.trans_a, c.trans_b)
-    for operand, pad, swz in (("a", pa, (0, 0)), ("b", pb, (sh, mk))):
+    for operand, pad, swz in (("a", pa, (ash, amk)), ("b", pb, (sh, mk))):
         for _, _, addrs, width, write, _ in g.lds_tile_accesses(*geo, operand, pad, swz):
             groups = len({g.lds_lane_cycle(l, width, write) for l in range(64)})
             assert g.lds_access_cycles(addrs, width, write) == groups, (operand, width, write)
@@ -222,7 +223,7 @@ def test_chosen_b_layout_is_conflict_free(name):
     rows that suit the b128 reads, stride = 4 mod 8 floats, put the two rows of
     a b128 write octet on the same banks)."""
     c, _ = catalog.SOLUTIONS[name]
-    pa, pb, sh, mk = c.lds_layout
+    pa, pb, sh, mk, _, _ = c.lds_layout
     geo = (c.mfma, c.wave_group, c.wave_tiling, c.depth_k, c.trans_a, c.trans_b)
     for operand, pad, swz in (("b", pb, (sh, mk)), ("a", pa, (0, 0))):
         for _, _, addrs, width, write, _ in g.lds_tile_accesses(*geo, operand, pad, swz):
