@@ -195,7 +195,7 @@ template <> struct Atom<16> {
     __device__ static __forceinline__ int row(int q, int lane) { return q + 4 * (lane >> 4); }
 };
 
-template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA>
+template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA, bool TB>
 struct Geometry {
     typedef Atom<AM> atom;
     static constexpr int NT = WG0 * WG1 * 64;
@@ -205,11 +205,13 @@ struct Geometry {
     static constexpr int KPL = (DK / atom::K >= 4) ? 4 : ((DK / atom::K >= 2) ? 2 : 1);
     static constexpr int KB = atom::K * KPL;
     // A tile: [DK][MT0 + PAD_A] (m contiguous), or for A^T [MT0][DK + PAD_A]
-    // (k contiguous, like B); B tile: [MT1][DK + PAD_B]
+    // (k contiguous, like B); B tile: [MT1][DK + PAD_B] (k contiguous), or
+    // for B^T [DK][MT1 + PAD_B] (n contiguous, like A): the tile keeps the
+    // operand's contiguous dimension, so every LDS write is a 16-byte row piece
     static constexpr int A_LD = TA ? DK + PAD_A : MT0 + PAD_A;  // LDS row stride of the A tile (floats)
-    static constexpr int B_LD = DK + PAD_B;   // LDS row stride of the B tile (floats)
+    static constexpr int B_LD = TB ? MT1 + PAD_B : DK + PAD_B;  // LDS row stride of the B tile (floats)
     static constexpr int A_STAGE = TA ? MT0 * A_LD : DK * A_LD;
-    static constexpr int B_STAGE = MT1 * B_LD;
+    static constexpr int B_STAGE = TB ? DK * B_LD : MT1 * B_LD;
     static constexpr int STAGE = A_STAGE + B_STAGE;
     static constexpr int LDS_FLOATS = NBUF * STAGE;
     // float4 chunks each thread moves per K tile
@@ -223,12 +225,13 @@ struct Geometry {
     static_assert(MT0 % 4 == 0, "MT0 must be a multiple of 4");
     static_assert(WT0 == 1 || WT0 == 2 || WT0 == 4 || WT0 == 8, "WT0 must be 1, 2, 4 or 8");
     static_assert(WT1 >= 1 && WT1 <= 8, "WT1 must be in [1, 8]");
+    static_assert(!TB || WT1 == 1 || WT1 == 2 || WT1 == 4 || WT1 == 8, "B^T reads WT1 consecutive floats");
     static_assert(PAD_A % 4 == 0 && PAD_B % 4 == 0, "LDS pads keep 16-byte rows");
     static_assert(NBUF >= 2, "at least two LDS buffers");
     static_assert(LDS_FLOATS * 4 <= 163840, "LDS tile exceeds the 160 KiB of a gfx950 CU");
 };
 
-typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0> G;
+typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0, SG_TB != 0> G;
 
 // B-tile chunk swizzle of row n (0: rows stored straight).  The XOR stays
 // inside a row when its chunk count is a multiple of MASK + 1, and a lane's
@@ -469,13 +472,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const float* a_tile = TA ? a + (size_t)row0 * lda : a + row0;
     const float* b_tile = TB ? b + col0 : b + (size_t)col0 * ldb;
     // Chunk ch of a K tile -> (c0, c1), its float4 position along the
-    // operand's contiguous dimension and across it.  Chunks that lie along an
-    // LDS row (A, A^T, B) go contiguous dimension first (A^T at depth 16 with
-    // its rows reordered, below).  B^T's chunks are
-    // scattered with four ds_write_b32 down LDS columns, so their order sets
-    // the banks 32 lanes hit at once: 16 k, then n chunks (16 columns of k at
-    // two row groups four rows apart), which keeps 64 contiguous bytes per
-    // lane group in global memory.
+    // operand's contiguous dimension and across it; every chunk lies along an
+    // LDS row, contiguous dimension first (A^T at depth 16 with its rows
+    // reordered, below).
     auto a_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
         if constexpr (TA && A_C0 == 4) {
             // an 8-lane write cycle covers two A^T rows: take them four rows
@@ -490,15 +489,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         }
     };
     auto b_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
-        if constexpr (TB) {
-            constexpr int KG = DK % 16 == 0 ? 16 : DK;
-            const int rest = ch / KG;
-            c0 = rest % B_C0;
-            c1 = ch % KG + KG * (rest / B_C0);
-        } else {
-            c0 = ch % B_C0;
-            c1 = ch / B_C0;
-        }
+        c0 = ch % B_C0;
+        c1 = ch / B_C0;
     };
     uint32_t a_off[G::LA], b_off[G::LB];  // bytes from the K tile's first element
     int a_lds[G::LA], b_lds[G::LB];
@@ -531,7 +523,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         } else {              // c0: n / 4, c1: k
             const uint32_t cc = col0 + (uint32_t)(c0 * 4) < n ? (uint32_t)(c0 * 4) : 0u;
             b_off[i] = (cc + (uint32_t)c1 * ldb) * 4u;
-            b_lds[i] = G::A_STAGE + (c0 * 4) * G::B_LD + c1;
+            b_lds[i] = G::A_STAGE + c1 * G::B_LD + c0 * 4;
         }
     }
     // Bytes one K tile of each operand spans from its first element: DK
@@ -700,12 +692,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
 #pragma unroll
         for (int i = 0; i < G::LB; ++i)
             if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS) {
-                if constexpr (!TB) {
-                    *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[set][i];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) s[b_lds[i] + e * G::B_LD] = rb[set][i][e];
-                }
+                *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[set][i];  // a row of B or of B^T
             }
     };
 
@@ -717,7 +704,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const int a_rd = TA ? (wm * (AT::M * WT0) + r * WT0) * G::A_LD + (SG_ASWZ_MASK ? 0 : g * KPL)
                         : g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
     const int a_fr = sg::aswz(wm * (AT::M * WT0) + r * WT0);  // the swizzle of every A^T row this lane reads
-    const int b_rd = G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + (SG_BSWZ_MASK ? 0 : g * KPL);
+    // B: rows n = wn * SN + jn * AN + r, KPL consecutive k each; B^T: row k =
+    // g * KPL + ..., WT1 consecutive n (the interleaved atoms: column r of
+    // atom jn is tile column r * WT1 + jn, which the epilogue follows)
+    const int b_rd = TB ? G::A_STAGE + g * KPL * G::B_LD + wn * (AT::N * WT1) + r * WT1
+                        : G::A_STAGE + (wn * (AT::N * WT1) + r) * G::B_LD + (SG_BSWZ_MASK ? 0 : g * KPL);
     const int b_fr = sg::bswz(r);  // the swizzle of every B row this lane reads
 
     acc_t acc[WT0][WT1];
@@ -754,19 +745,29 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 for (int j = 0; j < KPL; ++j) f.a[j][i] = tmp[j];
             }
         }
+        if constexpr (TB) {
 #pragma unroll
-        for (int jn = 0; jn < WT1; ++jn) {
-            const float* p;
-            if constexpr (SG_BSWZ_MASK == 0) {
-                p = s + b_rd + jn * AT::N * G::B_LD + kb * KB;
-            } else {
-                const int kc = g * KPL + kb * KB;  // first k of the read, inside one chunk
-                p = s + b_rd + jn * AT::N * G::B_LD + ((((kc >> 2) ^ b_fr) << 2) | (kc & 3));
+            for (int j = 0; j < KPL; ++j) {
+                float tmp[WT1];
+                lds_read_row<WT1>(s + b_rd + (kb * KB + j) * G::B_LD, tmp);
+#pragma unroll
+                for (int jn = 0; jn < WT1; ++jn) f.b[jn][j] = tmp[jn];
             }
-            float tmp[KPL];
-            lds_read_row<KPL>(p, tmp);
+        } else {
 #pragma unroll
-            for (int j = 0; j < KPL; ++j) f.b[jn][j] = tmp[j];
+            for (int jn = 0; jn < WT1; ++jn) {
+                const float* p;
+                if constexpr (SG_BSWZ_MASK == 0) {
+                    p = s + b_rd + jn * AT::N * G::B_LD + kb * KB;
+                } else {
+                    const int kc = g * KPL + kb * KB;  // first k of the read, inside one chunk
+                    p = s + b_rd + jn * AT::N * G::B_LD + ((((kc >> 2) ^ b_fr) << 2) | (kc & 3));
+                }
+                float tmp[KPL];
+                lds_read_row<KPL>(p, tmp);
+#pragma unroll
+                for (int j = 0; j < KPL; ++j) f.b[jn][j] = tmp[j];
+            }
         }
     };
     auto mfma_frag = [&](const Frag& f) __attribute__((always_inline)) {
@@ -977,6 +978,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // ---- epilogue: D = alpha * acc + beta * C ----
     const int wrow = row0 + wm * (AT::M * WT0);
     const int wcol = col0 + wn * (AT::N * WT1);
+    // column (inside the wave's sub-tile) of column c of atom group jn: the
+    // groups side by side, or for B^T interleaved (the order of its reads)
+    auto sub_col = [](int jn, int c) __attribute__((always_inline)) {
+        return TB ? c * WT1 + jn : jn * AT::N + c;
+    };
     // Whole tiles go through LDS: the accumulators of one MFMA column group
     // (atom_n columns of the wave's SM-row sub-tile) are scattered into a
     // column-major LDS chunk, then read back as float4 runs down each column,
@@ -1057,7 +1063,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                 static_assert(E_PER_LANE % EB == 0, "whole batches of runs");
                 auto run_off = [&](int p, uint32_t ld) __attribute__((always_inline)) {
                     const int idx = p * 64 + lane;
-                    return ((uint32_t)(jn * AT::N + idx / E_RUNS) * ld + (uint32_t)((idx % E_RUNS) * 4)) * 4u;
+                    return ((uint32_t)sub_col(jn, idx / E_RUNS) * ld + (uint32_t)((idx % E_RUNS) * 4)) * 4u;
                 };
 #pragma unroll
                 for (int p0 = 0; p0 < E_PER_LANE; p0 += EB) {
@@ -1093,7 +1099,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         for (int b = 0; b < EB; ++b) {
                             const int idx = (p0 + b) * 64 + lane;
                             const uint32_t row = (uint32_t)wrow + (uint32_t)((idx % E_RUNS) * 4);
-                            const uint32_t col = (uint32_t)wcol + (uint32_t)(jn * AT::N + idx / E_RUNS);
+                            const uint32_t col = (uint32_t)wcol + (uint32_t)sub_col(jn, idx / E_RUNS);
                             const uint32_t off = run_off(p0 + b, ldd);
                             if (col < n && row < m) {
                                 if (row + 4u <= m) {
@@ -1130,7 +1136,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                        ((reinterpret_cast<uintptr_t>(c) | reinterpret_cast<uintptr_t>(d)) & 15u) == 0;
 #pragma unroll
     for (int jn = 0; jn < WT1; ++jn) {
-        const size_t colo = (size_t)(wcol + jn * AT::N + (lane % AT::N));
+        const size_t colo = (size_t)(wcol + sub_col(jn, lane % AT::N));
 #pragma unroll
         for (int q = 0; q < AT::ACC; ++q) {
             const int rr = wrow + AT::row(q, lane) * WT0;

@@ -322,16 +322,20 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
                     reads.append((row * lda + chunk(row, kc >> 2) * 4 + (kc & 3)) * 4)
                 out.append(("read", 0, reads, 4 * kpl, False, waves))
         return out
+    if trans_b:
+        # B^T: rows of k with n contiguous (the mirror of A); a lane reads WT1
+        # consecutive n, the B operands of the interleaved atoms
+        ldb = mt1 + pad
+        writes(mt1 * depth_k // 4, rows_first(mt1 // 4), lambda cc: [([c1 * ldb * 4 + c0 * 16 for c0, c1 in cc], 16)])
+        width = 4 * wave_tiling[1]
+        reads = [((l // an) * kpl * ldb + (l % an) * wave_tiling[1]) * 4 for l in range(64)]
+        for part in range(max(1, width // 16)):
+            out.append(("read", 0, [x + 16 * part for x in reads], min(width, 16), False, waves * nkb * kpl))
+        return out
     ldb = depth_k + pad
-
-    if not trans_b:  # float4 along k into row n, chunk swizzled
-        writes(mt1 * depth_k // 4, rows_first(depth_k // 4),
-               lambda cc: [([(c1 * ldb + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
-    else:  # float4 along n scattered across rows: four dword writes, 16 k then n chunks
-        kg = 16 if depth_k % 16 == 0 else depth_k
-        b_c0 = mt1 // 4
-        writes(mt1 * depth_k // 4, lambda ch: ((ch // kg) % b_c0, ch % kg + kg * ((ch // kg) // b_c0)),
-               lambda cc: [([((c0 * 4 + e) * ldb + c1) * 4 for c0, c1 in cc], 4) for e in range(4)])
+    # float4 along k into row n, chunk swizzled
+    writes(mt1 * depth_k // 4, rows_first(depth_k // 4),
+           lambda cc: [([(c1 * ldb + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
     for kb in range(nkb):
         reads = []
         for l in range(64):
@@ -479,6 +483,9 @@ class GemmSolutionConfig:
             raise RuntimeError(f"Invalid wave tiling along M (1, 2, 4 or 8): {self.wave_tiling}")
         if not 1 <= self.wave_tiling[1] <= 8:
             raise RuntimeError(f"Invalid wave tiling along N (1..8): {self.wave_tiling}")
+        if self.trans_b and self.wave_tiling[1] not in (1, 2, 4, 8):
+            # B^T's tile is n contiguous: a lane reads its WT1 atoms' operands at once
+            raise RuntimeError(f"Invalid wave tiling along N for B^T (1, 2, 4 or 8): {self.wave_tiling}")
         if self.depth_k < 4 or self.depth_k % 4:
             raise RuntimeError(f"depth_k must be a positive multiple of 4: {self.depth_k}")
         if self.depth_k % self.k_block:
@@ -576,9 +583,13 @@ class GemmSolutionConfig:
     @property
     def lds_swap_offset_bytes(self) -> int:
         """Bytes of one LDS stage: A [DK][MT0 + padA] (A^T: [MT0][DK + padA])
-        then B [MT1][DK + padB]."""
+        then B [MT1][DK + padB] (B^T: [DK][MT1 + padB])."""
         pad_b = self.lds_pad_bytes[1] // datatype_size(self.b_type)
-        return self._lds_a_stage_bytes() + self.tile_size[1] * (self.depth_k + pad_b) * datatype_size(self.b_type)
+        if self.trans_b:
+            b = self.depth_k * (self.tile_size[1] + pad_b)
+        else:
+            b = self.tile_size[1] * (self.depth_k + pad_b)
+        return self._lds_a_stage_bytes() + b * datatype_size(self.b_type)
 
     @property
     def lds_usage_bytes(self) -> int:

@@ -187,12 +187,12 @@ def test_committed_lds_measurements_match_the_model():
 @pytest.mark.parametrize("name", ["mt256x256_a32_wg2x2_dk16_s3_nt", "mt256x256_a32_wg2x2_dk16_s3_tt",
                                   "mt256x256_a32_wg2x2_dk16_s3_tn", "mt32x32_a32_wg1x1_dk16_tt"])
 def test_transposed_scatter_is_conflict_free(name):
-    """B^T's float4 chunks are scattered down LDS columns with four
-    ds_write_b32, taken 16 k at a time; A^T's tile is stored k contiguous, as
-    B's is, with its own chunk swizzle.  Every write and read of these
-    instances' chosen layouts takes one cycle per lane group (B^T's first
-    order, n chunks fastest, cost 16 cycles per write group at 256 x 256: 15%
-    of the NT kernel's speed)."""
+    """A transposed operand's LDS tile keeps its contiguous dimension: A^T's
+    is stored k contiguous, as B's is, with its own chunk swizzle, and B^T's
+    n contiguous, as A's is, with its atoms' columns interleaved.  Every write
+    and read of these instances' chosen layouts takes one cycle per lane group
+    (the scatters they replaced, four ds_write_b32 per float4 chunk, cost NT
+    15% of its speed at 256 x 256)."""
     c, _ = catalog.SOLUTIONS[name]
     pa, pb, sh, mk, ash, amk = c.lds_layout
     geo = (c.mfma, c.wave_group, c.wave_tiling, c.depth_k, c.trans_a, c.trans_b)
