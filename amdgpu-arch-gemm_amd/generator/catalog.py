@@ -11,6 +11,7 @@ point and keeps nothing (sgemm_tuner.py:116-128).
 """
 from __future__ import annotations
 
+import copy
 import os
 from concurrent.futures import ThreadPoolExecutor
 from typing import Dict, List, Optional, Tuple
@@ -257,6 +258,43 @@ STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
     "mt128x64_a16_wg2x2_dk32_s3_occ2": 2,
     "mt128x64_a16_wg2x4_dk64": 1,
 }
+
+# Transposed twins of the time model's candidates: the same geometry and
+# knobs with trans_a / trans_b, named <candidate>_tn / _nt / _tt, for
+# select(..., trans_a, trans_b).  The transposed tiles keep each operand's
+# contiguous dimension and run at the NN speed (4096^3 on 256 x 256: NN, TN,
+# NT, TT 151.3 / 151.3 / 151.2 / 151.1 TFLOP/s), so a twin is ranked with its
+# candidate's constants -- where its LDS tile keeps as many work-groups per CU
+# as the candidate holds (A^T's padded tile can be larger than A's); twins
+# that would lose one are not built.  They carry no edge kernels (those must
+# share the layout).
+LAYOUT_SUFFIX: Dict[Tuple[bool, bool], str] = {(True, False): "_tn", (False, True): "_nt", (True, True): "_tt"}
+_CU_LDS_BYTES = 163840
+TWINS: Dict[Tuple[str, bool, bool], str] = {}
+
+
+def _add_twins() -> None:
+    for name in CANDIDATES:
+        cfg, opt = SOLUTIONS[name]
+        resident = min(_CU_LDS_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, _CU_LDS_BYTES))
+        for (ta, tb), suffix in LAYOUT_SUFFIX.items():
+            try:
+                twin_cfg = _cfg(cfg.mfma, cfg.wave_group, cfg.wave_tiling, cfg.depth_k, stages=cfg.vmem_stage,
+                                ta=ta, tb=tb)
+            except RuntimeError:
+                continue
+            if _CU_LDS_BYTES // twin_cfg.lds_usage_bytes < resident:
+                continue
+            twin = name + suffix
+            SOLUTIONS[twin] = (twin_cfg, copy.copy(opt))
+            TWINS[(name, ta, tb)] = twin
+            if name in RESIDENT_PER_CU:
+                RESIDENT_PER_CU[twin] = RESIDENT_PER_CU[name]
+            if name in STREAM_K_GROUPS_PER_CU:
+                STREAM_K_GROUPS_PER_CU[twin] = STREAM_K_GROUPS_PER_CU[name]
+
+
+_add_twins()
 # rate of the streamed tiles relative to whole tiles: interleaved runs at
 # 1792^2..4864^2 x 4096 and 3000^3 measured 0.89-0.92 of the model's whole-tile
 # rate when every tile is streamed, approaching 1 as the streamed share falls
@@ -422,12 +460,22 @@ def predicted_launch_seconds(name: str, m: int, n: int, k: int, compute_units: i
     return rounds * (loop + epilogue / occ) + epilogue * (1.0 - 1.0 / occ) + reduce
 
 
-def select(m: int, n: int, k: int) -> str:
+def select(m: int, n: int, k: int, trans_a: bool = False, trans_b: bool = False) -> str:
     """Instance for an (m, n, k) problem: the tuner's choice for a BASELINE
     shape, else the candidate with the least predicted time
-    (predicted_seconds; the larger tile among near ties)."""
+    (predicted_seconds; the larger tile among near ties).  With trans_a /
+    trans_b (op(A) = A^T, op(B) = B^T) the same choice among the candidates
+    that have a twin of that layout (TWINS), without edge strips, returns
+    the twin."""
     if m <= 0 or n <= 0:
         raise RuntimeError(f"empty problem {m}x{n}x{k}")
+    if trans_a or trans_b:
+        pick = next((nm for shape, nm in PREFERRED if shape == (m, n, k)), None)
+        if (pick, trans_a, trans_b) not in TWINS:
+            pick = min((nm for nm in CANDIDATES if (nm, trans_a, trans_b) in TWINS),
+                       key=lambda nm: (predicted_launch_seconds(nm, m, n, k),
+                                       -SOLUTIONS[nm][0].tile_size[0] * SOLUTIONS[nm][0].tile_size[1]))
+        return TWINS[(pick, trans_a, trans_b)]
     for shape, name in PREFERRED:
         if shape == (m, n, k):
             return name

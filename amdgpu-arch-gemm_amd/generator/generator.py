@@ -243,8 +243,17 @@ def lds_lane_cycle(lane: int, access_bytes: int, write: bool = False) -> int:
 def lds_access_cycles(byte_addrs: Sequence[int], access_bytes: int, write: bool = False) -> int:
     """Cycles one wave-wide LDS access takes: per cycle of lds_lane_cycle, as
     many as the most-used bank holds distinct dwords (lanes that read or write
-    the same dword share its bank cycle)."""
+    the same dword share its bank cycle).  Patterns that differ by a whole
+    number of bank rows cost the same, so each is counted once."""
     banks, _ = LDS_SERVICE[(bool(write), access_bytes)]
+    period = banks * LDS_BANK_BYTES
+    base = min(byte_addrs) // period * period
+    return _lds_access_cycles(tuple(a - base for a in byte_addrs), access_bytes, bool(write))
+
+
+@functools.lru_cache(maxsize=1 << 16)
+def _lds_access_cycles(byte_addrs: Tuple[int, ...], access_bytes: int, write: bool) -> int:
+    banks, _ = LDS_SERVICE[(write, access_bytes)]
     groups: Dict[int, List[int]] = {}
     for lane, addr in enumerate(byte_addrs):
         groups.setdefault(lds_lane_cycle(lane, access_bytes, write), []).append(addr)
@@ -394,40 +403,45 @@ def lds_tile_cycles(accesses) -> int:
 
 
 @functools.lru_cache(maxsize=None)
-def _lds_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int], depth_k: int,
-                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int, int, int]:
-    """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
-    A^T swizzle mask) with the fewest LDS cycles per K tile
-    (lds_tile_cycles); ties go to the smaller pad, then to no swizzle.
-    Swizzles are tried for the operands whose tile rows are k contiguous (B,
-    A^T): masks whose XOR stays inside a row's depth_k / 4 chunks and shifts
-    that give every row a lane reads one swizzle (B rows atom-N apart; A^T
-    rows r * WT0 + i of the interleaved atoms, atom-M * WT0 apart)."""
-    geo = (mfma, wave_group, wave_tiling, depth_k, trans_a, trans_b)
-
-    def cost(operand, pad, swz=(0, 0)):
-        return lds_tile_cycles(lds_tile_accesses(*geo, operand, pad, swz))
-
-    def best(operand, swizzles):
-        return min(((p, sw) for p in LDS_PADS for sw in swizzles),
-                   key=lambda x: (cost(operand, x[0], x[1]), x[0], x[1][1], x[1][0]))
-
-    a_swizzles = [(0, 0)]
-    if trans_a:
+def _lds_operand_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int],
+                        depth_k: int, operand: str, trans: bool) -> Tuple[int, int, int]:
+    """(pad, swizzle shift, swizzle mask) of one operand's tile with the
+    fewest LDS cycles per K tile (lds_tile_cycles); ties go to the smaller
+    pad, then to no swizzle.  Swizzles are tried where the operand's tile
+    rows are k contiguous (B, A^T): masks whose XOR stays inside a row's
+    depth_k / 4 chunks and shifts that give every row a lane reads one
+    swizzle (B rows atom-N apart; A^T rows r * WT0 + i of the interleaved
+    atoms, atom-M * WT0 apart).  An operand's tile does not depend on the
+    other operand's layout."""
+    geo = (mfma, wave_group, wave_tiling, depth_k, trans, trans)
+    swizzles = [(0, 0)]
+    if operand == "a" and trans:
         wt0, rows = wave_tiling[0], mfma[0] * wave_tiling[0]
         for mask in (1, 3, 7, 15):
             for shift in range(8):
                 if (depth_k // 4) % (mask + 1) == 0 and (1 << shift) >= wt0 and rows % ((mask + 1) << shift) == 0:
-                    a_swizzles.append((shift, mask))
-    b_swizzles = [(0, 0)]
-    if not trans_b:
+                    swizzles.append((shift, mask))
+    if operand == "b" and not trans:
         for mask in (1, 3, 7, 15):
             for shift in range(5):
                 if (depth_k // 4) % (mask + 1) == 0 and mfma[1] % ((mask + 1) << shift) == 0:
-                    b_swizzles.append((shift, mask))
-    pad_a, a_swz = best("a", a_swizzles)
-    pad_b, b_swz = best("b", b_swizzles)
-    return pad_a, pad_b, b_swz[0], b_swz[1], a_swz[0], a_swz[1]
+                    swizzles.append((shift, mask))
+
+    def cost(pad, swz):
+        return lds_tile_cycles(lds_tile_accesses(*geo, operand, pad, swz))
+
+    pad, swz = min(((p, sw) for p in LDS_PADS for sw in swizzles),
+                   key=lambda x: (cost(x[0], x[1]), x[0], x[1][1], x[1][0]))
+    return pad, swz[0], swz[1]
+
+
+def _lds_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int], depth_k: int,
+                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int, int, int]:
+    """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
+    A^T swizzle mask): each operand's _lds_operand_layout."""
+    pad_a, a_shift, a_mask = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "a", trans_a)
+    pad_b, b_shift, b_mask = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "b", trans_b)
+    return pad_a, pad_b, b_shift, b_mask, a_shift, a_mask
 
 
 class GemmSolutionConfig:

@@ -1,6 +1,6 @@
 """Headline benchmark: FP32 column-major NN SGEMM at 4096^3 on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3] [--layout nn]
 
 A step is one launch of the tuned gfx950 kernel on the BASELINE.json config
 (M = N = K = 4096, A and B uniform[-1, 1) from seed 2, C = 0, alpha = 1,
@@ -20,6 +20,10 @@ is also compared with the GPU result (normwise error, 1e-5 * sqrt(K) bar), and
 both float32 results with the float64 product of the same inputs.  A second,
 separately labelled CPU figure (cpu_baseline.parallel) runs the same loop over
 columns on up to 16 host threads (about 5 s).
+
+--layout tn / nt / tt stores A (k x m) and/or B (n x k) transposed and runs
+the instance catalog.select picks for that layout (op(A) = A^T, op(B) = B^T);
+the CPU baseline multiplies the transposed-back operands.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -166,6 +170,8 @@ def main():
     ap.add_argument("--stream-k", type=int, default=None,
                     help="stream-K mode (0 off, 1 auto, 2 forced; default: the instance's own setting)")
     ap.add_argument("--no-edge", action="store_true", help="do not attach the catalog's edge kernel")
+    ap.add_argument("--layout", default="nn", choices=["nn", "tn", "nt", "tt"],
+                    help="operand layout: t stores A (k x m) or B (n x k) transposed")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -174,15 +180,20 @@ def main():
         sys.exit(2)
 
     m, n, k, seed, dist = WORKLOADS[args.workload]
-    name = args.kernel or catalog.select(m, n, k)
+    ta, tb = args.layout[0] == "t", args.layout[1] == "t"
+    name = args.kernel or catalog.select(m, n, k, ta, tb)
     co, toml = catalog.paths(name)
     info = S.device_info()
     log(f"device: {info}")
-    log(f"workload {args.workload}: {m}x{n}x{k} seed {seed} dist {dist}; kernel {name}")
+    log(f"workload {args.workload} {args.layout}: {m}x{n}x{k} seed {seed} dist {dist}; kernel {name}")
 
-    A = S.fill_matrix(m, k, seed, 0, dist)
-    B = S.fill_matrix(k, n, seed, 1, dist)
+    A = S.fill_matrix(*((k, m) if ta else (m, k)), seed, 0, dist)
+    B = S.fill_matrix(*((n, k) if tb else (k, n)), seed, 1, dist)
     kern = S.Kernel(co, toml)
+    if (bool(kern.info.trans_a), bool(kern.info.trans_b)) != (ta, tb):
+        kern.close()
+        print(f"{name} is not a {args.layout} kernel", file=sys.stderr)
+        sys.exit(2)
     edges = []
     if name in catalog.EDGE_KERNEL and not args.no_edge:
         edges = [S.Kernel(*catalog.paths(e)) for e in catalog.EDGE_KERNEL[name]]
@@ -239,7 +250,8 @@ def main():
     alg_bytes = 4.0 * (m * k + k * n + m * n)
     traffic = read_traffic(name, args.workload)
     line = {
-        "metric": HEADLINE_METRIC if args.workload == "cfg3" else f"FP32 SGEMM TFLOP/s at {m}x{n}x{k} NN",
+        "metric": (HEADLINE_METRIC if (args.workload, args.layout) == ("cfg3", "nn")
+                   else f"FP32 SGEMM TFLOP/s at {m}x{n}x{k} {args.layout.upper()}"),
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -252,7 +264,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"sgemm_nn_colmajor_{m}x{n}x{k}",
+            "workload": f"sgemm_{args.layout}_colmajor_{m}x{n}x{k}",
             "m": m, "n": n, "k": k, "seed": seed,
             "dist": "uniform[-1,1)" if dist == S.SGEMM_DIST_UNIFORM else "normal(0,1)",
             "alpha": 1.0, "beta": 0.0,
@@ -278,7 +290,9 @@ def main():
         },
     }
     if not args.no_cpu_baseline and args.gpus == 1:
-        cpu, parity = cpu_baseline(A, B, D, m, n, k, args.cpu_seconds)
+        opA = np.asfortranarray(A.T) if ta else A
+        opB = np.asfortranarray(B.T) if tb else B
+        cpu, parity = cpu_baseline(opA, opB, D, m, n, k, args.cpu_seconds)
         line["cpu_baseline"] = cpu
         line["parity"] = parity
     else:

@@ -403,6 +403,44 @@ def test_select_prefers_tuned_and_divisible():
         catalog.select(0, 16, 16)
 
 
+def test_transposed_twins_and_select():
+    """Each twin is its candidate's geometry and knobs with the layout its
+    suffix names, holds as many work-groups per CU as the candidate (LDS and
+    the occupancy tables), and select(..., trans_a, trans_b) returns only
+    instances of the asked layout: the preferred instance's twin where it has
+    one, else the model's choice among the candidates with a twin."""
+    assert len(catalog.TWINS) >= 12
+    for (base, ta, tb), twin in catalog.TWINS.items():
+        bc, bo = catalog.SOLUTIONS[base]
+        tc, to = catalog.SOLUTIONS[twin]
+        assert twin == base + catalog.LAYOUT_SUFFIX[(ta, tb)]
+        assert (tc.trans_a, tc.trans_b) == (ta, tb) and not (bc.trans_a or bc.trans_b)
+        for attr in ("mfma", "wave_group", "wave_tiling", "depth_k", "vmem_stage", "tile_size"):
+            assert getattr(tc, attr) == getattr(bc, attr), (twin, attr)
+        assert to.to_dict() == bo.to_dict() and to is not bo
+        resident = catalog.RESIDENT_PER_CU.get(base, 1 << 20)
+        assert 163840 // tc.lds_usage_bytes >= min(163840 // bc.lds_usage_bytes, resident), twin
+        assert catalog.RESIDENT_PER_CU.get(twin) == catalog.RESIDENT_PER_CU.get(base)
+        assert catalog.STREAM_K_GROUPS_PER_CU.get(twin) == catalog.STREAM_K_GROUPS_PER_CU.get(base)
+        assert twin not in catalog.EDGE_KERNEL
+    for layout in catalog.LAYOUT_SUFFIX:
+        for shape in [s for s, _ in catalog.PREFERRED] + [(8192, 8192, 8192), (100, 70, 33), (3000, 17, 5000)]:
+            name = catalog.select(*shape, *layout)
+            cfg = catalog.SOLUTIONS[name][0]
+            assert (cfg.trans_a, cfg.trans_b) == layout, (shape, layout, name)
+        for shape, pref in catalog.PREFERRED:
+            if (pref, *layout) in catalog.TWINS:
+                assert catalog.select(*shape, *layout) == catalog.TWINS[(pref, *layout)]
+    # cfg5's eight-wave 128 x 64 instance has all three twins; 256 x 128 at
+    # depth 16 keeps its two work-groups per CU only with B^T
+    assert catalog.select(16384, 128, 4096, True, True) == "mt128x64_a16_wg2x4_dk64_tt"
+    assert catalog.select(4096, 4096, 4096, False, True) == "mt256x128_a32_wg2x2_dk16_s3_occ2_nt"
+    assert ("mt256x128_a32_wg2x2_dk16_s3_occ2", True, False) not in catalog.TWINS
+    assert catalog.select(4096, 4096, 4096, False, False) == "mt256x128_a32_wg2x2_dk16_s3_occ2"
+    with pytest.raises(RuntimeError):
+        catalog.select(16, 0, 16, True, False)
+
+
 SELECT_MEASURED = os.path.join(ROOT, "tests", "golden", "select_measured.json")
 
 

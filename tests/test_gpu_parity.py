@@ -865,6 +865,52 @@ def test_random_selected_launches(kernels, m, n, k, mode, alpha, beta):
     _check(D, oracle.cpu_gemm_mt(Af, Bf, Cf, alpha, beta, threads=16), k, name)
 
 
+def _selected_transposed_cases(count, seed):
+    """(m, n, k, trans_a, trans_b, stream-K mode or None, alpha, beta): random
+    grids as above in the three transposed layouts, plus the BASELINE shapes'
+    layouts at a shallow K (their twins, or the model's pick where the
+    preferred instance has none)."""
+    rng = np.random.default_rng(seed)
+    layouts = [(True, False), (False, True), (True, True)]
+    cases = []
+    for i in range(count):
+        m, n = (int(x) for x in rng.integers(600, 4600, size=2))
+        k = int(rng.integers(1, 320))
+        mode = [None, 2][int(rng.integers(2))]
+        cases.append((m, n, k, *layouts[i % 3], mode, float(rng.choice([1.0, -0.5])), float(rng.choice([0.0, 0.75]))))
+    for ta, tb in layouts:
+        cases += [(4096, 4096, 96, ta, tb, None, 1.0, 0.0), (16384, 128, 260, ta, tb, None, 1.0, 0.5),
+                  (8192, 8192, 24, ta, tb, 2, 1.0, 0.0)]
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,mode,alpha,beta", _selected_transposed_cases(
+    int(os.environ.get("SGEMM_SELECTED_CASES", "12")), int(os.environ.get("SGEMM_RANDOM_SEED", "2024")) + 1))
+def test_random_selected_transposed_launches(kernels, m, n, k, ta, tb, mode, alpha, beta):
+    """What a caller of catalog.select(m, n, k, trans_a, trans_b) gets: the
+    transposed twin (or model pick) on stored A^T / B^T, whole D against the
+    oracle on the transposed-back operands."""
+    name = catalog.select(m, n, k, ta, tb)
+    cfg = catalog.SOLUTIONS[name][0]
+    assert (cfg.trans_a, cfg.trans_b) == (ta, tb), name
+    Af = S.fill_matrix(*((k, m) if ta else (m, k)), 19, 0)
+    Bf = S.fill_matrix(*((n, k) if tb else (k, n)), 19, 1)
+    Cf = S.fill_matrix(m, n, 19, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer(m * n * 4)
+    with _kernel(name) as kern:
+        if mode is not None and kern.info.stream_k_groups:
+            kern.set_stream_k(mode)
+        sk = kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0
+        _say(f"selected {name} {m}x{n}x{k} ta {ta} tb {tb} stream-K tiles {sk} alpha {alpha} beta {beta}")
+        kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
+        kern.synchronize()
+    D = dD.download().reshape(n, m).T
+    opA = np.asfortranarray(Af.T) if ta else Af
+    opB = np.asfortranarray(Bf.T) if tb else Bf
+    _check(D, oracle.cpu_gemm_mt(opA, opB, Cf, alpha, beta, threads=16), k, name)
+
+
 # ----------------------------------------------------------------- runner
 def _run(cmd, timeout=300):
     _say("+ " + " ".join(cmd))
