@@ -128,6 +128,12 @@
 #ifndef SG_ASWZ_MASK
 #define SG_ASWZ_MASK 0
 #endif
+#ifndef SG_ARSW_SHIFT
+#define SG_ARSW_SHIFT 0
+#endif
+#ifndef SG_ARSW_MASK
+#define SG_ARSW_MASK 0
+#endif
 #ifndef SG_TA
 #define SG_TA 0
 #endif
@@ -254,6 +260,17 @@ static_assert(SG_ASWZ_MASK == 0 || ((1 << SG_ASWZ_SHIFT) >= SG_WT0 &&
                                     (G::atom::M * SG_WT0) % ((SG_ASWZ_MASK + 1) << SG_ASWZ_SHIFT) == 0),
               "swizzle varies across a lane's rows");
 static_assert(SG_ASWZ_MASK == 0 || SG_TA, "the A swizzle is for the layout with k contiguous in A^T");
+
+// A^T-tile row swizzle: row m is stored at row arow(m).  The XOR touches
+// only bits below SHIFT, so it is a bijection on [0, MT0).  It moves the
+// rows one LDS instruction touches (rows r * WT0 + i of the lanes of one
+// atom i, or the rows of one write cycle) onto different banks where a
+// pad would otherwise do it.  Rows a lane reads are found one by one.
+__device__ __forceinline__ constexpr int arow(int m) { return m ^ ((m >> SG_ARSW_SHIFT) & SG_ARSW_MASK); }
+static_assert(SG_ARSW_MASK == 0 || ((SG_ARSW_MASK & (SG_ARSW_MASK + 1)) == 0 && (1 << SG_ARSW_SHIFT) > SG_ARSW_MASK &&
+                                    SG_ARSW_MASK < G::MT0),
+              "the row swizzle is a bijection on the tile's rows");
+static_assert(SG_ARSW_MASK == 0 || SG_TA, "the row swizzle is for the layout with k contiguous in A^T");
 
 // Reads WT0 consecutive floats (the A operands of the WT0 interleaved atoms).
 template <int W> __device__ __forceinline__ void lds_read_row(const float* p, float (&out)[W]) {
@@ -476,10 +493,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // LDS row, contiguous dimension first (A^T at depth 16 with its rows
     // reordered, below).
     auto a_chunk = [&](int ch, int& c0, int& c1) __attribute__((always_inline)) {
-        if constexpr (TA && A_C0 == 4) {
+        if constexpr (TA && A_C0 == 4 && SG_ARSW_MASK == 0) {
             // an 8-lane write cycle covers two A^T rows: take them four rows
             // apart (row order 0, 4, 1, 5, 2, 6, 3, 7 in each group of eight),
-            // whose banks a 4- or 12-float pad keeps apart
+            // whose banks a 4- or 12-float pad keeps apart (a row swizzle
+            // keeps consecutive rows apart instead)
             const int j = ch >> 2;
             c0 = ch & 3;
             c1 = (j & ~7) | ((j & 1) << 2) | ((j >> 1) & 3);
@@ -507,7 +525,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         } else {              // c0: k / 4, c1: m
             const uint32_t r = row0 + (uint32_t)c1 < m ? (uint32_t)c1 : 0u;
             a_off[i] = ((uint32_t)(c0 * 4) + r * lda) * 4u;
-            a_lds[i] = c1 * G::A_LD + (c0 ^ sg::aswz(c1)) * 4;
+            a_lds[i] = sg::arow(c1) * G::A_LD + (c0 ^ sg::aswz(c1)) * 4;
         }
     }
 #pragma unroll
@@ -700,10 +718,15 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     const int r = lane % AT::M;  // row (A) / column (B) inside the atom
     const int g = lane / AT::M;  // k group
     // A: row k = g * KPL + ..., WT0 consecutive m (the interleaved atoms);
-    // A^T: rows m = wm * SM + r * WT0 + i, KPL consecutive k each
-    const int a_rd = TA ? (wm * (AT::M * WT0) + r * WT0) * G::A_LD + (SG_ASWZ_MASK ? 0 : g * KPL)
+    // A^T: rows m = wm * SM + r * WT0 + i, KPL consecutive k each, stored at
+    // rows arow(m): a_ri[i] is atom i's row offset from a_rd
+    const int a_row0 = wm * (AT::M * WT0) + r * WT0;
+    const int a_rd = TA ? a_row0 * G::A_LD + (SG_ASWZ_MASK ? 0 : g * KPL)
                         : g * KPL * G::A_LD + wm * (AT::M * WT0) + r * WT0;
-    const int a_fr = sg::aswz(wm * (AT::M * WT0) + r * WT0);  // the swizzle of every A^T row this lane reads
+    const int a_fr = sg::aswz(a_row0);  // the swizzle of every A^T row this lane reads
+    int a_ri[WT0];
+#pragma unroll
+    for (int i = 0; i < WT0; ++i) a_ri[i] = (sg::arow(a_row0 + i) - a_row0) * G::A_LD;
     // B: rows n = wn * SN + jn * AN + r, KPL consecutive k each; B^T: row k =
     // g * KPL + ..., WT1 consecutive n (the interleaved atoms: column r of
     // atom jn is tile column r * WT1 + jn, which the epilogue follows)
@@ -734,10 +757,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             for (int i = 0; i < WT0; ++i) {
                 const float* p;
                 if constexpr (SG_ASWZ_MASK == 0) {
-                    p = s + a_rd + i * G::A_LD + kb * KB;
+                    p = s + a_rd + a_ri[i] + kb * KB;
                 } else {
                     const int kc = g * KPL + kb * KB;  // first k of the read, inside one chunk
-                    p = s + a_rd + i * G::A_LD + ((((kc >> 2) ^ a_fr) << 2) | (kc & 3));
+                    p = s + a_rd + a_ri[i] + ((((kc >> 2) ^ a_fr) << 2) | (kc & 3));
                 }
                 float tmp[KPL];
                 lds_read_row<KPL>(p, tmp);
@@ -857,7 +880,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                             }
                             if constexpr (SG_PLR >= 3) {
                                 constexpr int NMFMA = KPL * WT0 * WT1;
-                                constexpr int NREAD = KPL * (WT0 >= 4 ? WT0 / 4 : 1) + WT1;
+                                // LDS read instructions of one block: float4 reads of
+                                // rows; rows of one or two floats pair up into one
+                                // ds_read2 (KPL rows of B^T, B_LD apart)
+                                constexpr int NREAD_A = TA ? WT0 * (KPL >= 4 ? KPL / 4 : 1)
+                                                           : KPL * (WT0 >= 4 ? WT0 / 4 : 1);
+                                constexpr int NREAD_B = TB ? (WT1 >= 4 ? KPL * (WT1 / 4) : (KPL + 1) / 2)
+                                                           : WT1 * (KPL >= 4 ? KPL / 4 : 1);
+                                constexpr int NREAD = NREAD_A + NREAD_B;
                                 constexpr int NREAD_NEXT = (NKB > 1 || NBUF >= 3) ? NREAD : 0;
                                 if (kb == 0) interleave_block<NMFMA, NREAD_NEXT, G::LA + G::LB, G::LA + G::LB>();
                                 else if (!last || NBUF >= 3) interleave_block<NMFMA, NREAD, 0, 0>();

@@ -265,12 +265,16 @@ STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
 # contiguous dimension and run at the NN speed (4096^3 on 256 x 256: NN, TN,
 # NT, TT 151.3 / 151.3 / 151.2 / 151.1 TFLOP/s), so a twin is ranked with its
 # candidate's constants -- where its LDS tile keeps as many work-groups per CU
-# as the candidate holds (A^T's padded tile can be larger than A's); twins
-# that would lose one are not built.  They carry no edge kernels (those must
-# share the layout).
+# as the candidate holds (the generator swizzles A^T's rows in place of a pad
+# to keep them); twins that would lose one are not built.  They carry no edge
+# kernels (those must share the layout).
 LAYOUT_SUFFIX: Dict[Tuple[bool, bool], str] = {(True, False): "_tn", (False, True): "_nt", (True, True): "_tt"}
 _CU_LDS_BYTES = 163840
 TWINS: Dict[Tuple[str, bool, bool], str] = {}
+# twins that are not built: the eight-wave 256 x 128 instance has 128 VGPRs
+# per lane (four waves per SIMD), and its A^T tile's row swizzle (one address
+# per atom row) spills two of them
+NO_TWIN = {("mt256x128_a32_wg4x2_dk16_s3_occ4_plr2", True, False)}
 
 
 def _add_twins() -> None:
@@ -278,6 +282,8 @@ def _add_twins() -> None:
         cfg, opt = SOLUTIONS[name]
         resident = min(_CU_LDS_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, _CU_LDS_BYTES))
         for (ta, tb), suffix in LAYOUT_SUFFIX.items():
+            if (name, ta, tb) in NO_TWIN:
+                continue
             try:
                 twin_cfg = _cfg(cfg.mfma, cfg.wave_group, cfg.wave_tiling, cfg.depth_k, stages=cfg.vmem_stage,
                                 ta=ta, tb=tb)

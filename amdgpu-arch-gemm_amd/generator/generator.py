@@ -269,7 +269,8 @@ def _lds_access_cycles(byte_addrs: Tuple[int, ...], access_bytes: int, write: bo
 
 
 def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tiling: Sequence[int], depth_k: int,
-                      trans_a: bool, trans_b: bool, operand: str, pad: int, b_swizzle: Tuple[int, int] = (0, 0)):
+                      trans_a: bool, trans_b: bool, operand: str, pad: int, b_swizzle: Tuple[int, int] = (0, 0),
+                      row_swizzle: Tuple[int, int] = (0, 0)):
     """The wave-wide LDS instructions of one work-group per K tile for one
     operand ("a" or "b") and layout, as (kind, wave, byte addresses, bytes per
     lane, write, count) -- the address formulas of csrc/sgemm_gfx950.hip: the
@@ -277,7 +278,10 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
     differ by uniform offsets, so wave 0's pattern stands for all, counted
     once per wave).  ``b_swizzle`` is the chunk swizzle (shift, mask) of the
     operand's k-contiguous rows: B's, or A^T's (whose tile is [MT0][DK + pad],
-    k contiguous, where A's is [DK][MT0 + pad])."""
+    k contiguous, where A's is [DK][MT0 + pad]).  ``row_swizzle`` (shift,
+    mask), A^T only, permutes the tile's rows: row m is stored at row
+    m ^ ((m >> shift) & mask), a bijection when shift is at least the mask's
+    bit width."""
     am, an, _, ak = mfma
     mt0 = am * wave_group[0] * wave_tiling[0]
     mt1 = an * wave_group[1] * wave_tiling[1]
@@ -318,17 +322,24 @@ def lds_tile_accesses(mfma: Sequence[int], wave_group: Sequence[int], wave_tilin
         # atom i reads row r * WT0 + i (the interleaved atoms), KPL k at once
         lda = depth_k + pad
         wt0 = wave_tiling[0]
-        # at depth 16 an 8-lane write cycle covers two rows: they are taken
-        # four rows apart (order 0, 4, 1, 5, 2, 6, 3, 7 in each group of eight)
+        row_shift, row_mask = row_swizzle
+
+        def prow(m):  # stored row of row m
+            return m ^ ((m >> row_shift) & row_mask)
+
+        # at depth 16 an 8-lane write cycle covers two rows: without a row
+        # swizzle they are taken four rows apart (order 0, 4, 1, 5, 2, 6, 3, 7
+        # in each group of eight)
         order = ((lambda ch: (ch & 3, ((ch >> 2) & ~7) | (((ch >> 2) & 1) << 2) | (((ch >> 2) >> 1) & 3)))
-                 if depth_k // 4 == 4 else rows_first(depth_k // 4))
-        writes(mt0 * depth_k // 4, order, lambda cc: [([(c1 * lda + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
+                 if depth_k // 4 == 4 and not row_mask else rows_first(depth_k // 4))
+        writes(mt0 * depth_k // 4, order,
+               lambda cc: [([(prow(c1) * lda + chunk(c1, c0) * 4) * 4 for c0, c1 in cc], 16)])
         for kb in range(nkb):
             for i in range(wt0):
                 reads = []
                 for l in range(64):
                     row, kc = (l % am) * wt0 + i, (l // am) * kpl + kb * kb_len
-                    reads.append((row * lda + chunk(row, kc >> 2) * 4 + (kc & 3)) * 4)
+                    reads.append((prow(row) * lda + chunk(row, kc >> 2) * 4 + (kc & 3)) * 4)
                 out.append(("read", 0, reads, 4 * kpl, False, waves))
         return out
     if trans_b:
@@ -402,24 +413,38 @@ def lds_tile_cycles(accesses) -> int:
     return sum(count * lds_access_cycles(addrs, width, write) for _, _, addrs, width, write, count in accesses)
 
 
+def lds_tile_min_cycles(accesses) -> int:
+    """The least LDS cycles the same instructions can take: one cycle per
+    group of lanes served together (lds_lane_cycle), that is, no bank
+    conflicts."""
+    return sum(count * len({lds_lane_cycle(lane, width, write) for lane in range(len(addrs))})
+               for _, _, addrs, width, write, count in accesses)
+
+
 @functools.lru_cache(maxsize=None)
 def _lds_operand_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int],
-                        depth_k: int, operand: str, trans: bool) -> Tuple[int, int, int]:
-    """(pad, swizzle shift, swizzle mask) of one operand's tile with the
-    fewest LDS cycles per K tile (lds_tile_cycles); ties go to the smaller
-    pad, then to no swizzle.  Swizzles are tried where the operand's tile
-    rows are k contiguous (B, A^T): masks whose XOR stays inside a row's
-    depth_k / 4 chunks and shifts that give every row a lane reads one
-    swizzle (B rows atom-N apart; A^T rows r * WT0 + i of the interleaved
-    atoms, atom-M * WT0 apart).  An operand's tile does not depend on the
-    other operand's layout."""
+                        depth_k: int, operand: str, trans: bool, rows: bool = False) -> Tuple[int, Tuple[int, ...]]:
+    """(LDS cycles, (pad, swizzle shift, swizzle mask, row swizzle shift,
+    row swizzle mask)) of one operand's tile with the fewest LDS cycles per
+    K tile (lds_tile_cycles); ties go to the smaller pad, then to the smaller
+    row swizzle, then to the smaller chunk swizzle.  Swizzles
+    are tried where the operand's tile rows are k contiguous (B, A^T): masks
+    whose XOR stays inside a row's depth_k / 4 chunks and shifts that give
+    every row a lane reads one swizzle (B rows atom-N apart; A^T rows
+    r * WT0 + i of the interleaved atoms, atom-M * WT0 apart).  With
+    ``rows``, A^T also tries row swizzles (lds_tile_accesses' row_swizzle)
+    in place of a pad: they move the rows that one instruction touches onto
+    different banks.
+    Candidates are tried in tie-break order and the search stops at the
+    first that is conflict-free (lds_tile_min_cycles).  An operand's tile
+    does not depend on the other operand's layout."""
     geo = (mfma, wave_group, wave_tiling, depth_k, trans, trans)
     swizzles = [(0, 0)]
     if operand == "a" and trans:
-        wt0, rows = wave_tiling[0], mfma[0] * wave_tiling[0]
+        wt0, sub_rows = wave_tiling[0], mfma[0] * wave_tiling[0]
         for mask in (1, 3, 7, 15):
             for shift in range(8):
-                if (depth_k // 4) % (mask + 1) == 0 and (1 << shift) >= wt0 and rows % ((mask + 1) << shift) == 0:
+                if (depth_k // 4) % (mask + 1) == 0 and (1 << shift) >= wt0 and sub_rows % ((mask + 1) << shift) == 0:
                     swizzles.append((shift, mask))
     if operand == "b" and not trans:
         for mask in (1, 3, 7, 15):
@@ -427,21 +452,49 @@ def _lds_operand_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave
                 if (depth_k // 4) % (mask + 1) == 0 and mfma[1] % ((mask + 1) << shift) == 0:
                     swizzles.append((shift, mask))
 
-    def cost(pad, swz):
-        return lds_tile_cycles(lds_tile_accesses(*geo, operand, pad, swz))
-
-    pad, swz = min(((p, sw) for p in LDS_PADS for sw in swizzles),
-                   key=lambda x: (cost(x[0], x[1]), x[0], x[1][1], x[1][0]))
-    return pad, swz[0], swz[1]
+    row_swizzles = [(0, 0)]
+    if operand == "a" and trans and rows:
+        mt0 = mfma[0] * wave_group[0] * wave_tiling[0]
+        row_swizzles += [(sh, rm) for rm in (1, 3, 7) for sh in range(rm.bit_length(), 8)
+                         if (mt0 >> sh) > 1 and rm < mt0]
+    # a row swizzle stands in for a pad: tried without one
+    order = sorted(((p, sw, rs) for p in LDS_PADS for sw in swizzles for rs in row_swizzles if p == 0 or not rs[1]),
+                   key=lambda x: (x[0], x[2][1], x[2][0], x[1][1], x[1][0]))
+    best = None
+    for p, sw, rs in order:
+        acc = lds_tile_accesses(*geo, operand, p, sw, rs)
+        c = lds_tile_cycles(acc)
+        if best is None or c < best[0]:
+            best = (c, p, sw, rs)
+        if c == lds_tile_min_cycles(acc):
+            break
+    c, pad, swz, rsw = best
+    return c, (pad, swz[0], swz[1], rsw[0], rsw[1])
 
 
 def _lds_layout(mfma: Tuple[int, ...], wave_group: Tuple[int, int], wave_tiling: Tuple[int, int], depth_k: int,
-                trans_a: bool, trans_b: bool) -> Tuple[int, int, int, int, int, int]:
+                trans_a: bool, trans_b: bool, vmem_stage: int = 1) -> Tuple[int, int, int, int, int, int, int, int]:
     """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
-    A^T swizzle mask): each operand's _lds_operand_layout."""
-    pad_a, a_shift, a_mask = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "a", trans_a)
-    pad_b, b_shift, b_mask = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "b", trans_b)
-    return pad_a, pad_b, b_shift, b_mask, a_shift, a_mask
+    A^T swizzle mask, A^T row swizzle shift, A^T row swizzle mask): each
+    operand's _lds_operand_layout.  An A^T row swizzle costs registers (a
+    lane's rows are found one by one; at 256 x 256 depth 24 they spill), so
+    it is taken only where its pad-free tile fits more work-groups in a CU's
+    LDS than the best layout without one (vmem_stage + 1 stages of both
+    tiles) and is as free of bank conflicts."""
+    _, (pad_b, b_shift, b_mask, _, _) = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "b", trans_b)
+    cyc, a = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "a", trans_a)
+    if trans_a:
+        cyc_r, a_r = _lds_operand_layout(mfma, wave_group, wave_tiling, depth_k, "a", trans_a, True)
+        mt0 = mfma[0] * wave_group[0] * wave_tiling[0]
+        mt1 = mfma[1] * wave_group[1] * wave_tiling[1]
+        b_floats = depth_k * (mt1 + pad_b) if trans_b else mt1 * (depth_k + pad_b)
+
+        def per_cu(pad_a):
+            return MAX_LDS_NUM_BYTES // ((vmem_stage + 1) * (mt0 * (depth_k + pad_a) + b_floats) * 4)
+        if cyc_r <= cyc and per_cu(a_r[0]) > per_cu(a[0]):
+            a = a_r
+    pad_a, a_shift, a_mask, r_shift, r_mask = a
+    return pad_a, pad_b, b_shift, b_mask, a_shift, a_mask, r_shift, r_mask
 
 
 class GemmSolutionConfig:
@@ -563,11 +616,12 @@ class GemmSolutionConfig:
 
     # ------------------------------------------------------------------- LDS
     @property
-    def lds_layout(self) -> Tuple[int, int, int, int, int, int]:
+    def lds_layout(self) -> Tuple[int, int, int, int, int, int, int, int]:
         """(pad A, pad B, B swizzle shift, B swizzle mask, A^T swizzle shift,
-        A^T swizzle mask): see _lds_layout."""
+        A^T swizzle mask, A^T row swizzle shift, A^T row swizzle mask): see
+        _lds_layout."""
         return _lds_layout(tuple(self.mfma), tuple(self.wave_group), tuple(self.wave_tiling), self.depth_k,
-                           self.trans_a, self.trans_b)
+                           self.trans_a, self.trans_b, self.vmem_stage)
 
     @property
     def lds_pad_bytes(self) -> Tuple[int, int]:
@@ -583,6 +637,12 @@ class GemmSolutionConfig:
     def lds_a_swizzle(self) -> Tuple[int, int]:
         """(shift, mask) of the A^T-tile chunk swizzle (mask 0: none)."""
         return self.lds_layout[4], self.lds_layout[5]
+
+    @property
+    def lds_a_row_swizzle(self) -> Tuple[int, int]:
+        """(shift, mask) of the A^T-tile row swizzle: row m is stored at row
+        m ^ ((m >> shift) & mask) (mask 0: none)."""
+        return self.lds_layout[6], self.lds_layout[7]
 
     def _lds_a_stage_bytes(self) -> int:
         pad_a = self.lds_pad_bytes[0] // datatype_size(self.a_type)
@@ -756,6 +816,8 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_BSWZ_MASK": config.lds_b_swizzle[1],
         "SG_ASWZ_SHIFT": config.lds_a_swizzle[0],
         "SG_ASWZ_MASK": config.lds_a_swizzle[1],
+        "SG_ARSW_SHIFT": config.lds_a_row_swizzle[0],
+        "SG_ARSW_MASK": config.lds_a_row_swizzle[1],
         "SG_KERNEL_NAME": name,
     }
 

@@ -58,6 +58,9 @@ INSTANCES = (
     "mt64x16_a16_wg4x1_dk64_s3",
     "mt256x256_a32_wg2x2_dk16_s3_tn",
     "mt256x256_a32_wg2x2_dk16_s3_nt",
+    "mt256x128_a32_wg2x2_dk16_s3_occ2_tn",
+    "mt256x128_a32_wg4x2_dk16_s3_occ4_plr2_tt",
+    "mt128x64_a16_wg2x4_dk64_nt",
 )
 
 Pattern = Tuple[str, str, int, List[int]]  # name, r|w, bytes per lane, 64 byte addresses
@@ -89,19 +92,20 @@ def stride_patterns() -> List[Pattern]:
 
 
 def kernel_layouts(name: str):
-    """(label, operand, pad, swizzle) of the layouts measured for an instance:
-    each pad without a swizzle, and the generator's choice."""
+    """(label, operand, pad, chunk swizzle, row swizzle) of the layouts
+    measured for an instance: each pad without a swizzle, and the generator's
+    choice."""
     cfg, _ = catalog.SOLUTIONS[name]
-    pad_a, pad_b, shift, mask, a_shift, a_mask = cfg.lds_layout
-    out = [(f"pad{p}", op, p, (0, 0)) for op in ("a", "b") for p in PADS]
-    out += [("chosen", "a", pad_a, (a_shift, a_mask)), ("chosen", "b", pad_b, (shift, mask))]
+    pad_a, pad_b, shift, mask, a_shift, a_mask, r_shift, r_mask = cfg.lds_layout
+    out = [(f"pad{p}", op, p, (0, 0), (0, 0)) for op in ("a", "b") for p in PADS]
+    out += [("chosen", "a", pad_a, (a_shift, a_mask), (r_shift, r_mask)), ("chosen", "b", pad_b, (shift, mask), (0, 0))]
     return out
 
 
-def kernel_accesses(name: str, operand: str, pad: int, swz: Tuple[int, int]):
+def kernel_accesses(name: str, operand: str, pad: int, swz: Tuple[int, int], rsw: Tuple[int, int] = (0, 0)):
     cfg, _ = catalog.SOLUTIONS[name]
     return lds_tile_accesses(cfg.mfma, cfg.wave_group, cfg.wave_tiling, cfg.depth_k, cfg.trans_a, cfg.trans_b,
-                             operand, pad, swz)
+                             operand, pad, swz, rsw)
 
 
 # staged-epilogue layouts measured per instance: (label, column pad in floats,
@@ -132,8 +136,8 @@ def kernel_patterns() -> List[Pattern]:
                 out.append((key, "w" if write else "r", width, list(addrs)))
 
     for name in INSTANCES:
-        for _, operand, pad, swz in kernel_layouts(name):
-            add(kernel_accesses(name, operand, pad, swz))
+        for _, operand, pad, swz, rsw in kernel_layouts(name):
+            add(kernel_accesses(name, operand, pad, swz, rsw))
         for _, pad, swizzle, grouped in EPILOGUE_LAYOUTS:
             add(epilogue_accesses(name, pad, swizzle, grouped))
     return out
@@ -210,15 +214,15 @@ def summarise(res: Dict[str, Tuple[float, float]], pats: List[Pattern], cmd: str
               "for B, the chunk swizzle `(shift, mask)`.", "",
               "| instance | operand | layout | measured | model | conflict-free cycles |", "|---|---|---|---|---|---|"]
     for name in INSTANCES:
-        for label, operand, pad, swz in kernel_layouts(name):
+        for label, operand, pad, swz, rsw in kernel_layouts(name):
             meas = model = base = 0.0
-            for _, _, addrs, width, write, count in kernel_accesses(name, operand, pad, swz):
+            for _, _, addrs, width, write, count in kernel_accesses(name, operand, pad, swz, rsw):
                 key = _pattern_key(addrs, width, write)
                 groups = len({lds_lane_cycle(l, width, write) for l in range(64)})
                 meas = meas + count * res[key][0] if key in res and meas is not None else None
                 model += count * (lds_access_cycles(addrs, width, write) - groups)
                 base += count * groups
-            desc = f"pad {pad}" + (f", swizzle {swz}" if swz[1] else "")
+            desc = f"pad {pad}" + (f", swizzle {swz}" if swz[1] else "") + (f", row swizzle {rsw}" if rsw[1] else "")
             shown = "n/a (beyond the probe's LDS)" if meas is None else f"{meas:.0f}"
             lines.append(f"| `{name}` | {operand.upper()} | {label}: {desc} | {shown} | {model:.0f} | {base:.0f} |")
     lines += ["", "## The staged epilogue per layout", "",

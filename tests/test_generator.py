@@ -194,10 +194,10 @@ def test_transposed_scatter_is_conflict_free(name):
     (the scatters they replaced, four ds_write_b32 per float4 chunk, cost NT
     15% of its speed at 256 x 256)."""
     c, _ = catalog.SOLUTIONS[name]
-    pa, pb, sh, mk, ash, amk = c.lds_layout
+    pa, pb, sh, mk, ash, amk, rsh, rmk = c.lds_layout
     geo = (c.mfma, c.wave_group, c.wave_tiling, c.depth_k, c.trans_a, c.trans_b)
-    for operand, pad, swz in (("a", pa, (ash, amk)), ("b", pb, (sh, mk))):
-        for _, _, addrs, width, write, _ in g.lds_tile_accesses(*geo, operand, pad, swz):
+    for operand, pad, swz, rsw in (("a", pa, (ash, amk), (rsh, rmk)), ("b", pb, (sh, mk), (0, 0))):
+        for _, _, addrs, width, write, _ in g.lds_tile_accesses(*geo, operand, pad, swz, rsw):
             groups = len({g.lds_lane_cycle(l, width, write) for l in range(64)})
             assert g.lds_access_cycles(addrs, width, write) == groups, (operand, width, write)
 
@@ -223,7 +223,7 @@ def test_chosen_b_layout_is_conflict_free(name):
     rows that suit the b128 reads, stride = 4 mod 8 floats, put the two rows of
     a b128 write octet on the same banks)."""
     c, _ = catalog.SOLUTIONS[name]
-    pa, pb, sh, mk, _, _ = c.lds_layout
+    pa, pb, sh, mk = c.lds_layout[:4]
     geo = (c.mfma, c.wave_group, c.wave_tiling, c.depth_k, c.trans_a, c.trans_b)
     for operand, pad, swz in (("b", pb, (sh, mk)), ("a", pa, (0, 0))):
         for _, _, addrs, width, write, _ in g.lds_tile_accesses(*geo, operand, pad, swz):
@@ -431,11 +431,18 @@ def test_transposed_twins_and_select():
         for shape, pref in catalog.PREFERRED:
             if (pref, *layout) in catalog.TWINS:
                 assert catalog.select(*shape, *layout) == catalog.TWINS[(pref, *layout)]
-    # cfg5's eight-wave 128 x 64 instance has all three twins; 256 x 128 at
-    # depth 16 keeps its two work-groups per CU only with B^T
-    assert catalog.select(16384, 128, 4096, True, True) == "mt128x64_a16_wg2x4_dk64_tt"
-    assert catalog.select(4096, 4096, 4096, False, True) == "mt256x128_a32_wg2x2_dk16_s3_occ2_nt"
-    assert ("mt256x128_a32_wg2x2_dk16_s3_occ2", True, False) not in catalog.TWINS
+    # every BASELINE shape's instance has its three twins (256 x 128 at depth
+    # 16 keeps its two work-groups per CU with A^T through the row swizzle)
+    # but where a twin would spill (catalog.NO_TWIN)
+    for shape, pref in catalog.PREFERRED:
+        for layout, suffix in catalog.LAYOUT_SUFFIX.items():
+            if (pref, *layout) not in catalog.NO_TWIN:
+                assert catalog.select(*shape, *layout) == pref + suffix, (shape, layout)
+            else:
+                assert (pref, *layout) not in catalog.TWINS
+    occ2 = catalog.SOLUTIONS["mt256x128_a32_wg2x2_dk16_s3_occ2_tn"][0]
+    assert occ2.lds_a_row_swizzle[1] > 0 and occ2.lds_pad_bytes[0] == 0
+    assert occ2.lds_usage_bytes == catalog.SOLUTIONS["mt256x128_a32_wg2x2_dk16_s3_occ2"][0].lds_usage_bytes
     assert catalog.select(4096, 4096, 4096, False, False) == "mt256x128_a32_wg2x2_dk16_s3_occ2"
     with pytest.raises(RuntimeError):
         catalog.select(16, 0, 16, True, False)

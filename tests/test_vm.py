@@ -345,10 +345,14 @@ def test_k_remainder_keeps_the_vector_path(name, m, n, k):
 
 
 @pytest.mark.parametrize("name", ["mt32x32_a32_wg1x1_dk16_tt", "mt16x16_a16_wg1x1_dk16_nt",
-                                  "mt64x64_a16_wg2x2_dk32_s3_tn"])
+                                  "mt64x64_a16_wg2x2_dk32_s3_tn", "mt128x64_a16_wg2x2_dk32_s3_tt"])
 @pytest.mark.parametrize("shape,pad", [((None, None, None), 0), ((35, 59, 33), 1), ((5, 3, 1), 0)])
 def test_transposed_layouts_in_vm(name, shape, pad):
-    """op(A) = A^T and/or op(B) = B^T, with guarded buffers."""
+    """op(A) = A^T and/or op(B) = B^T, with guarded buffers; the first and
+    last instances store A^T's rows swizzled (one row per lane, and four
+    atoms' rows per lane)."""
+    if name.endswith("_tt"):
+        assert catalog.SOLUTIONS[name][0].lds_a_row_swizzle[1] > 0
     prog, cfg = program(name)
     t0, t1 = cfg.tile_size
     m, n, k = (2 * t0, 2 * t1, 3 * cfg.depth_k) if shape[0] is None else shape
