@@ -266,8 +266,10 @@ STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
 # NT, TT 151.3 / 151.3 / 151.2 / 151.1 TFLOP/s), so a twin is ranked with its
 # candidate's constants -- where its LDS tile keeps as many work-groups per CU
 # as the candidate holds (the generator swizzles A^T's rows in place of a pad
-# to keep them); twins that would lose one are not built.  They carry no edge
-# kernels (those must share the layout).
+# to keep them); twins that would lose one are not built.  The edge pair has
+# twins of every layout too (<edge>_tn / _nt / _tt), and a twin carries the
+# pair of its own layout wherever its candidate carries EDGE_PAIR (attached
+# edge kernels must share the main kernel's layout).
 LAYOUT_SUFFIX: Dict[Tuple[bool, bool], str] = {(True, False): "_tn", (False, True): "_nt", (True, True): "_tt"}
 _CU_LDS_BYTES = 163840
 TWINS: Dict[Tuple[str, bool, bool], str] = {}
@@ -278,6 +280,11 @@ NO_TWIN = {("mt256x128_a32_wg4x2_dk16_s3_occ4_plr2", True, False)}
 
 
 def _add_twins() -> None:
+    for name in EDGE_PAIR:
+        cfg, opt = SOLUTIONS[name]
+        for (ta, tb), suffix in LAYOUT_SUFFIX.items():
+            SOLUTIONS[name + suffix] = (_cfg(cfg.mfma, cfg.wave_group, cfg.wave_tiling, cfg.depth_k,
+                                             stages=cfg.vmem_stage, ta=ta, tb=tb), copy.copy(opt))
     for name in CANDIDATES:
         cfg, opt = SOLUTIONS[name]
         resident = min(_CU_LDS_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, _CU_LDS_BYTES))
@@ -298,6 +305,8 @@ def _add_twins() -> None:
                 RESIDENT_PER_CU[twin] = RESIDENT_PER_CU[name]
             if name in STREAM_K_GROUPS_PER_CU:
                 STREAM_K_GROUPS_PER_CU[twin] = STREAM_K_GROUPS_PER_CU[name]
+            if EDGE_KERNEL.get(name) == EDGE_PAIR:
+                EDGE_KERNEL[twin] = tuple(e + suffix for e in EDGE_PAIR)
 
 
 _add_twins()
@@ -471,25 +480,13 @@ def select(m: int, n: int, k: int, trans_a: bool = False, trans_b: bool = False)
     shape, else the candidate with the least predicted time
     (predicted_seconds; the larger tile among near ties).  With trans_a /
     trans_b (op(A) = A^T, op(B) = B^T) the same choice among the candidates
-    that have a twin of that layout (TWINS), without edge strips, returns
-    the twin."""
+    that have a twin of that layout (TWINS) returns the twin."""
     if m <= 0 or n <= 0:
         raise RuntimeError(f"empty problem {m}x{n}x{k}")
-    if trans_a or trans_b:
-        pick = next((nm for shape, nm in PREFERRED if shape == (m, n, k)), None)
-        if (pick, trans_a, trans_b) not in TWINS:
-            pick = min((nm for nm in CANDIDATES if (nm, trans_a, trans_b) in TWINS),
-                       key=lambda nm: (predicted_launch_seconds(nm, m, n, k),
-                                       -SOLUTIONS[nm][0].tile_size[0] * SOLUTIONS[nm][0].tile_size[1]))
-        return TWINS[(pick, trans_a, trans_b)]
-    for shape, name in PREFERRED:
-        if shape == (m, n, k):
-            return name
-    best = None
-    for name in CANDIDATES:
-        cfg, _ = SOLUTIONS[name]
-        t0, t1 = cfg.tile_size
-        key = (predicted_seconds(name, m, n, k), -t0 * t1)
-        if best is None or key < best[0]:
-            best = (key, name)
-    return best[1]
+    trans = trans_a or trans_b
+    pick = next((nm for shape, nm in PREFERRED if shape == (m, n, k)), None)
+    if pick is None or (trans and (pick, trans_a, trans_b) not in TWINS):
+        names = [nm for nm in CANDIDATES if not trans or (nm, trans_a, trans_b) in TWINS]
+        pick = min(names, key=lambda nm: (predicted_seconds(nm, m, n, k),
+                                          -SOLUTIONS[nm][0].tile_size[0] * SOLUTIONS[nm][0].tile_size[1]))
+    return TWINS[(pick, trans_a, trans_b)] if trans else pick

@@ -422,7 +422,14 @@ def test_transposed_twins_and_select():
         assert 163840 // tc.lds_usage_bytes >= min(163840 // bc.lds_usage_bytes, resident), twin
         assert catalog.RESIDENT_PER_CU.get(twin) == catalog.RESIDENT_PER_CU.get(base)
         assert catalog.STREAM_K_GROUPS_PER_CU.get(twin) == catalog.STREAM_K_GROUPS_PER_CU.get(base)
-        assert twin not in catalog.EDGE_KERNEL
+        if base in catalog.EDGE_KERNEL:
+            edges = catalog.EDGE_KERNEL[twin]
+            assert edges == tuple(e + catalog.LAYOUT_SUFFIX[(ta, tb)] for e in catalog.EDGE_KERNEL[base])
+            for e, be in zip(edges, catalog.EDGE_KERNEL[base]):
+                ec, bc_ = catalog.SOLUTIONS[e][0], catalog.SOLUTIONS[be][0]
+                assert (ec.trans_a, ec.trans_b) == (ta, tb) and ec.tile_size == bc_.tile_size
+        else:
+            assert twin not in catalog.EDGE_KERNEL
     for layout in catalog.LAYOUT_SUFFIX:
         for shape in [s for s, _ in catalog.PREFERRED] + [(8192, 8192, 8192), (100, 70, 33), (3000, 17, 5000)]:
             name = catalog.select(*shape, *layout)

@@ -880,7 +880,7 @@ def _selected_transposed_cases(count, seed):
         cases.append((m, n, k, *layouts[i % 3], mode, float(rng.choice([1.0, -0.5])), float(rng.choice([0.0, 0.75]))))
     for ta, tb in layouts:
         cases += [(4096, 4096, 96, ta, tb, None, 1.0, 0.0), (16384, 128, 260, ta, tb, None, 1.0, 0.5),
-                  (8192, 8192, 24, ta, tb, 2, 1.0, 0.0)]
+                  (8192, 8192, 24, ta, tb, 2, 1.0, 0.0), (4097, 4097, 64, ta, tb, None, 1.0, 0.0)]
     return cases
 
 
@@ -888,8 +888,9 @@ def _selected_transposed_cases(count, seed):
     int(os.environ.get("SGEMM_SELECTED_CASES", "12")), int(os.environ.get("SGEMM_RANDOM_SEED", "2024")) + 1))
 def test_random_selected_transposed_launches(kernels, m, n, k, ta, tb, mode, alpha, beta):
     """What a caller of catalog.select(m, n, k, trans_a, trans_b) gets: the
-    transposed twin (or model pick) on stored A^T / B^T, whole D against the
-    oracle on the transposed-back operands."""
+    transposed twin (or model pick) with its edge kernels of the same layout
+    attached, on stored A^T / B^T, whole D against the oracle on the
+    transposed-back operands."""
     name = catalog.select(m, n, k, ta, tb)
     cfg = catalog.SOLUTIONS[name][0]
     assert (cfg.trans_a, cfg.trans_b) == (ta, tb), name
@@ -898,13 +899,21 @@ def test_random_selected_transposed_launches(kernels, m, n, k, ta, tb, mode, alp
     Cf = S.fill_matrix(m, n, 19, 2)
     dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
     dD = S.DeviceBuffer(m * n * 4)
-    with _kernel(name) as kern:
-        if mode is not None and kern.info.stream_k_groups:
-            kern.set_stream_k(mode)
-        sk = kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0
-        _say(f"selected {name} {m}x{n}x{k} ta {ta} tb {tb} stream-K tiles {sk} alpha {alpha} beta {beta}")
-        kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
-        kern.synchronize()
+    edges = [_kernel(e) for e in catalog.EDGE_KERNEL.get(name, ())]
+    try:
+        with _kernel(name) as kern:
+            if edges:
+                kern.set_edge_kernels(*edges)
+            if mode is not None and kern.info.stream_k_groups:
+                kern.set_stream_k(mode)
+            sk = kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0
+            _say(f"selected {name} {m}x{n}x{k} ta {ta} tb {tb} stream-K tiles {sk} "
+                 f"interior {kern.edge_interior(m, n, k)} alpha {alpha} beta {beta}")
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
+            kern.synchronize()
+    finally:
+        for e in edges:
+            e.close()
     D = dD.download().reshape(n, m).T
     opA = np.asfortranarray(Af.T) if ta else Af
     opB = np.asfortranarray(Bf.T) if tb else Bf
