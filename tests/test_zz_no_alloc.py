@@ -139,6 +139,10 @@ GRAPH_CASES = [
     ("mt64x64_a16_wg1x4_dk32_s3", None, None, 256, 256, 8192),
     ("mt64x64_a16_wg1x4_dk32_s3", None, 2, 1792, 1792, 256),
     ("mt256x128_a32_wg2x2_dk16_s3_occ2", catalog.EDGE_PAIR, None, 4097, 4096, 64),
+    # transposed operands: strips of the twin's own layout, and split-K on A^T
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2_tt", catalog.EDGE_KERNEL["mt256x128_a32_wg2x2_dk16_s3_occ2_tt"], None,
+     4097, 4096, 64),
+    ("mt64x64_a16_wg1x4_dk32_s3_tn", None, None, 256, 256, 8192),
 ]
 
 
@@ -161,13 +165,16 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
         plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0,
                 kern.edge_interior(m, n, k))
         _say(f"graph {main} {m}x{n}x{k}: splits, stream-K tiles, interior = {plan}")
+        cfg = catalog.SOLUTIONS[main][0]
+        sa = (k, m) if cfg.trans_a else (m, k)   # stored A and B
+        sb = (n, k) if cfg.trans_b else (k, n)
         assert plan[0] > 1 or plan[1] > 0 or plan[2] != (m, n), "the case must use the scratch or the strips"
         dA, dB, dC, dD = S.DeviceBuffer(4 * m * k), S.DeviceBuffer(4 * k * n), S.DeviceBuffer(4 * m * n), \
             S.DeviceBuffer(4 * m * n)
         kern.set_stream(stream.value)
         # one eager call first: it looks up the scratch's device address
-        dA.upload(_col(S.fill_matrix(m, k, 1, 0)))
-        dB.upload(_col(S.fill_matrix(k, n, 1, 1)))
+        dA.upload(_col(S.fill_matrix(*sa, 1, 0)))
+        dB.upload(_col(S.fill_matrix(*sb, 1, 1)))
         dC.upload(_col(S.fill_matrix(m, n, 1, 2)))
         kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
         kern.synchronize()
@@ -179,7 +186,7 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
         _ok(_hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
         for replay in range(3):
             seed = 50 + replay
-            A, B, C = S.fill_matrix(m, k, seed, 0), S.fill_matrix(k, n, seed, 1), S.fill_matrix(m, n, seed, 2)
+            A, B, C = S.fill_matrix(*sa, seed, 0), S.fill_matrix(*sb, seed, 1), S.fill_matrix(m, n, seed, 2)
             dA.upload(_col(A))
             dB.upload(_col(B))
             dC.upload(_col(C))
@@ -193,7 +200,9 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
             D_eager = dD.download().reshape(n, m).T.copy()
             _say(f"  replay {replay}: checking")
             assert np.array_equal(D_graph, D_eager), f"replay {replay} differs from the eager launch"
-            err = oracle.normwise_error(D_graph, oracle.cpu_gemm_mt(A, B, C, 1.5, -0.5, threads=16))
+            opA = np.asfortranarray(A.T) if cfg.trans_a else A
+            opB = np.asfortranarray(B.T) if cfg.trans_b else B
+            err = oracle.normwise_error(D_graph, oracle.cpu_gemm_mt(opA, opB, C, 1.5, -0.5, threads=16))
             assert err <= oracle.tolerance(k), (replay, err)
     finally:
         if exe.value:
