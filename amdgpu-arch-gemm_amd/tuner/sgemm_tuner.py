@@ -104,13 +104,17 @@ def point_key(cfg: GemmSolutionConfig, opt: GemmOptimizations) -> str:
     return (f"a{cfg.mfma[0]}_wg{cfg.wave_group[0]}x{cfg.wave_group[1]}_wt{cfg.wave_tiling[0]}x{cfg.wave_tiling[1]}"
             f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}"
             + (f"_pd{opt.pd}" if opt.pd != 1 else "") + (f"_occ{opt.occ}" if opt.occ else "")
-            + (f"_sk{opt.split_k}" if opt.split_k != 1 else ""))
+            + (f"_sk{opt.split_k}" if opt.split_k != 1 else "")
+            + ("_" + ("t" if cfg.trans_a else "n") + ("t" if cfg.trans_b else "n")
+               if cfg.trans_a or cfg.trans_b else ""))
 
 
 def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1, occ=0,
-               split_k=1) -> Optional[Point]:
+               split_k=1, trans: Tuple[bool, bool] = (False, False)) -> Optional[Point]:
+    """One candidate; ``trans`` = (trans_a, trans_b) builds it for op(A) = A^T
+    and/or op(B) = B^T (the reference's schema fields, generator.py:1007-1009)."""
     try:
-        cfg = GemmSolutionConfig(F, F, F, F, mfma, wg, wt, depth_k, False, False, vmem_stage=vmem_stage)
+        cfg = GemmSolutionConfig(F, F, F, F, mfma, wg, wt, depth_k, trans[0], trans[1], vmem_stage=vmem_stage)
         opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd, pd=pd, occ=occ,
                                 split_k=split_k)
     except RuntimeError as e:
@@ -132,13 +136,15 @@ def fits(cfg: GemmSolutionConfig, m: int, n: int, k: int) -> bool:
 
 
 def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
-                    depths: Sequence[int] = (16,), tiles: Optional[Sequence[Tuple[int, int]]] = None) -> Iterable[Point]:
+                    depths: Sequence[int] = (16,), tiles: Optional[Sequence[Tuple[int, int]]] = None,
+                    trans: Tuple[bool, bool] = (False, False)) -> Iterable[Point]:
     """Stage-1 candidates: every macro-tile x wave-group x atom geometry at the
     default code-shape knobs, once per occupancy target in ``occs`` and K
     depth in ``depths``: a geometry that only pays with two work-groups per
     CU (the 4096^3 winner, 256 x 128) or with a deeper K tile (16x16x4 atoms:
     128 x 64 runs 30% faster at depth 32 than at 16) must reach stage 2 at
-    that setting.  ``tiles`` narrows the macro-tiles to the given list."""
+    that setting.  ``tiles`` narrows the macro-tiles to the given list;
+    ``trans`` is the operands' layout."""
     if tiles is None:
         tiles = GFX950_WIDE_MACRO_TILES if wide else GFX950_MACRO_TILES
     groups = GFX950_WIDE_WAVE_GROUPS if wide else GFX950_WAVE_GROUPS
@@ -147,7 +153,7 @@ def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
             continue
         wt = (mt0 // (mfma[0] * wg[0]), mt1 // (mfma[1] * wg[1]))
         p = make_point(mfma, wg, wt, dk, knobs["vmem_stage"], knobs["wgm"], knobs["plr"], knobs["gw"],
-                       knobs["map_k_idx"], knobs["xcd"], occ=occ)
+                       knobs["map_k_idx"], knobs["xcd"], occ=occ, trans=trans)
         if p:
             yield p
 
@@ -157,21 +163,22 @@ def knob_points(cfg: GemmSolutionConfig, split_ks: Sequence[int] = (1,), occs: S
     """Stage-2 candidates of one geometry; ``split_ks`` and ``occs`` add the
     gfx950-only split-K (0 = chosen per problem) and occupancy knobs, ``gws``
     the epilogue flavour (1: staged through LDS, 0: stores straight from the
-    accumulators)."""
+    accumulators).  The layout is ``cfg``'s."""
     for dk, st, wgm, xcd, plr, pd, sk, occ, gw in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES, GFX950_WGM,
                                                           GFX950_XCD, GFX950_PLR, GFX950_PD, split_ks, occs, gws):
         if pd == 2 and plr < 2:
             continue
-        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, gw, 0, xcd, pd, occ, sk)
+        p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, gw, 0, xcd, pd, occ, sk,
+                       (cfg.trans_a, cfg.trans_b))
         if p:
             yield p
 
 
-def reference_points() -> Iterable[Point]:
+def reference_points(trans: Tuple[bool, bool] = (False, False)) -> Iterable[Point]:
     for wg, wt, mfma, dk, wgm, plr, gw, mk, st in product(
             SUPPORTED_WAVE_GROUPS, SUPPORTED_WAVE_TILINGS, SUPPORTED_MFMAS, SUPPORTED_DEPTH_K, SUPPORTED_WGM,
             SUPPORTED_PLR, SUPPORTED_GW, SUPPORTED_MAP_K_IDX, SUPPORTED_VMEM_STAGES):
-        p = make_point(mfma, wg, wt, dk, st, wgm, plr, gw, mk, 0)
+        p = make_point(mfma, wg, wt, dk, st, wgm, plr, gw, mk, 0, trans=trans)
         if p:
             yield p
 
@@ -322,7 +329,8 @@ def sweep(points: List[Point], out: str, m: int, n: int, k: int, bench, timeout:
             continue
         rec = {"key": rkey, "point": key, "shape": [m, n, k], "tile": list(cfg.tile_size), "mfma": list(cfg.mfma),
                "wave_group": list(cfg.wave_group), "wave_tiling": list(cfg.wave_tiling), "depth_k": cfg.depth_k,
-               "vmem_stage": cfg.vmem_stage, **opt.to_dict(), "source_sha": sha, "gflops": 0.0, "status": "ok"}
+               "vmem_stage": cfg.vmem_stage, "trans_a": cfg.trans_a, "trans_b": cfg.trans_b, **opt.to_dict(),
+               "source_sha": sha, "gflops": 0.0, "status": "ok"}
         co = os.path.join(point_dir(out), f"{key}.co")
         toml = os.path.join(point_dir(out), f"{key}.toml")
         if compiled.get(key, 0) != 0 or not os.path.exists(co):
@@ -452,6 +460,8 @@ def main(argv=None):
     ap.add_argument("--stage1-depths", default=",".join(str(d) for d in STAGE1_DEPTHS),
                     help="comma-separated K depths every stage-1 geometry is tried at")
     ap.add_argument("--summary", default=None, help="write a markdown summary of the sweep to this path")
+    ap.add_argument("--trans-a", action="store_true", help="op(A) = A^T: A stored k x m (lda >= k)")
+    ap.add_argument("--trans-b", action="store_true", help="op(B) = B^T: B stored n x k (ldb >= n)")
     args = ap.parse_args(argv)
     m, n, k, out = args.m, args.n, args.k, args.output_folder
     split_ks = [int(x) for x in args.split_k.split(",") if x.strip()]
@@ -466,11 +476,12 @@ def main(argv=None):
     POINTS_DIR = args.points_dir
     results_path = args.results or os.path.join(out, "results.jsonl")
 
+    trans = (args.trans_a, args.trans_b)
     if args.space == "reference":
-        stage1 = [p for p in reference_points() if fits(p[0], m, n, k)]
+        stage1 = [p for p in reference_points(trans) if fits(p[0], m, n, k)]
     else:
         stage1 = [p for p in geometry_points(DEFAULT_KNOBS, wide=args.space == "gfx950-wide", occs=occs,
-                                             depths=depths, tiles=tiles) if fits(p[0], m, n, k)]
+                                             depths=depths, tiles=tiles, trans=trans) if fits(p[0], m, n, k)]
 
     if args.compile_only:
         pts = list(stage1)
@@ -522,6 +533,7 @@ def main(argv=None):
           f"MT: {tuple(best['tile'])}, DK: {best['depth_k']}, MI: {tuple(best['mfma'])}, wg: {tuple(best['wave_group'])}, "
           f"wgm: {best['wgm']}, plr: {best['plr']}, gw: {best['gw']}, map_k_idx: {best['map_k_idx']}, "
           f"vmem_stage: {best['vmem_stage']}, xcd: {best['xcd']}, split_k: {best.get('split_k', 1)}, "
+          f"trans_a: {best.get('trans_a', False)}, trans_b: {best.get('trans_b', False)}, "
           f"occ: {best.get('occ', 0)} -> {out}/generated_gemm.co")
     if args.summary:
         write_summary(args.summary, recs, best, m, n, k, argv if argv is not None else sys.argv[1:])

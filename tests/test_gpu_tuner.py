@@ -83,3 +83,41 @@ def test_small_sweep_emits_a_validated_drop_in_pair(kernels, tmp_path):
     assert ret2.returncode == 0, log2
     assert "Gflops: " not in "\n".join(ln for ln in log2.splitlines() if not ln.startswith(("Best", "validation")))
     assert len(open(os.path.join(out, "results.jsonl")).read().splitlines()) == len(recs)
+
+
+def test_transposed_sweep_emits_a_validated_tt_pair(kernels, tmp_path):
+    """The same sweep for op(A) = A^T, op(B) = B^T (--trans-a --trans-b): the
+    emitted pair is a TT kernel, and it validates in this build's runner and
+    against the oracle on transposed storage (the reference's runner ignores
+    the layout fields, so it is not asked)."""
+    out = str(tmp_path / "tune_tt")
+    c = graft.TUNER_CHECK
+    cmd = [sys.executable, TUNER, "--m", str(c["m"]), "--n", str(c["n"]), "--k", str(c["k"]), "--bench", RUNNER,
+           "--output-folder", out, "--points-dir", graft.TUNER_CHECK_POINTS, "--in-process", "--refine", "0",
+           "--tiles", c["tiles"], "--occ", c["occ"], "--stage1-depths", c["depths"], "--warmup", "3", "--runs", "10",
+           "--jobs", "16", "--timeout", "60", "--trans-a", "--trans-b"]
+    _say("+ " + " ".join(cmd))
+    ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=600)
+    log = ret.stdout.decode(errors="replace")
+    _say(log[-2000:])
+    assert ret.returncode == 0, log
+    recs = [json.loads(x) for x in open(os.path.join(out, "results.jsonl")).read().splitlines()]
+    ok = [r for r in recs if r["status"] == "ok"]
+    assert len(ok) >= 4 and all(r["trans_a"] and r["trans_b"] and r["point"].endswith("_tt") for r in ok)
+    assert "compile" not in " ".join(r["status"] for r in recs)    # every point came prebuilt
+    best = max(ok, key=lambda r: r["gflops"])
+    assert f"validation of {best['point']}: PASS" in log
+    co, toml = os.path.join(out, "generated_gemm.co"), os.path.join(out, "generated_gemm.toml")
+    with S.Kernel(co, toml) as kern:
+        assert kern.info.trans_a and kern.info.trans_b
+    r = subprocess.run([RUNNER, co, toml, "700", "333", "515", "1", "2", "1", "3"], stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, timeout=300)
+    out_runner = r.stdout.decode()
+    _say(out_runner[-600:])
+    assert r.returncode == 0 and "validation: PASS" in out_runner and "# of mismatches: 0/" in out_runner
+    m, n, k = c["m"], c["n"], c["k"]
+    A, B, C = S.fill_matrix(k, m, 9, 0), S.fill_matrix(n, k, 9, 1), S.fill_matrix(m, n, 9, 2)
+    with S.Kernel(co, toml) as kern:
+        D, _ = kern.run(A, B, C, m, n, k, alpha=1.5, beta=-0.5)
+    ref = oracle.cpu_gemm(np.asfortranarray(A.T), np.asfortranarray(B.T), C, 1.5, -0.5)
+    assert oracle.normwise_error(D, ref) <= oracle.tolerance(k)

@@ -164,6 +164,26 @@ def test_compile_only_builds_stage1_with_split_and_occupancy_knobs(tmp_path):
     assert sum(1 for k in keys if k.endswith("_sk0")) * 2 == len(keys)
 
 
+def test_transposed_layout_flags_reach_every_point(tmp_path):
+    """--trans-a / --trans-b build every candidate for op(A) = A^T, op(B) =
+    B^T: the keys carry the layout, stage 2 keeps it and the emitted .toml
+    records it (the reference's schema fields)."""
+    out = str(tmp_path)
+    rc = T.main(["--m", "64", "--n", "64", "--k", "64", "--bench", "unused", "--output-folder", out,
+                 "--compile-only", "--jobs", "8", "--tiles", "32x32,64x64", "--trans-a", "--trans-b"])
+    assert rc == 0
+    built = sorted(f for f in os.listdir(os.path.join(out, "points")) if f.endswith(".co"))
+    assert built and all(f.endswith("_tt.co") for f in built)
+    for f in built:
+        d = g.read_toml(os.path.join(out, "points", f[:-3] + ".toml"))
+        assert d["trans_a"] is True and d["trans_b"] is True and d["scratch_bytes_per_lane"] == 0
+    cfg, _ = T.make_point((16, 16, 1, 4), (2, 2), (2, 2), 16, 2, 4, 3, 0, 0, 8, trans=(True, False))
+    keys = {T.point_key(*p) for p in T.knob_points(cfg)}
+    assert keys and all(k.endswith("_tn") for k in keys)
+    nn, _ = T.make_point((16, 16, 1, 4), (2, 2), (2, 2), 16, 2, 4, 3, 0, 0, 8)
+    assert T.point_key(nn, _).endswith("_x8")
+
+
 @pytest.mark.parametrize("name,occs,depths", [
     ("mt128x64_a16_wg2x4_dk64", (0,), (32, 64)),              # cfg5's instance
     ("mt256x128_a32_wg4x2_dk16_s3_occ4_plr2", (0, 2, 4), (16,)),  # cfg4's instance
