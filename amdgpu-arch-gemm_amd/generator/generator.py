@@ -996,10 +996,10 @@ def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimi
 
 
 # Default instance of the CLI: the configuration the gfx950 tuner selected for
-# the 4096^3 headline problem.
-def default_config() -> Tuple[GemmSolutionConfig, GemmOptimizations]:
+# the 4096^3 headline problem (in the layout trans_a / trans_b ask for).
+def default_config(trans_a: bool = False, trans_b: bool = False) -> Tuple[GemmSolutionConfig, GemmOptimizations]:
     cfg = GemmSolutionConfig(DataType.FP32, DataType.FP32, DataType.FP32, DataType.FP32,
-                             MFMA_32x32x2, (2, 2), (4, 2), 16, False, False, vmem_stage=2)
+                             MFMA_32x32x2, (2, 2), (4, 2), 16, trans_a, trans_b, vmem_stage=2)
     opt = GemmOptimizations(1, wgm=4, plr=3, gw=1, map_k_idx=0, xcd=8, occ=2)
     return cfg, opt
 
@@ -1008,8 +1008,10 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="Generate the gfx950 SGEMM code object and its .toml")
     ap.add_argument(dest="output_folder", action="store", type=str, help="Output folder")
     ap.add_argument("--arch", dest="arch", action="store", choices=list(SUPPORTED_ARCHS), default="gfx950")
+    ap.add_argument("--trans-a", action="store_true", help="op(A) = A^T: A stored k x m (lda >= k)")
+    ap.add_argument("--trans-b", action="store_true", help="op(B) = B^T: B stored n x k (ldb >= n)")
     args = ap.parse_args(argv)
-    cfg, opt = default_config()
+    cfg, opt = default_config(args.trans_a, args.trans_b)
     src = gemm(None, "generated_gemm", args.arch, cfg, opt, default_arguments())
     rc = compile("generated_gemm", src, args.arch, args.output_folder, cfg, opt, verbose=True)
     if rc == 0:

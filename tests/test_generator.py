@@ -379,6 +379,21 @@ def test_cli_default_is_the_catalog_headline_instance():
     got_cfg, got_opt = g.default_config()
     assert got_cfg.to_dict() == want_cfg.to_dict(), name
     assert got_opt.to_dict() == want_opt.to_dict(), name
+    # --trans-a / --trans-b: the same instance in that layout, the catalog's twin
+    for layout in catalog.LAYOUT_SUFFIX:
+        twin = catalog.select(4096, 4096, 4096, *layout)
+        got_cfg, got_opt = g.default_config(*layout)
+        assert got_cfg.to_dict() == catalog.SOLUTIONS[twin][0].to_dict(), twin
+        assert got_opt.to_dict() == catalog.SOLUTIONS[twin][1].to_dict(), twin
+
+
+def test_cli_writes_a_transposed_pair(tmp_path):
+    """generator.py out --trans-a --trans-b writes the TT code object and a
+    .toml that records the layout (the reference CLI has only --arch)."""
+    assert g.main([str(tmp_path), "--trans-a", "--trans-b"]) == 0
+    d = g.read_toml(str(tmp_path / "generated_gemm.toml"))
+    assert d["trans_a"] is True and d["trans_b"] is True and d["scratch_bytes_per_lane"] == 0
+    assert (tmp_path / "generated_gemm.co").stat().st_size > 0
 
 
 # ------------------------------------------------------------- catalog
