@@ -16,8 +16,8 @@ import os
 from concurrent.futures import ThreadPoolExecutor
 from typing import Dict, List, Optional, Tuple
 
-from .generator import (MAX_SPLIT_K, DataType, GemmOptimizations, GemmSolutionConfig, MFMA_16x16x4,
-                        MFMA_32x32x2, build_kernel)
+from .generator import (MAX_LDS_NUM_BYTES, MAX_SPLIT_K, DataType, GemmOptimizations, GemmSolutionConfig,
+                        MFMA_16x16x4, MFMA_32x32x2, build_kernel)
 
 PACKAGE_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 KERNEL_DIR = os.path.join(PACKAGE_ROOT, "kernels")
@@ -271,7 +271,6 @@ STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
 # pair of its own layout wherever its candidate carries EDGE_PAIR (attached
 # edge kernels must share the main kernel's layout).
 LAYOUT_SUFFIX: Dict[Tuple[bool, bool], str] = {(True, False): "_tn", (False, True): "_nt", (True, True): "_tt"}
-_CU_LDS_BYTES = 163840
 TWINS: Dict[Tuple[str, bool, bool], str] = {}
 # twins that are not built: the eight-wave 256 x 128 instance has 128 VGPRs
 # per lane (four waves per SIMD), and its A^T tile's row swizzle (one address
@@ -287,7 +286,7 @@ def _add_twins() -> None:
                                              stages=cfg.vmem_stage, ta=ta, tb=tb), copy.copy(opt))
     for name in CANDIDATES:
         cfg, opt = SOLUTIONS[name]
-        resident = min(_CU_LDS_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, _CU_LDS_BYTES))
+        resident = min(MAX_LDS_NUM_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, MAX_LDS_NUM_BYTES))
         for (ta, tb), suffix in LAYOUT_SUFFIX.items():
             if (name, ta, tb) in NO_TWIN:
                 continue
@@ -296,7 +295,7 @@ def _add_twins() -> None:
                                 ta=ta, tb=tb)
             except RuntimeError:
                 continue
-            if _CU_LDS_BYTES // twin_cfg.lds_usage_bytes < resident:
+            if MAX_LDS_NUM_BYTES // twin_cfg.lds_usage_bytes < resident:
                 continue
             twin = name + suffix
             SOLUTIONS[twin] = (twin_cfg, copy.copy(opt))
