@@ -415,9 +415,12 @@ struct Fixup {
 };
 
 // One output tile (tx, ty): the K loop over [k_first, k_first + k) of the
-// operands, the fix-up, then the epilogue.
+// operands, the fix-up, then the epilogue.  c and d may be one matrix (an
+// in-place update of C): an element of C is read only by the lane that then
+// writes that element of D, in the one epilogue that finishes its tile, so
+// neither pointer is declared restrict.
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const float* __restrict__ b,
-                                          const float* __restrict__ c, float* __restrict__ d,
+                                          const float* c, float* d,
                                           uint32_t m, uint32_t n, uint32_t k_total,
                                           uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                                           float alpha, float beta, int tx, int ty, uint32_t k_first, uint32_t k,
@@ -1206,7 +1209,7 @@ __device__ __forceinline__ void grid_tile(int bx, int by, int nwgx, int nwgy, in
 
 extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
 SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
-               const float* __restrict__ c, float* __restrict__ d,
+               const float* c, float* d,
                uint32_t m, uint32_t n, uint32_t k,
                uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY) {
@@ -1229,7 +1232,7 @@ SG_KERNEL_NAME(const float* __restrict__ a, const float* __restrict__ b,
 // overlap.
 extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
 SG_KERNEL_NAME_SPLITK(const float* __restrict__ a, const float* __restrict__ b,
-                      const float* __restrict__ c, float* __restrict__ d,
+                      const float* c, float* d,
                       uint32_t m, uint32_t n, uint32_t k,
                       uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                       float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY,
@@ -1270,7 +1273,7 @@ SG_KERNEL_NAME_SPLITK(const float* __restrict__ a, const float* __restrict__ b,
 // G zeros, left zero by the launch; launches sharing them must not overlap.
 extern "C" __global__ void __launch_bounds__(sg::G::NT) SG_OCC_ATTR
 SG_KERNEL_NAME_STREAMK(const float* __restrict__ a, const float* __restrict__ b,
-                       const float* __restrict__ c, float* __restrict__ d,
+                       const float* c, float* d,
                        uint32_t m, uint32_t n, uint32_t k,
                        uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t ldd,
                        float alpha, float beta, int32_t numWorkgroupX, int32_t numWorkgroupY,

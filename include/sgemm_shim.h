@@ -23,7 +23,8 @@
  *     with op(A) m x k and op(B) k x n; A is stored m x k (lda >= m), or
  *     k x m (lda >= k) for a kernel built with trans_a; B is stored k x n
  *     (ldb >= k), or n x k (ldb >= n) with trans_b; C and D are m x n
- *     (ldc, ldd >= m).  C is not read when beta == 0.
+ *     (ldc, ldd >= m).  C is not read when beta == 0.  dC may equal dD (with
+ *     ldc == ldd): an in-place update D = alpha * op(A) * op(B) + beta * D.
  */
 #ifndef SGEMM_SHIM_H
 #define SGEMM_SHIM_H

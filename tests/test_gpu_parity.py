@@ -920,6 +920,48 @@ def test_random_selected_transposed_launches(kernels, m, n, k, ta, tb, mode, alp
     _check(D, oracle.cpu_gemm_mt(opA, opB, Cf, alpha, beta, threads=16), k, name)
 
 
+# D = alpha * op(A) * op(B) + beta * D in place (C and D one buffer): every
+# kind of launch -- plain, transposed, split-K, stream-K, edge strips and the
+# no-alloc entry point -- against the same launch into a separate D
+IN_PLACE_CASES = [
+    ("mt64x64_a32_wg2x2_dk16", None, None, 200, 130, 96, "launch"),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2_tt", None, None, 700, 300, 80, "launch"),
+    ("mt64x64_a16_wg1x4_dk32_s3", None, None, 256, 256, 4096, "launch"),          # split-K
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 2, 1792, 1792, 256, "launch"),            # stream-K
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "edges", None, 4097, 4096, 64, "launch"),  # edge strips
+    ("mt64x64_a16_wg1x4_dk32_s3_tn", None, None, 256, 256, 4096, "launch_noalloc"),
+]
+
+
+@pytest.mark.parametrize("name,edges,mode,m,n,k,entry", IN_PLACE_CASES)
+def test_in_place_update_of_c(kernels, name, edges, mode, m, n, k, entry):
+    A, B, opA, opB = _operands(name, m, n, k, 23)
+    C = S.fill_matrix(m, n, 23, 2)
+    dA, dB = S.DeviceBuffer.from_array(A), S.DeviceBuffer.from_array(B)
+    strips = [_kernel(e) for e in catalog.EDGE_KERNEL[name]] if edges else []
+    try:
+        with _kernel(name) as kern:
+            if strips:
+                kern.set_edge_kernels(*strips)
+            if mode is not None:
+                kern.set_stream_k(mode)
+            plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0,
+                    kern.edge_interior(m, n, k))
+            _say(f"in place {name} {m}x{n}x{k} {entry}: splits, stream-K tiles, interior = {plan}")
+            dC, dD = S.DeviceBuffer.from_array(C), S.DeviceBuffer(4 * m * n)
+            getattr(kern, entry)(dA, dB, dC, dD, m, n, k, alpha=0.5, beta=-1.5)
+            dCD = S.DeviceBuffer.from_array(C)
+            getattr(kern, entry)(dA, dB, dCD, dCD, m, n, k, alpha=0.5, beta=-1.5)
+            kern.synchronize()
+    finally:
+        for e in strips:
+            e.close()
+    D_sep = dD.download().reshape(n, m).T
+    D_in = dCD.download().reshape(n, m).T
+    assert np.array_equal(D_in, D_sep), "the in-place update differs from the launch into a separate D"
+    _check(D_in, oracle.cpu_gemm_mt(opA, opB, C, 0.5, -1.5, threads=16), k, name)
+
+
 # ----------------------------------------------------------------- runner
 def _run(cmd, timeout=300):
     _say("+ " + " ".join(cmd))
