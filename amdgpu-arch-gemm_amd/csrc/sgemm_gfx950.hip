@@ -885,9 +885,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                                 constexpr int NMFMA = KPL * WT0 * WT1;
                                 // LDS read instructions of one block: float4 reads of
                                 // rows; rows of one or two floats pair up into one
-                                // ds_read2 (KPL rows of B^T, B_LD apart)
+                                // ds_read2 (KPL rows of A or of B^T, A_LD or B_LD apart)
                                 constexpr int NREAD_A = TA ? WT0 * (KPL >= 4 ? KPL / 4 : 1)
-                                                           : KPL * (WT0 >= 4 ? WT0 / 4 : 1);
+                                                           : (WT0 >= 4 ? KPL * (WT0 / 4) : (KPL + 1) / 2);
                                 constexpr int NREAD_B = TB ? (WT1 >= 4 ? KPL * (WT1 / 4) : (KPL + 1) / 2)
                                                            : WT1 * (KPL >= 4 ? KPL / 4 : 1);
                                 constexpr int NREAD = NREAD_A + NREAD_B;
