@@ -65,6 +65,11 @@ struct Part {
 SGEMM_INTERNAL int decompose(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
                              uint32_t ldc, uint32_t ldd, Part out[3]);
 
+// Looks up the device address of sgemm_launch_noalloc's static scratch on
+// device `dev` (once per device; later calls return at once).  sgemm_open
+// calls it for the handle's device, so launches never do.
+SGEMM_INTERNAL int noalloc_prepare(int dev);
+
 SGEMM_INTERNAL hipStream_t stream(const sgemm_handle* h);
 SGEMM_INTERNAL int device(const sgemm_handle* h);
 // Records `message` as the calling thread's sgemm_last_error and returns `code`.

@@ -9,7 +9,10 @@
 //
 // Host code never uses the array's name as a device address: the address of
 // each device's copy is looked up once, with that device current, through
-// hipGetSymbolAddress, and that pointer is what the kernels receive.
+// hipGetSymbolAddress, and that pointer is what the kernels receive.  The
+// lookup runs in sgemm_open (noalloc_prepare) for the handle's device, so a
+// launch -- even the first one on a device, even under graph capture -- only
+// reads the stored pointer.
 
 #include "sgemm_internal.hpp"
 
@@ -64,6 +67,11 @@ int scratch_address(int dev, void** out) {
 }
 
 }  // namespace
+
+int sgemm_internal::noalloc_prepare(int dev) {
+    void* p = nullptr;
+    return scratch_address(dev, &p);
+}
 
 extern "C" int sgemm_launch_noalloc(sgemm_handle* h, const float* dA, const float* dB, const float* dC, float* dD,
                                     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc,

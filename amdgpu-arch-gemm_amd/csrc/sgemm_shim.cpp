@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cerrno>
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstddef>
@@ -18,6 +19,7 @@
 #include <cstring>
 #include <fstream>
 #include <map>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <thread>
@@ -98,6 +100,12 @@ int parse_toml(const std::string& path, std::map<std::string, TomlValue>* out) {
         if (eq == std::string::npos) return fail(SGEMM_E_CONFIG, "%s:%d: expected key = value", path.c_str(), lineno);
         std::string key = trim(line.substr(0, eq));
         std::string val = trim(line.substr(eq + 1));
+        // bare keys only (A-Z a-z 0-9 _ -), as every key of the schema is
+        bool bare = !key.empty();
+        for (char ch : key)
+            bare = bare && ((ch >= 'A' && ch <= 'Z') || (ch >= 'a' && ch <= 'z') || (ch >= '0' && ch <= '9') ||
+                            ch == '_' || ch == '-');
+        if (!bare) return fail(SGEMM_E_CONFIG, "%s:%d: bad key", path.c_str(), lineno);
         TomlValue v;
         if (val == "true" || val == "false") {
             v.kind = TomlValue::BOOL;
@@ -139,6 +147,8 @@ int toml_int(const std::map<std::string, TomlValue>& t, const char* key, int* ou
         return SGEMM_OK;
     }
     if (it->second.kind != TomlValue::INT) return fail(SGEMM_E_CONFIG, "key '%s' must be an integer", key);
+    if (it->second.i < INT_MIN || it->second.i > INT_MAX)
+        return fail(SGEMM_E_CONFIG, "key '%s' = %lld does not fit a 32-bit integer", key, it->second.i);
     *out = (int)it->second.i;
     return SGEMM_OK;
 }
@@ -156,7 +166,12 @@ int toml_arr(const std::map<std::string, TomlValue>& t, const char* key, int* ou
     if (it == t.end()) return fail(SGEMM_E_CONFIG, "kernel config misses key '%s'", key);
     if (it->second.kind != TomlValue::INT_ARRAY || it->second.arr.size() < n)
         return fail(SGEMM_E_CONFIG, "key '%s' must be an array of %zu integers", key, n);
-    for (size_t i = 0; i < n; ++i) out[i] = (int)it->second.arr[i];
+    for (size_t i = 0; i < n; ++i) {
+        const long long v = it->second.arr[i];
+        if (v < INT_MIN || v > INT_MAX)
+            return fail(SGEMM_E_CONFIG, "key '%s': item %lld does not fit a 32-bit integer", key, v);
+        out[i] = (int)v;
+    }
     return SGEMM_OK;
 }
 
@@ -203,11 +218,19 @@ int load_config(const char* path, sgemm_kernel_info* info) {
     const bool atom32 = mf[0] == 32 && mf[1] == 32 && mf[2] == 1 && mf[3] == 2;
     const bool atom16 = mf[0] == 16 && mf[1] == 16 && mf[2] == 1 && mf[3] == 4;
     if (!atom32 && !atom16) return fail(SGEMM_E_CONFIG, "unsupported mfma atom [%d, %d, %d, %d]", mf[0], mf[1], mf[2], mf[3]);
+    // bounds far beyond any real kernel (a work-group holds at most 16 waves,
+    // a tile edge at most a few hundred rows), so that the geometry below
+    // cannot overflow
     for (int i = 0; i < 2; ++i) {
         if (info->wave_group[i] <= 0 || info->wave_tiling[i] <= 0)
             return fail(SGEMM_E_CONFIG, "wave_group and wave_tiling must be positive");
+        if (info->wave_group[i] > 16 || info->wave_tiling[i] > 64)
+            return fail(SGEMM_E_CONFIG, "wave_group [%d, %d] / wave_tiling [%d, %d] outside 1..16 / 1..64",
+                        info->wave_group[0], info->wave_group[1], info->wave_tiling[0], info->wave_tiling[1]);
     }
-    if (info->depth_k <= 0) return fail(SGEMM_E_CONFIG, "depth_k must be positive");
+    if (info->depth_k <= 0 || info->depth_k > 4096) return fail(SGEMM_E_CONFIG, "depth_k must be in 1..4096");
+    if (info->vmem_stage < 1 || info->vmem_stage > 16) return fail(SGEMM_E_CONFIG, "vmem_stage must be in 1..16");
+    if (info->lds_usage_bytes < 0) return fail(SGEMM_E_CONFIG, "lds_usage_bytes must not be negative");
     info->tile_m = mf[0] * info->wave_group[0] * info->wave_tiling[0];
     info->tile_n = mf[1] * info->wave_group[1] * info->wave_tiling[1];
     info->workitems = info->wave_group[0] * info->wave_group[1] * info->wavefront_size;
@@ -249,7 +272,7 @@ static_assert(offsetof(KernArgsSplit, ws) == 80 && offsetof(KernArgsSplit, ticke
 // K ranges a launch really uses: the configured count (or, for 0, the
 // per-problem choice documented at sgemm_set_split_k), at most one per K tile.
 uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_t m, uint32_t n, uint32_t k) {
-    const uint32_t ktiles = (k + (uint32_t)i.depth_k - 1) / (uint32_t)i.depth_k;
+    const uint64_t ktiles = ((uint64_t)k + (uint32_t)i.depth_k - 1) / (uint32_t)i.depth_k;
     uint64_t s = (uint32_t)i.split_k;
     if (s == 0) {
         // Work-groups run in rounds of one per compute unit; a work-group
@@ -259,8 +282,8 @@ uint32_t effective_splits(const sgemm_kernel_info& i, int compute_units, uint32_
         // s with the least (the smallest s among ties), keeping at least 4 K
         // tiles per range.
         constexpr uint64_t kSplitRangeOverhead = 4;
-        const uint64_t tiles = (uint64_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
-                               ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+        const uint64_t tiles = (((uint64_t)m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+                               (((uint64_t)n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
         const uint64_t cus = compute_units > 0 ? (uint64_t)compute_units : 1;
         s = 1;
         if (tiles > 0 && tiles < cus) {
@@ -357,19 +380,62 @@ struct sgemm_handle {
     sgemm_handle* edge_cols = nullptr;        // strip of rows past the last tile row, of columns past the last
     int resident = 0;                         // work-groups of generated_gemm the device holds at once (0: unknown)
     hipStream_t own_stream = nullptr;         // created at sgemm_open; `stream` is it unless sgemm_set_stream
+    std::vector<sgemm_handle*> edge_of;       // handles this one serves as an edge kernel (under g_edge_mutex)
 };
+
+namespace {
+
+// Guards edge_rows / edge_cols / edge_of links between handles, which
+// sgemm_set_edge_kernels and sgemm_close of different handles update.
+std::mutex g_edge_mutex;
+
+void unlink_edge(sgemm_handle* edge, sgemm_handle* main) {
+    if (!edge) return;
+    auto& v = edge->edge_of;
+    for (size_t i = 0; i < v.size(); ++i)
+        if (v[i] == main) {
+            v.erase(v.begin() + (long)i);
+            return;  // one entry per attachment: rows and cols each add one
+        }
+}
+
+}  // namespace
+
+namespace {
+
+// Bytes [lo, hi) a column-major rows x cols matrix with leading dimension ld
+// occupies from p (empty for a null pointer or an empty matrix).
+struct Span {
+    uintptr_t lo = 0, hi = 0;
+    bool overlaps(const Span& o) const { return lo < hi && o.lo < o.hi && lo < o.hi && o.lo < hi; }
+};
+
+Span span_of(const float* p, uint32_t rows, uint32_t cols, uint32_t ld) {
+    Span s;
+    if (!p || !rows || !cols) return s;
+    s.lo = (uintptr_t)p;
+    s.hi = s.lo + (((uintptr_t)(cols - 1) * ld + rows) * sizeof(float));
+    return s;
+}
+
+}  // namespace
 
 namespace sgemm_internal {
 
 Plan plan(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k) {
     const sgemm_kernel_info& i = h->info;
     Plan p;
-    p.tiles = (size_t)((m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
-              ((n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n);
+    p.tiles = (size_t)((((uint64_t)m + (uint32_t)i.tile_m - 1) / (uint32_t)i.tile_m) *
+                       (((uint64_t)n + (uint32_t)i.tile_n - 1) / (uint32_t)i.tile_n));
     const size_t tile_bytes = (size_t)i.tile_m * (size_t)i.tile_n * 4;
     p.splits = effective_splits(i, h->compute_units, m, n, k);
     if (p.splits > 1) {
-        p.partial_bytes = p.tiles * p.splits * tile_bytes;
+        // saturates for shapes no device could hold (any allocation then fails)
+        size_t bytes = 0;
+        if (__builtin_mul_overflow(p.tiles, (size_t)p.splits, &bytes) ||
+            __builtin_mul_overflow(bytes, tile_bytes, &bytes))
+            bytes = SIZE_MAX;
+        p.partial_bytes = bytes;
         p.ticket_count = p.tiles;
         return p;
     }
@@ -434,6 +500,18 @@ int check_launch(const sgemm_handle* h, const float* dA, const float* dB, const 
     // buffer loads and stores need dword alignment only
     if (((uintptr_t)dA | (uintptr_t)dB | (uintptr_t)dC | (uintptr_t)dD) & 3u)
         return fail(SGEMM_E_INVALID, "sgemm_launch: device pointers must be 4-byte aligned");
+    // Tiles store D while other tiles still read A, B and C: D may share no
+    // byte with A or B, and may share bytes with C only as the very same
+    // matrix (dC == dD, ldc == ldd: every tile reads its C block before it
+    // writes the same D block, and no other tile touches that block).
+    const uint32_t a_rows = h->info.trans_a ? k : m, a_cols = h->info.trans_a ? m : k;
+    const uint32_t b_rows = h->info.trans_b ? n : k, b_cols = h->info.trans_b ? k : n;
+    const Span d_span = span_of(dD, m, n, ldd);
+    if (k && (d_span.overlaps(span_of(dA, a_rows, a_cols, lda)) || d_span.overlaps(span_of(dB, b_rows, b_cols, ldb))))
+        return fail(SGEMM_E_INVALID, "sgemm_launch: D overlaps A or B");
+    if (beta != 0.0f && d_span.overlaps(span_of(dC, m, n, ldc)) && !(dC == dD && ldc == ldd))
+        return fail(SGEMM_E_INVALID, "sgemm_launch: C and D overlap without being the same matrix (dC == dD and "
+                    "ldc == ldd)");
     return SGEMM_OK;
 }
 
@@ -454,7 +532,7 @@ int decompose(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t k, uint32_
     // replaces cost nothing while they fit in a round the interior needs anyway
     const uint64_t res = (uint64_t)h->resident;
     auto rounds = [&](uint32_t rm, uint32_t rn) {
-        return ((uint64_t)((rm + tm - 1) / tm) * ((rn + tn - 1) / tn) + res - 1) / res;
+        return ((((uint64_t)rm + tm - 1) / tm) * (((uint64_t)rn + tn - 1) / tn) + res - 1) / res;
     };
     const uint64_t both = rounds(m - me, n - ne);
     if (rounds(m, n) <= both) return 1;
@@ -565,6 +643,13 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
             (void)hipGetLastError();
         }
         if (!h->info.stream_k_groups) h->info.stream_k = 0;
+        // the static scratch of sgemm_launch_noalloc on this device: looked
+        // up here, so that no launch (maybe under graph capture) does it
+        const int sr = sgemm_internal::noalloc_prepare(dev);
+        if (sr != SGEMM_OK) {
+            sgemm_close(h);
+            return sr;
+        }
         if (h->info.split_k > h->info.split_k_max) {
             sgemm_close(h);
             return fail(SGEMM_E_CONFIG, "split_k = %d but %s has no generated_gemm_splitk", info.split_k, co_path);
@@ -584,6 +669,20 @@ int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out) {
 
 void sgemm_close(sgemm_handle* h) {
     if (!h) return;
+    {
+        // detach h from every handle it serves as an edge kernel (those fall
+        // back to running their whole problem themselves), and from its own
+        // edge kernels' lists
+        std::lock_guard<std::mutex> lock(g_edge_mutex);
+        for (sgemm_handle* main : h->edge_of) {
+            if (main->edge_rows == h) main->edge_rows = nullptr;
+            if (main->edge_cols == h) main->edge_cols = nullptr;
+        }
+        h->edge_of.clear();
+        unlink_edge(h->edge_rows, h);
+        unlink_edge(h->edge_cols, h);
+        h->edge_rows = h->edge_cols = nullptr;
+    }
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     if (h->own_stream && h->own_stream != h->stream) (void)hipStreamSynchronize(h->own_stream);
     if (h->ev_start) (void)hipEventDestroy(h->ev_start);
@@ -668,7 +767,11 @@ int sgemm_workspace_size(const sgemm_handle* h, uint32_t m, uint32_t n, uint32_t
     if (m && n) {
         own_part(h, m, n, k, &m, &n);
         const sgemm_internal::Plan p = sgemm_internal::plan(h, m, n, k);
-        *bytes = p.partial_bytes ? p.partial_bytes + p.ticket_count * 4 : 0;
+        size_t total = 0;
+        if (p.partial_bytes && (__builtin_mul_overflow(p.ticket_count, (size_t)4, &total) ||
+                                __builtin_add_overflow(total, p.partial_bytes, &total)))
+            total = SIZE_MAX;
+        *bytes = p.partial_bytes ? total : 0;
     }
     return SGEMM_OK;
 }
@@ -810,11 +913,18 @@ int check_edge(const sgemm_handle* h, const sgemm_handle* e, bool rows) {
 
 int sgemm_set_edge_kernels(sgemm_handle* h, sgemm_handle* rows, sgemm_handle* cols) {
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_edge_kernels: null handle");
+    std::lock_guard<std::mutex> lock(g_edge_mutex);
     int r = check_edge(h, rows, true);
     if (r == SGEMM_OK) r = check_edge(h, cols, false);
     if (r != SGEMM_OK) return r;
+    if (!h->edge_of.empty())
+        return fail(SGEMM_E_INVALID, "sgemm_set_edge_kernels: this handle is itself attached as an edge kernel");
+    unlink_edge(h->edge_rows, h);
+    unlink_edge(h->edge_cols, h);
     h->edge_rows = rows;
     h->edge_cols = cols;
+    if (rows) rows->edge_of.push_back(h);
+    if (cols) cols->edge_of.push_back(h);
     return SGEMM_OK;
 }
 
@@ -884,6 +994,14 @@ int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const flo
 int sgemm_set_stream(sgemm_handle* h, void* stream) {
     if (!h) return fail(SGEMM_E_INVALID, "sgemm_set_stream: null handle");
     hipStream_t next = stream ? static_cast<hipStream_t>(stream) : h->own_stream;
+    if (stream) {
+        // the handle's module, workspace and scratch live on its device
+        hipDevice_t dev = -1;
+        HIP_TRY(hipStreamGetDevice(next, &dev));
+        if (dev != h->device)
+            return fail(SGEMM_E_INVALID, "sgemm_set_stream: the stream belongs to device %d, the handle to device %d",
+                        (int)dev, h->device);
+    }
     if (next != h->stream) {
         // work already enqueued through h finishes before h moves on; not
         // under capture (a capturing stream cannot be synchronized)

@@ -155,19 +155,30 @@ class DeviceBuffer:
         _check("sgemm_malloc", load_library().sgemm_malloc(ctypes.byref(p), self.nbytes))
         self.ptr = p.value
 
+    @staticmethod
+    def column_major_bytes(a: np.ndarray) -> np.ndarray:
+        """The float32 values of `a` in the order the device holds them: a 2-D
+        array column by column (element (i, j) at i + j * rows), whatever its
+        numpy order or strides; a 1-D array as it is.  Arrays of other ranks
+        are refused: their device layout would be a guess."""
+        a = np.asarray(a, dtype=np.float32)
+        if a.ndim not in (1, 2):
+            raise ValueError(f"device buffers hold 1-D or 2-D (column-major) arrays, not {a.ndim}-D")
+        return np.ascontiguousarray(a.ravel(order="F"))
+
     @classmethod
     def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
-        # 2-D arrays are stored column-major, whatever their numpy order
-        flat = np.ascontiguousarray(np.asarray(a, dtype=np.float32).ravel(order="F"))
+        flat = cls.column_major_bytes(a)
         buf = cls(flat.nbytes)
         buf.upload(flat)
         return buf
 
     def upload(self, a: np.ndarray):
-        a = np.ascontiguousarray(a)
-        if a.nbytes > self.nbytes:
+        """Copies `a` to the start of the buffer, column-major like from_array."""
+        flat = self.column_major_bytes(a)
+        if flat.nbytes > self.nbytes:
             raise ValueError("array larger than the device buffer")
-        _check("sgemm_memcpy_h2d", load_library().sgemm_memcpy_h2d(self.ptr, _ptr(a), a.nbytes))
+        _check("sgemm_memcpy_h2d", load_library().sgemm_memcpy_h2d(self.ptr, _ptr(flat), flat.nbytes))
 
     def download(self, count: Optional[int] = None) -> np.ndarray:
         count = self.nbytes // 4 if count is None else int(count)

@@ -25,6 +25,8 @@
  *     (ldb >= k), or n x k (ldb >= n) with trans_b; C and D are m x n
  *     (ldc, ldd >= m).  C is not read when beta == 0.  dC may equal dD (with
  *     ldc == ldd): an in-place update D = alpha * op(A) * op(B) + beta * D.
+ *     Any other overlap of D with C (when beta != 0), A or B is refused with
+ *     SGEMM_E_INVALID: tiles write D while other tiles still read them.
  */
 #ifndef SGEMM_SHIM_H
 #define SGEMM_SHIM_H
@@ -36,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SGEMM_SHIM_ABI_VERSION 8
+#define SGEMM_SHIM_ABI_VERSION 9
 
 /* Most K ranges generated_gemm_splitk splits one output tile into. */
 #define SGEMM_MAX_SPLIT_K 16
@@ -95,11 +97,16 @@ int sgemm_abi_version(void);
 int sgemm_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz, int* lds_per_block);
 
 /* Loads <co_path> (symbol "generated_gemm", and "generated_gemm_splitk" when
- * present) and its <toml_path> config.
+ * present) and its <toml_path> config.  It also looks up, once per device,
+ * the device address of sgemm_launch_noalloc's static scratch on the current
+ * device, so no launch ever does (the first no-alloc call may be captured).
  * Replaces getAsmKernelConfig + prepareASMKernel (generator_runner.cpp:100-124, :69-73). */
 int sgemm_open(const char* co_path, const char* toml_path, sgemm_handle** out);
 
-/* Unloads the module and releases the stream and events (generator_runner.cpp:318). */
+/* Unloads the module and releases the stream and events (generator_runner.cpp:318).
+ * A handle attached to others as an edge kernel (sgemm_set_edge_kernels) is
+ * detached from them first: their later launches run the whole problem on
+ * their own kernel. */
 void sgemm_close(sgemm_handle* h);
 
 /* Copies the handle's kernel configuration (generator_runner.cpp:127-153 geometry). */
@@ -174,8 +181,10 @@ int sgemm_set_stream_k(sgemm_handle* h, int mode);
  * column wide).  The strips use their kernels' own split-K / stream-K
  * settings and workspace.  Either may be NULL (that strip then stays with
  * h); the same handle may serve both.
- * The attached handles must stay open while attached, and must not run other
- * work concurrently with launches through h.  No counterpart in the
+ * Closing an attached handle detaches it (h's strips then stay with h).  A
+ * handle serving as another's edge kernel cannot take edge kernels itself.
+ * The attached handles must not run other work concurrently with launches
+ * through h.  No counterpart in the
  * reference, whose tuner skips shapes its tiles do not divide
  * (tuner/sgemm_tuner.py:97-100). */
 int sgemm_set_edge_kernels(sgemm_handle* h, sgemm_handle* rows, sgemm_handle* cols);
@@ -252,7 +261,8 @@ int sgemm_time_each(sgemm_handle* h, const float* dA, const float* dB, const flo
 int sgemm_synchronize(sgemm_handle* h);
 
 /* Makes later launches, timings and synchronisations of h use `stream` (a
- * hipStream_t of the handle's device, owned by the caller, who keeps it alive
+ * hipStream_t of the handle's device -- one of another device is refused
+ * with SGEMM_E_INVALID -- owned by the caller, who keeps it alive
  * while h uses it) instead of the stream h created at sgemm_open; NULL goes
  * back to that one.  Work already enqueued through h is waited for first, so
  * the handle's launches stay ordered; the current stream must not be

@@ -6,6 +6,9 @@ import this module, and only to check or to time the CPU baseline; the product
 
 * ``cpu_gemm`` / ``cpu_gemm_mt``: liboracle.so's restatement of the reference
   runner's cpuGemm (/root/reference/runner/generator_runner.cpp:16-33).
+* ``cpu_gemm_blocked``: the same arithmetic, cache- and register-blocked over
+  threads (every output keeps its one float accumulator and its order over l),
+  bitwise equal to ``cpu_gemm``; the whole-matrix checker at full sizes.
 * ``ref_cpu_gemm``: the reference's own cpuGemm, compiled from its source into
   ``_ref/libref_runner.so`` (see Makefile); ``None`` when that was not built.
 * ``gemm_f64``: double-accumulated reference for error bounds.
@@ -49,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_cpu_gemm.restype = None
         L.oracle_cpu_gemm_mt.argtypes = [_vp, _vp, _vp, _vp, _f, _f, _u32, _u32, _u32, ctypes.c_int]
         L.oracle_cpu_gemm_mt.restype = ctypes.c_int
+        L.oracle_cpu_gemm_blocked.argtypes = [_vp, _vp, _vp, _vp, _f, _f, _u32, _u32, _u32, ctypes.c_int]
+        L.oracle_cpu_gemm_blocked.restype = ctypes.c_int
         L.oracle_gemm_f64.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double, _u32, _u32, _u32]
         L.oracle_gemm_f64.restype = None
         L.oracle_splitmix64_at.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
@@ -103,6 +108,19 @@ def cpu_gemm_mt(A, B, C=None, alpha: float = 1.0, beta: float = 0.0, threads: in
     D = np.empty((m, n), dtype=np.float32, order="F")
     lib().oracle_cpu_gemm_mt(A.ctypes.data, B.ctypes.data, C.ctypes.data, D.ctypes.data, alpha, beta, m, n, k,
                              threads)
+    return D
+
+
+def cpu_gemm_blocked(A, B, C=None, alpha: float = 1.0, beta: float = 0.0, threads: int = 8) -> np.ndarray:
+    """cpuGemm's result (bitwise) from the blocked loop nest: seconds at 4096^3."""
+    A, B = _f32(A), _f32(B)
+    m, k = A.shape
+    k2, n = B.shape
+    assert k == k2
+    C = _zeros_like_c(m, n, C)
+    D = np.empty((m, n), dtype=np.float32, order="F")
+    lib().oracle_cpu_gemm_blocked(A.ctypes.data, B.ctypes.data, C.ctypes.data, D.ctypes.data, alpha, beta, m, n, k,
+                                  threads)
     return D
 
 

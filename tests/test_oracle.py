@@ -107,6 +107,63 @@ def test_cpu_gemm_threads_are_bitwise_identical():
         assert np.array_equal(D1, oracle.cpu_gemm_mt(A, B, C, 1.0, 1.0, threads=t))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (31, 3, 7), (32, 4, 64), (33, 5, 17), (37, 29, 301),
+                                   (64, 8, 1000), (100, 1, 33), (1, 100, 33), (65, 9, 0)])
+def test_blocked_cpu_gemm_is_bitwise_cpu_gemm(m, n, k):
+    """The blocked loop nest (whole-matrix checker) against the plain
+    restatement: full blocks, edge blocks in rows and columns, k = 0, and
+    every thread split, bit for bit."""
+    A = oracle.fill_matrix(m, k, 9, 0, 1)
+    B = oracle.fill_matrix(k, n, 9, 1, 1)
+    C = oracle.fill_matrix(m, n, 9, 2)
+    D = oracle.cpu_gemm(A, B, C, 0.75, -1.25)
+    for t in (1, 2, 3, 8, 300):
+        assert np.array_equal(oracle.cpu_gemm_blocked(A, B, C, 0.75, -1.25, threads=t), D), t
+
+
+def test_blocked_cpu_gemm_special_values_and_order():
+    """Cases a reordered or fused sum would get wrong: a sum that depends on
+    the order of l (1 + 2^-24 + 2^-24 rounds to 1 left to right, not right to
+    left), a fused multiply-add (the product 1 + 2^-23 squared loses its low
+    bit only when rounded before the add), and NaN/Inf propagation with
+    beta = 0 (0 * NaN in C stays NaN, as in the reference's d = beta*c + alpha*acc)."""
+    A = np.array([[1.0, 1.0, 1.0]] * 32, dtype=np.float32)
+    B = np.array([[1.0] * 4, [2.0 ** -24] * 4, [2.0 ** -24] * 4], dtype=np.float32)
+    D = oracle.cpu_gemm_blocked(A, B)
+    assert np.all(D == np.float32(1.0))
+    x = np.float32(1.0 + 2.0 ** -23)
+    A = np.full((32, 2), x, dtype=np.float32)
+    A[:, 0] = -1.0
+    B = np.array([[1.0] * 4, [x] * 4], dtype=np.float32)
+    # acc = -1, then acc + x*x: the rounded product 1 + 2^-22 gives 2^-22 exactly;
+    # fma(x, x, -1) would keep the product's 2^-46 as well
+    assert np.all(oracle.cpu_gemm_blocked(A, B) == np.float32(2.0 ** -22))
+    A = oracle.fill_matrix(40, 9, 4, 0)
+    B = oracle.fill_matrix(9, 6, 4, 1)
+    A[3, 2] = np.inf
+    B[4, 5] = np.nan
+    C = np.zeros((40, 6), dtype=np.float32)
+    C[7, 1] = np.nan
+    for beta in (0.0, 1.0):
+        got = oracle.cpu_gemm_blocked(A, B, C, 1.0, beta, threads=3)
+        want = oracle.cpu_gemm(A, B, C, 1.0, beta)
+        assert np.array_equal(np.isnan(got), np.isnan(want)) and np.isnan(got[7, 1])
+        ok = ~np.isnan(want)
+        assert np.array_equal(got[ok], want[ok])
+
+
+def test_blocked_cpu_gemm_catches_a_misplaced_output():
+    """A planted mistake (two output rows swapped) is seen by the bitwise
+    comparison the GPU tests use."""
+    A = oracle.fill_matrix(64, 50, 5, 0)
+    B = oracle.fill_matrix(50, 8, 5, 1)
+    D = oracle.cpu_gemm_blocked(A, B)
+    bad = D.copy()
+    bad[[3, 40]] = bad[[40, 3]]
+    assert not np.array_equal(bad, oracle.cpu_gemm(A, B))
+    assert oracle.normwise_error(bad, oracle.gemm_f64(A, B)) > oracle.tolerance(50)
+
+
 def test_cpu_gemm_column_slice_equals_full_gemm_columns():
     A = oracle.fill_matrix(64, 80, 2, 0)
     B = oracle.fill_matrix(80, 40, 2, 1)
@@ -125,7 +182,9 @@ def test_oracle_equals_reference_cpu_gemm_bitwise():
         A = oracle.fill_matrix(m, k, seed, 0, dist)
         B = oracle.fill_matrix(k, n, seed, 1, dist)
         C = oracle.fill_matrix(m, n, seed, 2, dist)
-        assert np.array_equal(oracle.cpu_gemm(A, B, C, alpha, beta), oracle.ref_cpu_gemm(A, B, C, alpha, beta))
+        ref = oracle.ref_cpu_gemm(A, B, C, alpha, beta)
+        assert np.array_equal(oracle.cpu_gemm(A, B, C, alpha, beta), ref)
+        assert np.array_equal(oracle.cpu_gemm_blocked(A, B, C, alpha, beta, threads=3), ref)
 
 
 def test_reference_arange_cases_against_exact_golden():

@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # and the Python binding declares a signature for each of them
     assert set(declared_functions()) == set(S.SIGNATURES)
-    assert lib.sgemm_abi_version() == 8
+    assert lib.sgemm_abi_version() == 9
     assert ctypes.sizeof(S.KernelInfo) == 4 * 22  # 22 ints, as in sgemm_kernel_info
 
 
@@ -109,33 +109,58 @@ def test_runner_usage_error_exit_code():
 
 
 def test_runner_cpu_reference_matches_oracle():
-    """The runner's validation GEMM (runner/cpu_reference.hpp) is the same
-    arithmetic as the oracle: compile a tiny driver for it and compare bitwise."""
+    """The runner's validation GEMMs (runner/cpu_reference.hpp) are the
+    oracle's arithmetic: compile a tiny driver for the column-split loop, the
+    blocked loop and the reporting function the runner calls, and compare
+    bitwise; then parse the lines that function prints (the reference's
+    "cpuGemm func" figure as one single-threaded run, the blocked
+    multithreaded figure on its own line, the host CPU model and thread count)."""
     import oracle
+    import re
     import tempfile
     src = os.path.join(ROOT, "amdgpu-arch-gemm_amd", "runner")
     with tempfile.TemporaryDirectory() as tmp:
         c = os.path.join(tmp, "d.cpp")
         exe = os.path.join(tmp, "d")
         with open(c, "w") as f:
-            f.write('#include "cpu_reference.hpp"\n#include <cstdio>\n#include <vector>\n'
-                    'int main(){unsigned m=37,n=29,k=301; std::vector<float> a(m*k),b(k*n),c(m*n),d(m*n);\n'
+            f.write('#include "cpu_reference.hpp"\n#include <cstdio>\n#include <cstdlib>\n#include <iostream>\n'
+                    '#include <vector>\n'
+                    'int main(int argc, char** argv){unsigned m=atoi(argv[1]),n=atoi(argv[2]),k=atoi(argv[3]);\n'
+                    'double budget=atof(argv[4]);\n'
+                    'std::vector<float> a(m*k),b(k*n),c(m*n),d(m*n),e(m*n),g(m*n);\n'
                     'FILE* f=fopen("in.bin","rb"); fread(a.data(),4,a.size(),f); fread(b.data(),4,b.size(),f);'
                     ' fread(c.data(),4,c.size(),f); fclose(f);\n'
                     'runner_cpu_gemm(a.data(),b.data(),c.data(),d.data(),0.5f,-2.0f,m,n,k,3);\n'
-                    'f=fopen("out.bin","wb"); fwrite(d.data(),4,d.size(),f); fclose(f); return 0;}\n')
+                    'runner_cpu_gemm_blocked(a.data(),b.data(),c.data(),e.data(),0.5f,-2.0f,m,n,k,5);\n'
+                    'bool same=runner_cpu_reference(a.data(),b.data(),c.data(),g.data(),0.5f,-2.0f,m,n,k,4,budget,'
+                    'std::cout);\n'
+                    'f=fopen("out.bin","wb"); fwrite(d.data(),4,d.size(),f); fwrite(e.data(),4,e.size(),f);'
+                    ' fwrite(g.data(),4,g.size(),f); fclose(f); return same ? 0 : 3;}\n')
         subprocess.run(["g++", "-O2", "-ffp-contract=off", "-std=c++17", "-I", src, c, "-o", exe, "-pthread"],
                        check=True)
-        m, n, k = 37, 29, 301
-        A = oracle.fill_matrix(m, k, 8, 0)
-        B = oracle.fill_matrix(k, n, 8, 1)
-        C = oracle.fill_matrix(m, n, 8, 2)
-        with open(os.path.join(tmp, "in.bin"), "wb") as f:
-            for X in (A, B, C):
-                f.write(np.asarray(X, dtype=np.float32).ravel(order="F").tobytes())
-        subprocess.run([exe], cwd=tmp, check=True)
-        D = np.fromfile(os.path.join(tmp, "out.bin"), dtype=np.float32).reshape(n, m).T
-    assert np.array_equal(D, oracle.cpu_gemm(A, B, C, 0.5, -2.0))
+        for (m, n, k, budget) in ((37, 29, 301, 1e9), (70, 9, 64, 1e9), (256, 64, 2048, 0.0)):
+            A = oracle.fill_matrix(m, k, 8, 0)
+            B = oracle.fill_matrix(k, n, 8, 1)
+            C = oracle.fill_matrix(m, n, 8, 2)
+            with open(os.path.join(tmp, "in.bin"), "wb") as f:
+                for X in (A, B, C):
+                    f.write(np.asarray(X, dtype=np.float32).ravel(order="F").tobytes())
+            ret = subprocess.run([exe, str(m), str(n), str(k), str(budget)], cwd=tmp, stdout=subprocess.PIPE,
+                                 check=True)
+            out = np.fromfile(os.path.join(tmp, "out.bin"), dtype=np.float32).reshape(3, n, m)
+            want = oracle.cpu_gemm(A, B, C, 0.5, -2.0)
+            for X in out:
+                assert np.array_equal(X.T, want)
+            text = ret.stdout.decode()
+            lines = text.splitlines()
+            assert re.match(r"host CPU: .+, hardware_concurrency \d+$", lines[0]), text
+            assert lines[1].startswith("cpuGemm func: ") and "1 thread, reference loop order" in lines[1], text
+            if budget > 1e6:
+                assert lines[1].endswith("whole matrix)"), text
+            else:  # zero budget: one column timed, scaled by n
+                assert f"scaled by {n}/1 from columns [0, 1) of {n}" in lines[1], text
+            assert re.match(r"cpuGemm blocked, 4 threads: [0-9.e+-]+ ms \(whole matrix; bitwise equal", lines[2]), \
+                text
 
 
 def test_device_view_bounds_and_ownership():
@@ -151,3 +176,17 @@ def test_device_view_bounds_and_ownership():
         with pytest.raises(ValueError):
             S.DeviceView(owner, off, nb)
     assert S.DeviceView(owner, 64, 0).nbytes == 0
+
+
+def test_device_buffers_take_column_major_bytes():
+    """What upload() and from_array() send to the device, checked without a
+    device: a 2-D array column by column whatever its numpy order, a 1-D
+    array as it is; other ranks are refused."""
+    base = np.arange(12, dtype=np.float64).reshape(3, 4)
+    want = base.T.ravel().astype(np.float32)
+    for arr in (base, np.asfortranarray(base), base[:, :], np.ascontiguousarray(base.T).T):
+        got = S.DeviceBuffer.column_major_bytes(arr)
+        assert got.dtype == np.float32 and got.flags.c_contiguous and np.array_equal(got, want)
+    assert np.array_equal(S.DeviceBuffer.column_major_bytes(np.arange(5)), np.arange(5, dtype=np.float32))
+    with pytest.raises(ValueError):
+        S.DeviceBuffer.column_major_bytes(np.zeros((2, 2, 2)))

@@ -9,6 +9,9 @@ into a HIP graph on a caller's stream (sgemm_set_stream) -- split-K,
 stream-K and edge-strip launches -- it must replay what an eager call gives.
 """
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -129,11 +132,6 @@ def _ok(rc, what):
     assert rc == 0, f"{what} failed: {rc}"
 
 
-def _col(x):
-    """The column-major bytes of a matrix (upload copies an array's memory order)."""
-    return np.ascontiguousarray(np.asarray(x, dtype=np.float32).ravel(order="F"))
-
-
 GRAPH_CASES = [
     # (main, edges or None, stream-K mode or None, m, n, k): split-K, stream-K and edge-strip launches
     ("mt64x64_a16_wg1x4_dk32_s3", None, None, 256, 256, 8192),
@@ -172,10 +170,11 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
         dA, dB, dC, dD = S.DeviceBuffer(4 * m * k), S.DeviceBuffer(4 * k * n), S.DeviceBuffer(4 * m * n), \
             S.DeviceBuffer(4 * m * n)
         kern.set_stream(stream.value)
-        # one eager call first: it looks up the scratch's device address
-        dA.upload(_col(S.fill_matrix(*sa, 1, 0)))
-        dB.upload(_col(S.fill_matrix(*sb, 1, 1)))
-        dC.upload(_col(S.fill_matrix(m, n, 1, 2)))
+        # one eager call before the capture (the first call of all is captured
+        # in test_first_noalloc_call_of_a_process_may_be_captured)
+        dA.upload(S.fill_matrix(*sa, 1, 0))
+        dB.upload(S.fill_matrix(*sb, 1, 1))
+        dC.upload(S.fill_matrix(m, n, 1, 2))
         kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
         kern.synchronize()
         _ok(_hip.hipStreamBeginCapture(stream, CAPTURE_MODE_GLOBAL), "hipStreamBeginCapture")
@@ -187,9 +186,9 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
         for replay in range(3):
             seed = 50 + replay
             A, B, C = S.fill_matrix(*sa, seed, 0), S.fill_matrix(*sb, seed, 1), S.fill_matrix(m, n, seed, 2)
-            dA.upload(_col(A))
-            dB.upload(_col(B))
-            dC.upload(_col(C))
+            dA.upload(A)
+            dB.upload(B)
+            dC.upload(C)
             dD.upload(np.full((m, n), np.nan, dtype=np.float32))
             _ok(_hip.hipGraphLaunch(exe, stream), "hipGraphLaunch")
             _ok(_hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
@@ -214,3 +213,69 @@ def test_noalloc_launch_replays_from_a_hip_graph(kernels, main, edges, mode, m, 
         for kk in reversed(opened):
             kk.close()
         _hip.hipStreamDestroy(stream)
+
+
+FIRST_CAPTURE_CHILD = r"""
+import ctypes, sys
+import numpy as np
+sys.path[:0] = sys.argv[1:4]
+import oracle
+from generator import catalog
+from shim import sgemm_shim as S
+hip = ctypes.CDLL("libamdhip64.so")
+vp = ctypes.c_void_p
+def ok(rc, what):
+    assert rc == 0, f"{what} failed: {rc}"
+name, (m, n, k) = "mt64x64_a16_wg1x4_dk32_s3", (256, 256, 8192)
+kern = S.Kernel(*catalog.paths(name))
+ref = S.Kernel(*catalog.paths(name))
+assert kern.launch_splits(m, n, k) > 1
+stream, graph, exe = vp(), vp(), vp()
+ok(hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+A, B, C = S.fill_matrix(m, k, 7, 0), S.fill_matrix(k, n, 7, 1), S.fill_matrix(m, n, 7, 2)
+dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (A, B, C))
+dD, dR = S.DeviceBuffer.from_array(np.full((m, n), np.nan, np.float32)), S.DeviceBuffer(4 * m * n)
+kern.set_stream(stream.value)
+print("capturing the first sgemm_launch_noalloc of this process", flush=True)
+ok(hip.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+try:
+    kern.launch_noalloc(dA, dB, dC, dD, m, n, k, alpha=1.5, beta=-0.5)
+finally:
+    ok(hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+ok(hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0), "hipGraphInstantiate")
+ref.launch(dA, dB, dC, dR, m, n, k, alpha=1.5, beta=-0.5)
+ref.synchronize()
+R = dR.download().reshape(n, m).T.copy()
+for replay in range(3):
+    dD.upload(np.full((m, n), np.nan, np.float32))
+    ok(hip.hipGraphLaunch(exe, stream), "hipGraphLaunch")
+    ok(hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+    D = dD.download().reshape(n, m).T.copy()
+    assert np.array_equal(D, R), f"replay {replay} differs from sgemm_launch"
+    err = oracle.normwise_error(D, oracle.cpu_gemm_blocked(A, B, C, 1.5, -0.5, threads=8))
+    assert err <= oracle.tolerance(k), err
+    print(f"replay {replay}: equal to sgemm_launch, normwise error {err:.3e}", flush=True)
+hip.hipGraphExecDestroy(exe)
+hip.hipGraphDestroy(graph)
+kern.set_stream(None)
+kern.close()
+ref.close()
+hip.hipStreamDestroy(stream)
+print("FIRST_CAPTURE_OK", flush=True)
+"""
+
+
+def test_first_noalloc_call_of_a_process_may_be_captured(kernels):
+    """sgemm_open looks up the static scratch's device address, so the very
+    first sgemm_launch_noalloc of a process (split-K, using the scratch) may
+    run under graph capture: in a fresh child process, capture it first,
+    replay the graph three times and compare each replay with sgemm_launch."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    paths = [os.path.join(root, "amdgpu-arch-gemm_amd"), os.path.join(root, "oracle"), root]
+    _say("child process: first no-alloc call under capture")
+    ret = subprocess.run([sys.executable, "-u", "-c", FIRST_CAPTURE_CHILD] + paths, stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT, timeout=300)
+    out = ret.stdout.decode()
+    _say(out)
+    assert ret.returncode == 0 and "FIRST_CAPTURE_OK" in out, out
+
