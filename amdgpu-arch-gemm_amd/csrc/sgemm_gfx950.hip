@@ -140,6 +140,12 @@
 #ifndef SG_TB
 #define SG_TB 0
 #endif
+#ifndef SG_WS
+#define SG_WS 0
+#endif
+#ifndef SG_WS_PD
+#define SG_WS_PD 2
+#endif
 #ifndef SG_KERNEL_NAME
 #define SG_KERNEL_NAME generated_gemm
 #endif
@@ -201,12 +207,23 @@ template <> struct Atom<16> {
     __device__ static __forceinline__ int row(int q, int lane) { return q + 4 * (lane >> 4); }
 };
 
-template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA, bool TB>
+// WG0 x WG1 waves of WT0 x WT1 atoms describe the launch (the .toml's
+// wave_group / wave_tiling: NT work-items, an MT0 x MT1 tile).  With WS (wave
+// specialisation) the first half of the waves along M computes the whole tile
+// -- WG0 / 2 x WG1 waves of 2 * WT0 x WT1 atoms -- and the other half only
+// moves K tiles from memory to LDS; otherwise every wave does both.
+template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA, bool TB,
+          bool WS>
 struct Geometry {
     typedef Atom<AM> atom;
     static constexpr int NT = WG0 * WG1 * 64;
     static constexpr int MT0 = atom::M * WG0 * WT0;
     static constexpr int MT1 = atom::N * WG1 * WT1;
+    static constexpr int CWG0 = WS ? WG0 / 2 : WG0;   // computing waves along M
+    static constexpr int CWT0 = WS ? WT0 * 2 : WT0;   // their atoms along M
+    static constexpr int CWAVES = CWG0 * WG1;         // computing waves
+    static constexpr int CNT = CWAVES * 64;           // their work-items
+    static constexpr int LT = WS ? NT - CNT : NT;     // work-items that load K tiles
     // k values a lane reads per LDS read of B (and MFMA steps per k block)
     static constexpr int KPL = (DK / atom::K >= 4) ? 4 : ((DK / atom::K >= 2) ? 2 : 1);
     static constexpr int KB = atom::K * KPL;
@@ -223,13 +240,14 @@ struct Geometry {
     // float4 chunks each thread moves per K tile
     static constexpr int A_CHUNKS = MT0 * DK / 4;
     static constexpr int B_CHUNKS = MT1 * DK / 4;
-    static constexpr int LA = (A_CHUNKS + NT - 1) / NT;
-    static constexpr int LB = (B_CHUNKS + NT - 1) / NT;
+    static constexpr int LA = (A_CHUNKS + LT - 1) / LT;
+    static constexpr int LB = (B_CHUNKS + LT - 1) / LT;
 
     static_assert(DK % 4 == 0, "DK must be a multiple of 4");
     static_assert(DK % KB == 0, "DK must be a multiple of the k block");
     static_assert(MT0 % 4 == 0, "MT0 must be a multiple of 4");
-    static_assert(WT0 == 1 || WT0 == 2 || WT0 == 4 || WT0 == 8, "WT0 must be 1, 2, 4 or 8");
+    static_assert(CWT0 == 1 || CWT0 == 2 || CWT0 == 4 || CWT0 == 8, "WT0 must be 1, 2, 4 or 8");
+    static_assert(!WS || (WG0 % 2 == 0), "wave specialisation halves an even wave group along M");
     static_assert(WT1 >= 1 && WT1 <= 8, "WT1 must be in [1, 8]");
     static_assert(!TB || WT1 == 1 || WT1 == 2 || WT1 == 4 || WT1 == 8, "B^T reads WT1 consecutive floats");
     static_assert(PAD_A % 4 == 0 && PAD_B % 4 == 0, "LDS pads keep 16-byte rows");
@@ -237,7 +255,9 @@ struct Geometry {
     static_assert(LDS_FLOATS * 4 <= 163840, "LDS tile exceeds the 160 KiB of a gfx950 CU");
 };
 
-typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0, SG_TB != 0> G;
+typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0, SG_TB != 0,
+                 SG_WS != 0> G;
+static_assert(!SG_WS || (!SG_SPLITK && !SG_STREAMK), "the wave-specialised K loop has no split-K / stream-K variant");
 
 // B-tile chunk swizzle of row n (0: rows stored straight).  The XOR stays
 // inside a row when its chunk count is a multiple of MASK + 1, and a lane's
@@ -256,8 +276,8 @@ static_assert(SG_BSWZ_MASK == 0 || !SG_TB, "the B swizzle is for the layouts wit
 __device__ __forceinline__ constexpr int aswz(int m) { return (m >> SG_ASWZ_SHIFT) & SG_ASWZ_MASK; }
 static_assert(SG_ASWZ_MASK == 0 || (SG_ASWZ_MASK & (SG_ASWZ_MASK + 1)) == 0, "swizzle mask is 2^b - 1");
 static_assert((SG_DK / 4) % (SG_ASWZ_MASK + 1) == 0, "swizzle leaves the A^T row");
-static_assert(SG_ASWZ_MASK == 0 || ((1 << SG_ASWZ_SHIFT) >= SG_WT0 &&
-                                    (G::atom::M * SG_WT0) % ((SG_ASWZ_MASK + 1) << SG_ASWZ_SHIFT) == 0),
+static_assert(SG_ASWZ_MASK == 0 || ((1 << SG_ASWZ_SHIFT) >= G::CWT0 &&
+                                    (G::atom::M * G::CWT0) % ((SG_ASWZ_MASK + 1) << SG_ASWZ_SHIFT) == 0),
               "swizzle varies across a lane's rows");
 static_assert(SG_ASWZ_MASK == 0 || SG_TA, "the A swizzle is for the layout with k contiguous in A^T");
 
@@ -429,7 +449,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     typedef G::atom AT;
     typedef AT::acc_t acc_t;
     constexpr int NT = G::NT, MT0 = G::MT0, MT1 = G::MT1, DK = SG_DK, NBUF = SG_NBUF;
-    constexpr int WT0 = SG_WT0, WT1 = SG_WT1, KPL = G::KPL, KB = G::KB;
+    constexpr int WT0 = G::CWT0, WT1 = SG_WT1, KPL = G::KPL, KB = G::KB;
+    // K-tile loads: work-item ltid of LT (every work-item, or with wave
+    // specialisation those of the loading waves; the computing waves' ltid
+    // is a valid index they never use)
+    constexpr int LT = G::LT;
     constexpr bool TA = SG_TA != 0, TB = SG_TB != 0;
 
     __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
@@ -438,8 +462,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // wave-uniform (a scalar register): the epilogue's buffer descriptors
     // derived from it then need no per-lane waterfall loop
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave % SG_WG0;
-    const int wn = wave / SG_WG0;
+    const int wm = wave % G::CWG0;
+    const int wn = wave / G::CWG0;
+    const bool loader_wave = SG_WS && wave >= G::CWAVES;
+    const int ltid = SG_WS ? (tid >= G::CNT ? tid - G::CNT : tid % LT) : tid;
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
 
@@ -517,7 +543,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     int a_lds[G::LA], b_lds[G::LB];
 #pragma unroll
     for (int i = 0; i < G::LA; ++i) {
-        const int ch = tid + i * NT;
+        const int ch = ltid + i * LT;
         int c0, c1;
         a_chunk(ch, c0, c1);
         // a chunk of rows wholly past m reads the tile's first row instead
@@ -533,7 +559,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     }
 #pragma unroll
     for (int i = 0; i < G::LB; ++i) {
-        const int ch = tid + i * NT;
+        const int ch = ltid + i * LT;
         int c0, c1;
         b_chunk(ch, c0, c1);
         // a chunk of columns wholly past n reads the tile's first column instead
@@ -579,7 +605,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     int kt_first = 0;
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
 
-    // gload(tag, t, set, head): global -> VGPR copy of K tile t.  On the fast
+    // gload_to(tag, t, da, db, head): global -> VGPR copy of K tile t into
+    // da (A) and db (B); gload(tag, t, set, head) into register set `set`.  On the fast
     // path every chunk is one buffer_load_dwordx4: a wave-uniform descriptor
     // per operand and K tile (scalar arithmetic only; num_records is the K
     // tile's footprint) and the chunk's 32-bit byte offset -- no 64-bit vector
@@ -588,7 +615,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // SlowPath tag every element is
     // loaded from a clamped (always valid) address and replaced by 0 when it
     // lies outside A or B, so the code stays branch-free.
-    auto gload = [&](auto path, int t, int set, auto head) __attribute__((always_inline)) {
+    auto gload_to = [&](auto path, int t, f32x4 (&da)[G::LA], f32x4 (&db)[G::LB], auto head)
+        __attribute__((always_inline)) {
         int kt = kt_first + t;
         if (kt >= ktiles) kt -= ktiles;
         if constexpr (!decltype(path)::slow) {
@@ -637,31 +665,31 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             };
 #pragma unroll
             for (int i = 0; i < G::LA; ++i) {
-                const int ch = tid + i * NT;
-                if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
+                const int ch = ltid + i * LT;
+                if (G::A_CHUNKS % LT == 0 || ch < G::A_CHUNKS) {
                     if constexpr (decltype(head)::on) {
                         // k inside the tile of the chunk's first element: c1 (A), 4 * c0 (A^T)
                         int c0, c1;
                         a_chunk(ch, c0, c1);
                         const int kk = TA ? c0 * 4 : c1;
-                        ra[set][i] = head_load(rsa, a_off[i], kk, TA, TA ? 4u : lda * 4u);
+                        da[i] = head_load(rsa, a_off[i], kk, TA, TA ? 4u : lda * 4u);
                     } else {
-                        ra[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)a_off[i], 0, 0));
+                        da[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)a_off[i], 0, 0));
                     }
                 }
             }
 #pragma unroll
             for (int i = 0; i < G::LB; ++i) {
-                const int ch = tid + i * NT;
-                if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
+                const int ch = ltid + i * LT;
+                if (G::B_CHUNKS % LT == 0 || ch < G::B_CHUNKS) {
                     if constexpr (decltype(head)::on) {
                         // k inside the tile of the chunk's first element: 4 * c0 (B), c1 (B^T)
                         int c0, c1;
                         b_chunk(ch, c0, c1);
                         const int kk = TB ? c1 : c0 * 4;
-                        rb[set][i] = head_load(rsb, b_off[i], kk, !TB, TB ? ldb * 4u : 4u);
+                        db[i] = head_load(rsb, b_off[i], kk, !TB, TB ? ldb * 4u : 4u);
                     } else {
-                        rb[set][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)b_off[i], 0, 0));
+                        db[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)b_off[i], 0, 0));
                     }
                 }
             }
@@ -669,8 +697,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             const uint32_t k0 = (uint32_t)kt * DK;
 #pragma unroll
             for (int i = 0; i < G::LA; ++i) {
-                const int ch = tid + i * NT;
-                if (G::A_CHUNKS % NT == 0 || ch < G::A_CHUNKS) {
+                const int ch = ltid + i * LT;
+                if (G::A_CHUNKS % LT == 0 || ch < G::A_CHUNKS) {
                     int c0, c1;
                     a_chunk(ch, c0, c1);
 #pragma unroll
@@ -680,14 +708,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         const uint32_t rc = row < m ? row : m - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TA ? a[(size_t)rc * lda + kc] : a[(size_t)kc * lda + rc];
-                        ra[set][i][e] = (row < m && kk < k) ? x : 0.0f;
+                        da[i][e] = (row < m && kk < k) ? x : 0.0f;
                     }
                 }
             }
 #pragma unroll
             for (int i = 0; i < G::LB; ++i) {
-                const int ch = tid + i * NT;
-                if (G::B_CHUNKS % NT == 0 || ch < G::B_CHUNKS) {
+                const int ch = ltid + i * LT;
+                if (G::B_CHUNKS % LT == 0 || ch < G::B_CHUNKS) {
                     int c0, c1;
                     b_chunk(ch, c0, c1);
 #pragma unroll
@@ -697,25 +725,30 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         const uint32_t cc = col < n ? col : n - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TB ? b[(size_t)kc * ldb + cc] : b[(size_t)cc * ldb + kc];
-                        rb[set][i][e] = (col < n && kk < k) ? x : 0.0f;
+                        db[i][e] = (col < n && kk < k) ? x : 0.0f;
                     }
                 }
             }
         }
     };
-    auto swrite = [&](int buf, int set) __attribute__((always_inline)) {
+    auto gload = [&](auto path, int t, int set, auto head) __attribute__((always_inline)) {
+        gload_to(path, t, ra[set], rb[set], head);
+    };
+    auto swrite_from = [&](int buf, const f32x4 (&da)[G::LA], const f32x4 (&db)[G::LB])
+        __attribute__((always_inline)) {
         float* s = lds + buf * G::STAGE;
 #pragma unroll
         for (int i = 0; i < G::LA; ++i)
-            if (G::A_CHUNKS % NT == 0 || tid + i * NT < G::A_CHUNKS) {
-                *reinterpret_cast<f32x4*>(s + a_lds[i]) = ra[set][i];  // a row of A or of A^T
+            if (G::A_CHUNKS % LT == 0 || ltid + i * LT < G::A_CHUNKS) {
+                *reinterpret_cast<f32x4*>(s + a_lds[i]) = da[i];  // a row of A or of A^T
             }
 #pragma unroll
         for (int i = 0; i < G::LB; ++i)
-            if (G::B_CHUNKS % NT == 0 || tid + i * NT < G::B_CHUNKS) {
-                *reinterpret_cast<f32x4*>(s + b_lds[i]) = rb[set][i];  // a row of B or of B^T
+            if (G::B_CHUNKS % LT == 0 || ltid + i * LT < G::B_CHUNKS) {
+                *reinterpret_cast<f32x4*>(s + b_lds[i]) = db[i];  // a row of B or of B^T
             }
     };
+    auto swrite = [&](int buf, int set) __attribute__((always_inline)) { swrite_from(buf, ra[set], rb[set]); };
 
     // ---- LDS -> MFMA operand addresses ----
     const int r = lane % AT::M;  // row (A) / column (B) inside the atom
@@ -803,6 +836,17 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             for (int i = 0; i < WT0; ++i)
 #pragma unroll
                 for (int jn = 0; jn < WT1; ++jn) acc[i][jn] = AT::mfma(f.a[j][i], f.b[jn][j], acc[i][jn]);
+    };
+    // the k steps [j0, j1) of mfma_frag
+    auto mfma_frag_part = [&](const Frag& f, int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j)
+            if (j >= j0 && j < j1) {
+#pragma unroll
+                for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                    for (int jn = 0; jn < WT1; ++jn) acc[i][jn] = AT::mfma(f.a[j][i], f.b[jn][j], acc[i][jn]);
+            }
     };
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const float* s = lds + buf * G::STAGE;
@@ -918,8 +962,151 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             }
         }
     };
+#if SG_WS
+    // ---- wave-specialised K loop ----
+    // The loading waves copy K tiles into the NBUF LDS buffers; the computing
+    // waves only read LDS and multiply.  No work-group barrier inside the
+    // loop: two LDS counters per buffer order the roles.  ready[b] counts the
+    // loading waves that have written buffer b's current tile (NLW per tile),
+    // done[b] the computing waves that have finished reading it (CWAVES per
+    // tile).  Tile t -- round r = t / NBUF of buffer b = t % NBUF -- may be
+    // read once ready[b] >= NLW * (r + 1), and buffer b may take tile t +
+    // NBUF once done[b] >= CWAVES * (r + 1).  LDS serves one wave's accesses
+    // in issue order, so a count raised after a wave's writes (or reads) is
+    // seen by another wave only after them; compiler barriers keep that
+    // order in the code.  A wait gives up after a bounded number of polls:
+    // a broken count would end the loop with wrong values, never hang.
+    {
+        constexpr int NLW = G::NT / 64 - G::CWAVES;
+        static_assert(NLW > 0, "wave specialisation needs loading waves");
+        __shared__ uint32_t ws_count[2 * NBUF];
+        uint32_t* const ready = ws_count;
+        uint32_t* const done = ws_count + NBUF;
+        if (tid < 2 * NBUF) ws_count[tid] = 0u;
+        __syncthreads();
+        auto wait_at_least = [&](uint32_t* cnt, uint32_t target) __attribute__((always_inline)) {
+            for (uint32_t poll = 0; poll < (1u << 22); ++poll) {
+                const uint32_t v = __builtin_amdgcn_readfirstlane(
+                    __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (v >= target) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            asm volatile("" ::: "memory");
+        };
+        // One LDS add per wave, by lane 0 alone, without a branch: EXEC is
+        // narrowed to lane 0 around the ds_add_u32 (the low 32 bits of a
+        // pointer into LDS are its LDS address).  The asm is also a compiler
+        // barrier: the wave's LDS accesses before it stay before it.
+        auto raise = [&](uint32_t* cnt) __attribute__((always_inline)) {
+            const uint32_t addr = (uint32_t)reinterpret_cast<uintptr_t>(cnt);
+            uint64_t saved;
+            asm volatile(
+                "s_mov_b64 %0, exec\n\t"
+                "s_mov_b64 exec, 1\n\t"
+                "s_nop 1\n\t"
+                "ds_add_u32 %1, %2\n\t"
+                "s_mov_b64 exec, %0"
+                : "=&s"(saved)
+                : "v"(addr), "v"(1u)
+                : "memory");
+        };
+        if (loader_wave) {
+            // P register sets: the loads of tiles t + 1 .. t + P - 1 are in
+            // flight while tile t waits for its buffer and is written
+            constexpr int P = SG_WS_PD;
+            static_assert(P >= 2 && P <= 4, "2 to 4 register sets per loading wave");
+            f32x4 wa[P][G::LA], wb[P][G::LB];
+            auto produce = [&](auto path) __attribute__((always_inline)) {
+                // lcm(NBUF, P): buffer and register set are compile-time per step
+                constexpr int U = (NBUF % P == 0) ? NBUF : ((P % NBUF == 0) ? P : NBUF * P);
+                if (ktiles > 0) {
+                    if (kshift != 0u) gload_to(path, 0, wa[0], wb[0], Head{});
+                    else gload_to(path, 0, wa[0], wb[0], NoHead{});
+                }
+#pragma unroll
+                for (int j = 1; j < P; ++j)
+                    if (j < ktiles) gload_to(path, j, wa[j], wb[j], NoHead{});
+                for (int t0 = 0; t0 < ktiles; t0 += U) {
+#pragma unroll
+                    for (int uu = 0; uu < U; ++uu) {
+                        const int t = t0 + uu;
+                        if (t < ktiles) {
+                            const int u = uu % NBUF, set = uu % P;
+                            if (t >= NBUF) wait_at_least(&done[u], (uint32_t)(G::CWAVES * (t / NBUF)));
+                            swrite_from(u, wa[set], wb[set]);
+                            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                            raise(&ready[u]);
+                            if (t + P < ktiles) gload_to(path, t + P, wa[set], wb[set], NoHead{});
+                        }
+                    }
+                }
+            };
+            if (slow) produce(SlowPath{});
+            else produce(FastPath{});
+            __syncthreads();  // pairs with the computing waves' barrier below
+            return;
+        }
+        constexpr int NMFMA = KPL * WT0 * WT1;
+        constexpr int NREAD_A = TA ? WT0 * (KPL >= 4 ? KPL / 4 : 1) : (WT0 >= 4 ? KPL * (WT0 / 4) : (KPL + 1) / 2);
+        constexpr int NREAD_B = TB ? (WT1 >= 4 ? KPL * (WT1 / 4) : (KPL + 1) / 2) : WT1 * (KPL >= 4 ? KPL / 4 : 1);
+        constexpr int NREAD = NREAD_A + NREAD_B;
+        Frag cur, nxt;
+#ifdef SG_WS_AGPR_HINT
+        { float z = 0.0f; asm volatile("; accumulators may live in AGPRs" : "+a"(z)); acc[0][0][0] += z; }
+#endif
+        if (ktiles > 0) {
+            wait_at_least(&ready[0], (uint32_t)NLW);
+            load_frag(lds, 0, cur);
+        }
+        for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                const int t = t0 + u;
+                if (t < ktiles) {
+                    const float* sb = lds + u * G::STAGE;
+                    const int un = (u + 1) % NBUF;
+                    const uint32_t need = (uint32_t)(NLW * ((t + 1) / NBUF + 1));
+                    // the next buffer's count, read a tile ahead of its use
+                    const uint32_t seen = __hip_atomic_load(&ready[un], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        if (kb + 1 < NKB) {
+                            load_frag(sb, kb + 1, nxt);
+                        } else {
+                            // the next tile's first operands; branch-free past
+                            // the last tile (a valid buffer whose values go
+                            // unused), only the rare wait is conditional
+                            if (__builtin_expect(t + 1 < ktiles && __builtin_amdgcn_readfirstlane(seen) < need, 0))
+                                wait_at_least(&ready[un], need);
+                            asm volatile("" ::: "memory");
+                            load_frag(lds + un * G::STAGE, 0, nxt);
+                        }
+                        if (kb + 1 < NKB) {
+                            mfma_frag(cur);
+                        } else {
+                            // the last block's operands are in registers: buffer u is
+                            // free once half its MFMAs are issued (the signal then
+                            // sits between MFMAs, not at the tile boundary)
+                            mfma_frag_part(cur, 0, KPL / 2);
+                            raise(&done[u]);
+                            mfma_frag_part(cur, KPL / 2, KPL);
+                        }
+                        // the first block also carries the early read of the next count
+                        if constexpr (SG_PLR >= 3) {
+                            if (kb == 0) interleave_block<NMFMA, NREAD + 1, 0, 0>();
+                            else interleave_block<NMFMA, NREAD, 0, 0>();
+                        }
+                        cur = nxt;
+                    }
+                }
+            }
+        }
+        __syncthreads();  // every computing wave is past the K buffers: the epilogue reuses them
+    }
+#else
     if (slow) kloop(SlowPath{});
     else kloop(FastPath{});
+#endif
 
     if (fx.kind != FIX_NONE) {
         // ---- publish the partial; the last arrival combines ----
@@ -1037,10 +1224,11 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // SG_GW (the reference's global-write flavour, generator.py:2290-2508):
     // 1 stages through LDS as above when the chunks fit, 0 always stores
     // straight from the accumulators (no LDS, fewer live registers)
-    if constexpr (SG_GW != 0 && (NT / 64) * E_CHUNK <= G::LDS_FLOATS) {
+    if constexpr (SG_GW != 0 && G::CWAVES * E_CHUNK <= G::LDS_FLOATS) {
         {
             // every wave's last K-loop access to LDS is behind this barrier
-            __syncthreads();
+            // (the wave-specialised loop ends with that barrier itself)
+            if constexpr (!SG_WS) __syncthreads();
             float* e = lds + wave * E_CHUNK;
             // Buffer descriptors over the wave's sub-tile of D and of C (SN
             // columns of SM rows from (wrow, wcol)), cut at the matrix's last

@@ -31,9 +31,9 @@ def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1, stk=0, stk_rounds=0):
+def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1, stk=0, stk_rounds=0, ws=0, ws_pd=2):
     return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk,
-                             stream_k=stk, stream_k_rounds=stk_rounds)
+                             stream_k=stk, stream_k_rounds=stk_rounds, ws=ws, ws_pd=ws_pd)
 
 
 # name -> (config, optimizations)
@@ -83,6 +83,12 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     # 128 x 4096: 122.5 against 111.0)
     "mt128x64_a16_wg2x4_dk64": (_cfg(MFMA_16x16x4, (2, 4), (4, 1), 64), _opt(plr=3, sk=0, stk=1)),
     "mt64x128_a32_wg1x4_dk16_s3": (_cfg(MFMA_32x32x2, (1, 4), (2, 1), 16, stages=2), _opt(wgm=4, plr=3, xcd=8)),
+    # wave specialisation of the 1024^3 geometry: four computing waves, four
+    # loading waves, four LDS buffers ordered by LDS counters (no barrier per
+    # K tile).  Measured 2-3% behind the barrier-synchronised instance at
+    # 1024^3 and at 1024 x 1024 x 4096, so select() never picks it.
+    "mt64x64_a16_wg1x4_dk32_s4_ws": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=3),
+                                     _opt(wgm=8, plr=3, xcd=8, ws=1, ws_pd=2)),
     # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
     "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
                                        _opt(wgm=4, plr=3, xcd=8, pd=2)),

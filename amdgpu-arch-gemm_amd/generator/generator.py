@@ -134,6 +134,18 @@ class GemmOptimizations:
                        work-group (each tile cut at most once, fixed up by a
                        commutative two-partial sum); the host uses it when a
                        grid would leave a partial last round.
+    * ``ws``        -- (gfx950 only) 1 doubles the work-group with loading
+                       waves (wave specialisation): the configured waves only
+                       read LDS and multiply, and as many more waves copy K
+                       tiles from memory to LDS, the two roles ordered by LDS
+                       counters instead of a work-group barrier per K tile.
+                       The .toml then describes the launch: wave_group [2 *
+                       WG0, WG1] and wave_tiling [WT0 / 2, WT1] (the same tile,
+                       twice the work-items; WT0 must be even), with the
+                       computing geometry under compute_wave_group /
+                       compute_wave_tiling.  No split-K or stream-K kernel.
+    * ``ws_pd``     -- (with ``ws``) K tiles each loading wave keeps in
+                       flight in registers (2..4).
     * ``stream_k_rounds`` -- (host policy, written to the .toml) the most
                        whole-tile rounds of work-groups for which the host
                        still picks stream-K on its own (0: no limit); tiles
@@ -153,6 +165,8 @@ class GemmOptimizations:
         split_k: Optional[int] = None,
         stream_k: Optional[int] = None,
         stream_k_rounds: Optional[int] = None,
+        ws: Optional[int] = None,
+        ws_pd: Optional[int] = None,
     ):
         self.level = level
         self.wgm = 1
@@ -165,6 +179,8 @@ class GemmOptimizations:
         self.split_k = 1
         self.stream_k = 0
         self.stream_k_rounds = 0
+        self.ws = 0
+        self.ws_pd = 2
         self._setup_optimizations()
         if wgm is not None:
             self.wgm = wgm
@@ -186,6 +202,10 @@ class GemmOptimizations:
             self.stream_k = stream_k
         if stream_k_rounds is not None:
             self.stream_k_rounds = stream_k_rounds
+        if ws is not None:
+            self.ws = ws
+        if ws_pd is not None:
+            self.ws_pd = ws_pd
         if self.wgm < 1:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
@@ -202,6 +222,10 @@ class GemmOptimizations:
             raise RuntimeError(f"Invalid stream_k {self.stream_k} (0 or 1)")
         if self.stream_k_rounds < 0:
             raise RuntimeError(f"Invalid stream_k_rounds {self.stream_k_rounds} (0 = no limit)")
+        if self.ws not in (0, 1) or self.ws_pd not in (2, 3, 4):
+            raise RuntimeError(f"Invalid wave specialisation ws={self.ws} ws_pd={self.ws_pd}")
+        if self.ws and (self.split_k != 1 or self.stream_k):
+            raise RuntimeError("wave specialisation (ws=1) builds no split-K or stream-K kernel")
 
     def _setup_optimizations(self):
         if self.level != 0:
@@ -221,11 +245,14 @@ class GemmOptimizations:
             "split_k": int(self.split_k),
             "stream_k": int(self.stream_k),
             "stream_k_rounds": int(self.stream_k_rounds),
+            "ws": int(self.ws),
+            "ws_pd": int(self.ws_pd),
         }
 
     def __repr__(self) -> str:
         return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
-                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, split_k={self.split_k}, stream_k={self.stream_k})")
+                f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, "
+                f"split_k={self.split_k}, stream_k={self.stream_k}, ws={self.ws})")
 
 
 def lds_lane_cycle(lane: int, access_bytes: int, write: bool = False) -> int:
@@ -703,14 +730,16 @@ class GemmSolutionConfig:
         self.wavefront_size = int(d["wavefront_size"])
         self.name = d.get("name", "") or None
         self._validate()
-        if int(d["lds_usage_bytes"]) != self.lds_usage_bytes:
-            raise RuntimeError(
-                f"lds_usage_bytes {d['lds_usage_bytes']} does not match the geometry ({self.lds_usage_bytes})")
+        want = self.lds_usage_bytes + (ws_counter_bytes(self) if d.get("ws") else 0)
+        if int(d["lds_usage_bytes"]) != want:
+            raise RuntimeError(f"lds_usage_bytes {d['lds_usage_bytes']} does not match the geometry ({want})")
         return self
 
     @classmethod
     def from_toml(cls, path: str) -> "GemmSolutionConfig":
         d = read_toml(path)
+        if d.get("ws"):  # a wave-specialised kernel: the config is its computing geometry
+            d = dict(d, wave_group=d["compute_wave_group"], wave_tiling=d["compute_wave_tiling"])
         cfg = cls(d["a_type"], d["b_type"], d["cd_type"], d["scalar_type"], d["mfma"], d["wave_group"],
                   d["wave_tiling"], d["depth_k"], d["trans_a"], d["trans_b"], d.get("vmem_stage", 1))
         return cfg.from_dict(d)
@@ -788,15 +817,38 @@ class GpuContext:
         return self._asm
 
 
+def launch_geometry(config: GemmSolutionConfig, opt: GemmOptimizations) -> Tuple[Tuple[int, int], Tuple[int, int]]:
+    """(wave_group, wave_tiling) the kernel is launched with: the config's,
+    or with wave specialisation twice the waves along M at half the atoms
+    each (same tile; the loading waves make up the second half)."""
+    wg, wt = tuple(config.wave_group), tuple(config.wave_tiling)
+    if not opt.ws:
+        return wg, wt
+    if wt[0] % 2:
+        raise RuntimeError(f"wave specialisation needs an even wave_tiling along M: {wt}")
+    if 2 * wg[0] * wg[1] * config.wavefront_size > MAX_WORKITEMS:
+        raise RuntimeError(f"wave specialisation doubles the work-group past {MAX_WORKITEMS} work-items")
+    return (2 * wg[0], wg[1]), (wt[0] // 2, wt[1])
+
+
+def ws_counter_bytes(config: GemmSolutionConfig) -> int:
+    """Static LDS the wave-specialised K loop adds to the operand buffers: a
+    ready and a done counter (uint32) per buffer."""
+    return 2 * (config.vmem_stage + 1) * 4
+
+
 def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str = "generated_gemm") -> Dict[str, object]:
     pad_a = config.lds_pad_bytes[0] // 4
     pad_b = config.lds_pad_bytes[1] // 4
+    wg, wt = launch_geometry(config, opt)
     return {
         "SG_ATOM_M": config.mfma[0],
-        "SG_WG0": config.wave_group[0],
-        "SG_WG1": config.wave_group[1],
-        "SG_WT0": config.wave_tiling[0],
-        "SG_WT1": config.wave_tiling[1],
+        "SG_WG0": wg[0],
+        "SG_WG1": wg[1],
+        "SG_WT0": wt[0],
+        "SG_WT1": wt[1],
+        "SG_WS": int(opt.ws),
+        "SG_WS_PD": int(opt.ws_pd),
         "SG_DK": config.depth_k,
         "SG_NBUF": config.vmem_stage + 1,
         "SG_WGM": opt.wgm,
@@ -935,6 +987,13 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     d = gemm_config.to_dict()
     if not d["name"]:
         d["name"] = kern_name
+    if opt is not None and opt.ws:
+        # the launch geometry for every runner (the reference's included);
+        # the computing waves' own geometry beside it
+        wg, wt = launch_geometry(gemm_config, opt)
+        d["compute_wave_group"], d["compute_wave_tiling"] = d["wave_group"], d["wave_tiling"]
+        d["wave_group"], d["wave_tiling"] = list(wg), list(wt)
+        d["lds_usage_bytes"] += ws_counter_bytes(gemm_config)  # the code object's whole static LDS
     d["arch"] = arch
     if opt is not None:
         d.update(opt.to_dict())

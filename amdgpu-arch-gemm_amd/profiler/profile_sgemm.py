@@ -15,6 +15,9 @@ tracing, and no pass asks for more than the hardware collects at once):
   4. --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_BUSY_CYCLES
                                      MFMA utilisation and the shader clock
   5. --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE
+  (--issue) --pmc SQ_WAVES SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY
+     SQ_WAIT_INST_LDS SQ_ACTIVE_INST_ANY SQ_INSTS_LDS SQ_INSTS_SALU
+                                     where the waves' cycles go (per wave)
   6./7. FETCH_SIZE and WRITE_SIZE of copy_probe (a plain copy of a known byte
      count), whose ratio to the true bytes scales the SGEMM's counters.
 
@@ -168,6 +171,8 @@ def main():
                     help="untimed runner launches first (default: about 0.1 s of the workload, so the "
                          "engine clock has ramped up before the dispatches the medians describe)")
     ap.add_argument("--cus", type=int, default=256)
+    ap.add_argument("--issue", action="store_true",
+                    help="one more pass: wave cycles, waits and LDS / scalar instructions per wave")
     ap.add_argument("--analyze-only", action="store_true",
                     help="derive the summary from the rocprofv3 output already in --out (no GPU work)")
     args = ap.parse_args()
@@ -196,6 +201,9 @@ def main():
         "mfma": ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_BUSY_CYCLES"],
         "lds": ["SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"],
     }
+    if args.issue:
+        passes["issue"] = ["SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS",
+                           "SQ_ACTIVE_INST_ANY", "SQ_INSTS_LDS", "SQ_INSTS_SALU"]
     values = {}
     for key, counters in passes.items():
         d = os.path.join(args.out, f"pmc_{key}")
@@ -256,7 +264,8 @@ def main():
         "Command (from the repository root on the GPU box):",
         "",
         f"    python amdgpu-arch-gemm_amd/profiler/profile_sgemm.py --kernel {args.kernel} "
-        f"--workload {args.workload} --out {args.out} --summary {os.path.relpath(summary, ROOT)}",
+        f"--workload {args.workload}{' --issue' if args.issue else ''} --out {args.out} "
+        f"--summary {os.path.relpath(summary, ROOT)}",
         "",
         "which runs, each in its own process (`<runner>` = `"
         + " ".join(os.path.relpath(c, ROOT) if os.path.isabs(c) else c for c in runner) + "`):",
@@ -293,8 +302,22 @@ def main():
         f"{traffic / 1e6:.1f} MB ({traffic / alg_bytes:.2f}x the {alg_bytes / 1e6:.1f} MB algorithmic) |",
         f"| HBM bandwidth | {traffic / avg_s / 1e9:.1f} GB/s measured, {alg_bytes / avg_s / 1e9:.1f} GB/s algorithmic "
         f"(peak {HBM_PEAK_GBS:.0f}) |",
-        "",
     ]
+    if args.issue:
+        # per wave, in cycles (the SQ_WAVE_CYCLES / WAIT / ACTIVE counters count quad-cycles)
+        waves = max(med["SQ_WAVES"], 1.0)
+        wc = 4.0 * med["SQ_WAVE_CYCLES"] / waves
+        lines += [
+            f"| waves per dispatch / wave cycles per wave (SQ_WAVES, 4 x SQ_WAVE_CYCLES) | {waves:.0f} / {wc:.0f} |",
+            f"| per wave: waiting for anything / for instruction issue / for LDS issue (4 x SQ_WAIT_ANY, "
+            f"_INST_ANY, _INST_LDS) | {4.0 * med['SQ_WAIT_ANY'] / waves:.0f} / "
+            f"{4.0 * med['SQ_WAIT_INST_ANY'] / waves:.0f} / {4.0 * med['SQ_WAIT_INST_LDS'] / waves:.0f} cycles |",
+            f"| per wave: cycles working on any instruction (4 x SQ_ACTIVE_INST_ANY) | "
+            f"{4.0 * med['SQ_ACTIVE_INST_ANY'] / waves:.0f} |",
+            f"| per wave: LDS / scalar ALU instructions issued (SQ_INSTS_LDS, SQ_INSTS_SALU) | "
+            f"{med['SQ_INSTS_LDS'] / waves:.0f} / {med['SQ_INSTS_SALU'] / waves:.0f} |",
+        ]
+    lines.append("")
     with open(summary, "w") as f:
         f.write("\n".join(lines))
     traffic_path = os.path.join(os.path.dirname(os.path.abspath(summary)), f"{args.kernel}_{args.workload}_traffic.txt")

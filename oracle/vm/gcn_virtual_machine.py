@@ -261,6 +261,11 @@ class BarrierReached(Exception):
     pass
 
 
+class Yielded(Exception):
+    """A wave gave up its turn (``s_sleep``, or a preemption point) without
+    reaching a barrier: the other waves of its work-group run next."""
+
+
 # ---------------------------------------------------------------- the VM
 class GcnVirtualMachine:
     """One wave's architectural state plus the memories it sees."""
@@ -430,12 +435,16 @@ class GcnVirtualMachine:
         while not self.done:
             try:
                 self.step(prog, max_instructions)
-            except BarrierReached:
-                continue  # a lone wave passes its barriers
+            except (BarrierReached, Yielded):
+                continue  # a lone wave passes its barriers and keeps its turns
         return self
 
-    def step(self, prog: "Program", max_instructions: int = 10_000_000):
-        """Executes until s_endpgm (sets done) or an s_barrier (raises BarrierReached)."""
+    def step(self, prog: "Program", max_instructions: int = 10_000_000,
+             preempt: Optional[Callable[[], bool]] = None):
+        """Executes until s_endpgm (sets done), an s_barrier (raises
+        BarrierReached) or an s_sleep (raises Yielded).  ``preempt``, called
+        after every instruction, can end the turn early (raises Yielded): a
+        seeded random one explores interleavings of the waves' LDS accesses."""
         insts = prog.insts
         while True:
             if self.pc >= len(insts):
@@ -457,6 +466,8 @@ class GcnVirtualMachine:
                 return
             if r == "barrier":
                 raise BarrierReached()
+            if r == "yield" or (preempt is not None and preempt()):
+                raise Yielded()
 
     def drain(self):
         for q in self.pending.values():
@@ -775,9 +786,14 @@ def _s_barrier(vm, ins, prog):
     return "barrier"
 
 
-@op("s_nop", "s_setprio", "s_sleep", "s_sched_barrier", "s_code_end")
+@op("s_nop", "s_setprio", "s_sched_barrier", "s_code_end")
 def _s_nop(vm, ins, prog):
     return None
+
+
+@op("s_sleep")
+def _s_sleep(vm, ins, prog):
+    return "yield"  # a polling wave lets the others of its work-group run
 
 
 @op("s_waitcnt")
@@ -1357,6 +1373,22 @@ def _ds_write2(dwords_each, scale):
 for _nd, _sfx in ((1, "b32"), (2, "b64"), (3, "b96"), (4, "b128")):
     _DISPATCH[f"ds_read_{_sfx}"] = _ds_read(_nd)
     _DISPATCH[f"ds_write_{_sfx}"] = _ds_write(_nd)
+
+
+@op("ds_add_u32")
+def _ds_add_u32(vm, ins, prog):
+    """LDS atomic add without return: the active lanes' values are added in
+    lane order (32-bit wrap-around), visible to later accesses at once."""
+    addr_op, src = ins.ops[0], ins.ops[1]
+    mask = vm.exec_mask()
+    if mask.any():
+        addr = vm.rv32(addr_op).astype(np.int64) + ins.mods.get("offset", 0)
+        vals = vm.regfile(src)[src.index]
+        for lane in np.nonzero(mask)[0]:
+            a = np.array([addr[lane]])
+            cur = int(vm.lds.read_u32(a, 1, str(ins))[0, 0])
+            vm.lds.write_u32(a, np.array([[(cur + int(vals[lane])) & MASK32]], dtype=np.uint32), str(ins))
+    vm.pending["lgkmcnt"].append(lambda: None)
 _DISPATCH["ds_read2_b32"] = _ds_read2(1, 1)
 _DISPATCH["ds_read2_b64"] = _ds_read2(2, 1)
 _DISPATCH["ds_read2st64_b32"] = _ds_read2(1, 64)
@@ -1370,11 +1402,19 @@ _DISPATCH["ds_write2st64_b64"] = _ds_write2(2, 64)
 # ------------------------------------------------------------ dispatching
 def run_kernel(program, grid: Tuple[int, ...], workgroup_size: int, kernargs: bytes, vmem: Memory,
                max_instructions: int = 50_000_000, on_workgroup: Optional[Callable] = None,
-               order: Optional[Sequence[Tuple[int, int, int]]] = None) -> int:
+               order: Optional[Sequence[Tuple[int, int, int]]] = None,
+               preempt_seed: Optional[int] = None, preempt_rate: float = 1.0 / 16) -> int:
     """Runs every work-group of a grid (x fastest, then y, then z), each with
-    its waves interleaved at barriers; returns the number of instructions
-    executed.  ``order`` lists the (x, y, z) work-groups in the order to run
-    them instead (each exactly once)."""
+    its waves taking turns: a wave runs until it reaches a barrier (released
+    once every live wave of the work-group waits there), yields at an
+    ``s_sleep`` or ends; returns the number of instructions executed.
+    ``order`` lists the (x, y, z) work-groups in the order to run them
+    instead (each exactly once).  With ``preempt_seed`` a wave also loses its
+    turn after any instruction with probability ``preempt_rate`` (seeded),
+    so that waves synchronising through LDS are checked under many
+    interleavings, not just the one the turn order gives."""
+    rng = np.random.default_rng(preempt_seed) if preempt_seed is not None else None
+    preempt = (lambda: rng.random() < preempt_rate) if rng is not None else None
     prog = as_program(program)
     desc = prog.desc
     if not desc.get("amdhsa_user_sgpr_kernarg_segment_ptr", 0):
@@ -1422,17 +1462,23 @@ def run_kernel(program, grid: Tuple[int, ...], workgroup_size: int, kernargs: by
             vm.reset_wave()
             waves.append(vm)
         budget = max_instructions
+        at_barrier = [False] * len(waves)
         while not all(vm.done for vm in waves):
-            for vm in waves:
-                if vm.done:
+            for i, vm in enumerate(waves):
+                if vm.done or at_barrier[i]:
                     continue
                 try:
-                    vm.step(prog, budget)
+                    vm.step(prog, budget, preempt)
                 except BarrierReached:
+                    at_barrier[i] = True
+                except Yielded:
                     pass
-            live = [vm for vm in waves if not vm.done]
-            if live and len(live) != len(waves):
+            live = [i for i, vm in enumerate(waves) if not vm.done]
+            waiting = [i for i in live if at_barrier[i]]
+            if waiting and len(live) != len(waves):
                 raise RuntimeError("a wave ended while others wait at a barrier")
+            if live and len(waiting) == len(live):
+                at_barrier = [False] * len(waves)  # every live wave arrived: release
         total += sum(vm.executed for vm in waves)
         if on_workgroup:
             on_workgroup(wx, wy, waves)
@@ -1463,7 +1509,8 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
               C: Optional[np.ndarray] = None, alpha: float = 1.0, beta: float = 0.0,
               mnk: Optional[Tuple[int, int, int]] = None, ldd: Optional[int] = None,
               splits: int = 0, order: Optional[Sequence[Tuple[int, int, int]]] = None,
-              misalign: int = 0, stream_k: Optional[Tuple[int, int]] = None) -> Tuple[np.ndarray, Dict]:
+              misalign: int = 0, stream_k: Optional[Tuple[int, int]] = None,
+              preempt_seed: Optional[int] = None) -> Tuple[np.ndarray, Dict]:
     """Runs a compiled SGEMM kernel on column-major A, B, C.
 
     Without ``mnk`` the problem is A (m x k) @ B (k x n) with tight leading
@@ -1528,7 +1575,7 @@ def run_sgemm(program, tile: Tuple[int, int], workitems: int, A: np.ndarray, B: 
     else:
         grid = (nwgx, nwgy)
         prog = as_program(program)
-    count = run_kernel(prog, grid, workitems, ka, mem, order=order)
+    count = run_kernel(prog, grid, workitems, ka, mem, order=order, preempt_seed=preempt_seed)
     D = np.frombuffer(mem.read_bytes(offs[3], ldd * n * 4), dtype=np.float32).reshape(n, ldd).T.copy()
     if mnk is None:
         D = D[:m, :]

@@ -335,6 +335,38 @@ def test_split_k_knob_validation():
     assert g.kernel_defines(cfg(), g.GemmOptimizations(1))["SG_SPLITK"] == 0
 
 
+def test_wave_specialisation_knob():
+    """ws = 1 launches twice the waves along M at half the atoms each (same
+    tile), the template's SG_WS halves them back into computing waves; it
+    excludes split-K and stream-K, needs an even WT0, and its .toml gives the
+    launch geometry with the computing one beside it."""
+    c = cfg((16, 16, 1, 4), (1, 4), (4, 1), 32, stages=3)
+    o = g.GemmOptimizations(1, plr=3, ws=1, ws_pd=3)
+    d = g.kernel_defines(c, o)
+    assert (d["SG_WG0"], d["SG_WG1"], d["SG_WT0"], d["SG_WT1"], d["SG_WS"], d["SG_WS_PD"]) == (2, 4, 2, 1, 1, 3)
+    assert g.launch_geometry(c, o) == ((2, 4), (2, 1))
+    assert g.launch_geometry(c, g.GemmOptimizations(1)) == ((1, 4), (4, 1))
+    assert g.kernel_defines(c, g.GemmOptimizations(1))["SG_WS"] == 0
+    for bad in (dict(ws=2), dict(ws=1, ws_pd=1), dict(ws=1, ws_pd=5), dict(ws=1, split_k=0), dict(ws=1, stream_k=1)):
+        with pytest.raises(RuntimeError):
+            g.GemmOptimizations(1, **bad)
+    with pytest.raises(RuntimeError, match="even wave_tiling"):
+        g.kernel_defines(cfg((16, 16, 1, 4), (1, 4), (1, 1), 32), o)
+    with pytest.raises(RuntimeError, match="past 1024"):
+        g.kernel_defines(cfg((16, 16, 1, 4), (4, 4), (2, 1), 32), o)
+    assert g.ws_counter_bytes(c) == 2 * 4 * 4
+
+
+def test_wave_specialised_catalog_toml(kernels):
+    name = "mt64x64_a16_wg1x4_dk32_s4_ws"
+    d = g.read_toml(catalog.paths(name)[1])
+    assert d["ws"] == 1 and d["wave_group"] == [2, 4] and d["wave_tiling"] == [2, 1]
+    assert d["compute_wave_group"] == [1, 4] and d["compute_wave_tiling"] == [4, 1]
+    assert d["lds_bytes_compiled"] == d["lds_usage_bytes"] == 4 * (64 * 32 + 64 * 32) * 4 + 32
+    back = g.GemmSolutionConfig.from_toml(catalog.paths(name)[1])
+    assert back.wave_group == (1, 4) and back.wave_tiling == (4, 1) and back.tile_size == (64, 64)
+
+
 def test_auto_split_known_answers():
     """The per-problem split rule at the shapes it was calibrated on (MI355X,
     256 CUs): the best measured split counts lie where tiles x splits just

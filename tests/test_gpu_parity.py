@@ -456,6 +456,39 @@ def test_baseline_config(kernels, cid, m, n, k, seed, dist):
          f"|gpu - cpu| >= 1e-3 at {mismatches} of {m * n}, max |gpu - cpu| {float(np.max(np.abs(D - ref))):.3e}")
 
 
+# ----------------------------------------------------- wave specialisation
+WS_CASES = [
+    # (m, n, k): the 4-buffer ring wraps many times, K remainders (a head
+    # tile), edge tiles in M and N, a single K tile, k below one K tile
+    (1024, 1024, 1024), (333, 290, 5003), (64, 64, 32), (130, 70, 100), (2048, 64, 31), (1000, 999, 4097),
+]
+
+
+@pytest.mark.parametrize("m,n,k", WS_CASES)
+def test_wave_specialised_instance_equals_its_barrier_twin(kernels, m, n, k):
+    """The wave-specialised instance (loading waves, LDS counters, no barrier
+    per K tile) runs the same MFMA sequence per output as the
+    barrier-synchronised instance of the same computing geometry, so D is
+    bit-identical to it -- and to itself over repeated launches -- and within
+    the bar of the oracle."""
+    ws, twin = "mt64x64_a16_wg1x4_dk32_s4_ws", "mt64x64_a16_wg1x4_dk32_s3"
+    _say(f"wave-specialised {ws} vs {twin} {m}x{n}x{k}")
+    A = S.fill_matrix(m, k, 29, 0)
+    B = S.fill_matrix(k, n, 29, 1)
+    C = S.fill_matrix(m, n, 29, 2)
+    with _kernel(ws) as kw, _kernel(twin) as kt:
+        kt.set_split_k(1)    # the twin unsplit, so that its sums run in the same order
+        kt.set_stream_k(0)
+        assert kw.info.workitems == 2 * kt.info.workitems and kw.tile[:2] == kt.tile[:2]
+        assert kw.launch_splits(m, n, k) == 1
+        D1, _ = kw.run(A, B, C, m, n, k, alpha=0.5, beta=-1.5, warmup=0, runs=1)
+        D2, _ = kw.run(A, B, C, m, n, k, alpha=0.5, beta=-1.5, warmup=2, runs=5)
+        Dt, _ = kt.run(A, B, C, m, n, k, alpha=0.5, beta=-1.5, warmup=0, runs=1)
+    assert np.array_equal(D1, D2), "repeated launches differ"
+    assert np.array_equal(D1, Dt), "the wave-specialised result differs from its barrier twin"
+    _check(D1, oracle.cpu_gemm_blocked(A, B, C, 0.5, -1.5, threads=16), k, ws)
+
+
 # ----------------------------------------------------------------- split-K
 SPLIT_CASES = [
     # (instance, m, n, k, splits); 0 = the per-problem choice of the host library

@@ -202,3 +202,21 @@ def test_wide_space_reaches_the_eight_wave_instances(name, occs, depths):
     keys = {T.point_key(c, o) for c, o in T.knob_points(stage1[0], split_ks=(opt.split_k,), occs=(opt.occ,),
                                                           gws=(opt.gw,))}
     assert T.point_key(cfg, opt) in keys, name
+
+
+def test_stage2_wave_specialisation_points():
+    """--ws 0,1 adds wave-specialised stage-2 points: no split-K, no
+    occupancy cap, a fourth LDS buffer only with them, and keys that tell
+    them apart; geometries with odd WT0 get none."""
+    from generator.generator import GemmSolutionConfig, MFMA_16x16x4
+    base = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (1, 4), (4, 1), 32, False, False, vmem_stage=2)
+    pts = list(T.knob_points(base, split_ks=(1, 0), occs=(0, 2), gws=(1,), wss=(0, 1)))
+    ws = [(c, o) for c, o in pts if o.ws]
+    assert ws and all(o.split_k == 1 and o.occ == 0 and o.pd == 1 for _, o in ws)
+    assert {c.vmem_stage for c, _ in ws} == {1, 2, 3}
+    assert all(c.vmem_stage < 3 for c, o in pts if not o.ws)
+    keys = [T.point_key(c, o) for c, o in pts]
+    assert len(keys) == len(set(keys)) and all("_ws" in T.point_key(c, o) for c, o in ws)
+    odd = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (2, 2), (1, 2), 32, False, False, vmem_stage=2)
+    assert not [o for _, o in T.knob_points(odd, wss=(1,)) if o.ws]
+

@@ -867,3 +867,92 @@ def test_unknown_instruction_fails_loudly():
     vm = GcnVirtualMachine(104, 256, 64)
     with pytest.raises(NotImplementedError, match="v_frobnicate"):
         vm.run("generated_gemm:\n v_frobnicate v0, v1\n s_endpgm\n")
+
+
+# ------------------------------------------------------ wave specialisation
+WS_NAME = "mt64x64_a16_wg1x4_dk32_s4_ws"
+
+
+def _ws_workitems(name):
+    cfg, opt = catalog.SOLUTIONS[name]
+    wg, _ = g.launch_geometry(cfg, opt)
+    return wg[0] * wg[1] * 64
+
+
+@pytest.mark.parametrize("seed", [None, 1, 2, 3, 4])
+def test_wave_specialised_kernel_in_vm(seed):
+    """The loading / computing waves of the wave-specialised instance order
+    their LDS buffers with counters only (no barrier per K tile).  In the VM a
+    polling wave yields at s_sleep, and with a seed every wave also loses its
+    turn at random instructions, so the counters are exercised under many
+    interleavings: 7 K tiles (the 4-buffer ring wraps) with a K remainder
+    (a head tile), two tiles, alpha/beta -- every interleaving must give the
+    same bits, within the parity bar of float64."""
+    prog, cfg = program(WS_NAME)
+    m, n, k = 128, 64, 32 * 6 + 5
+    A = oracle.fill_matrix(m, k, 6, 0)
+    B = oracle.fill_matrix(k, n, 6, 1)
+    C = oracle.fill_matrix(m, n, 6, 2)
+    D, info = run_sgemm(prog, cfg.tile_size, _ws_workitems(WS_NAME), A, B, C, 0.5, -1.25, preempt_seed=seed)
+    assert info["grid"] == (2, 1)
+    assert oracle.normwise_error(D, oracle.gemm_f64(A, B, C, 0.5, -1.25)) <= oracle.tolerance(k)
+    D0, _ = run_sgemm(prog, cfg.tile_size, _ws_workitems(WS_NAME), A, B, C, 0.5, -1.25)
+    assert np.array_equal(D, D0)
+
+
+FLAG_PROTOCOL = """
+generated_gemm:
+    v_readfirstlane_b32 s4, v0
+    s_cmp_ge_u32 s4, 64
+    s_cbranch_scc1 .Lwriter
+    v_mov_b32 v1, 0
+.Lpoll:
+    ds_read_b32 v2, v1
+    s_waitcnt lgkmcnt(0)
+    v_readfirstlane_b32 s5, v2
+    s_cmp_eq_u32 s5, 1
+    s_cbranch_scc1 .Lgot
+    s_sleep 1
+    s_branch .Lpoll
+.Lgot:
+    ds_read_b32 v3, v1 offset:4
+    s_waitcnt lgkmcnt(0)
+    ds_write_b32 v1, v3 offset:8
+    s_endpgm
+.Lwriter:
+    v_mov_b32 v1, 0
+    v_mov_b32 v2, 42
+    v_mov_b32 v3, 1
+    {first}
+    {second}
+    s_endpgm
+.Lfunc_end0:
+.amdhsa_kernel generated_gemm
+    .amdhsa_group_segment_fixed_size 16
+    .amdhsa_user_sgpr_count 2
+    .amdhsa_user_sgpr_kernarg_segment_ptr 1
+    .amdhsa_system_sgpr_workgroup_id_x 1
+.end_amdhsa_kernel
+"""
+
+
+def _flag_protocol_result(data_first, seed):
+    data, flag = "ds_write_b32 v1, v2 offset:4", "ds_write_b32 v1, v3"
+    asm = FLAG_PROTOCOL.format(first=data if data_first else flag, second=flag if data_first else data)
+    seen = []
+    V.run_kernel(asm, (1, 1), 128, b"\0" * 8, V.Memory(64, "vmem"), preempt_seed=seed, preempt_rate=0.25,
+                 on_workgroup=lambda x, y, waves: seen.append(int(waves[0].lds.read_u32(np.array([8]), 1, "")[0, 0])))
+    return seen[0]
+
+
+def test_vm_preemption_catches_a_flag_raised_before_its_data():
+    """The checker behind the test above: wave 1 writes a value and raises a
+    flag, wave 0 polls the flag and copies the value.  With the flag raised
+    after the data every interleaving copies 42; raised before it, the turn
+    order alone still copies 42 (the writer is never interrupted), but
+    random preemption finds interleavings that copy the stale 0."""
+    assert all(_flag_protocol_result(True, s) == 42 for s in [None] + list(range(200)))
+    assert _flag_protocol_result(False, None) == 42
+    stale = [s for s in range(200) if _flag_protocol_result(False, s) == 0]
+    assert stale, "no interleaving put the reader between the writer's two writes"
+
