@@ -906,10 +906,6 @@ def gemm(
     return src
 
 
-def _offload_arch(arch: str) -> str:
-    return arch
-
-
 def compile_to_assembly(kern_str: str, arch: str = "gfx950") -> str:
     """AMD assembly of a generated kernel (this project's own build)."""
     with tempfile.TemporaryDirectory() as tmp:
@@ -917,7 +913,7 @@ def compile_to_assembly(kern_str: str, arch: str = "gfx950") -> str:
         out = os.path.join(tmp, "k.s")
         with open(src, "w") as f:
             f.write(kern_str)
-        cmd = [DEFAULT_HIPCC_PATH, "-S", "--cuda-device-only", f"--offload-arch={_offload_arch(arch)}",
+        cmd = [DEFAULT_HIPCC_PATH, "-S", "--cuda-device-only", f"--offload-arch={arch}",
                *HIPCC_KERNEL_FLAGS, src, "-o", out]
         ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
         if ret.returncode:
@@ -974,7 +970,7 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     tmp_co = co_path + ".tmp"
     # a plain amdhsa ELF code object (no offload bundle), like the reference's .co
     cmd = [DEFAULT_HIPCC_PATH, "--cuda-device-only", "-c", "--no-gpu-bundle-output",
-           f"--offload-arch={_offload_arch(arch)}", *HIPCC_KERNEL_FLAGS,
+           f"--offload-arch={arch}", *HIPCC_KERNEL_FLAGS,
            "-Rpass-analysis=kernel-resource-usage", src_path, "-o", tmp_co]
     ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
     if ret.returncode:
