@@ -227,6 +227,32 @@ def test_bad_leading_dimension_is_an_error_not_a_launch(kernels):
             assert msg and ("below 2^31" in msg or "too large" in msg), (m, n, k, msg)
 
 
+def test_overlapping_buffers_are_refused_before_a_launch(kernels):
+    """Tiles store D while other tiles still read A, B and C: D sharing bytes
+    with A or B, or with C other than as the very same matrix, is refused
+    (SGEMM_E_INVALID) on both launch entry points, and D is left untouched."""
+    name = "mt64x64_a16_wg1x4_dk32_s3"
+    m = n = k = 128
+    buf = S.DeviceBuffer(4 * (4 * m * n + 64))
+    A, B, C = buf.view(0, 4 * m * k), buf.view(4 * m * k, 4 * k * n), buf.view(8 * m * n, 4 * m * n)
+    D = buf.view(12 * m * n, 4 * m * n)
+    buf.upload(np.full(4 * m * n + 64, 1.0, dtype=np.float32))
+    with _kernel(name) as kern:
+        for entry in ("launch", "launch_noalloc"):
+            go = getattr(kern, entry)
+            for dd, cc, beta, kw in ((A, C, 0.0, {}),                              # D over A
+                                     (buf.view(4 * m * k + 4, 4 * m * n), C, 0.0, {}),  # D over B
+                                     (buf.view(8 * m * n + 4, 4 * m * n), C, 1.0, {}),  # D shifted over C
+                                     (C, C, 1.0, {"ldd": m + 1})):                 # C == D, ldc != ldd
+                with pytest.raises(S.SgemmError, match="overlap"):
+                    go(A, B, cc, dd, m, n - 1 if kw else n, k, alpha=1.0, beta=beta, **kw)
+            # beta = 0: C is not read, so D may overlap it; in place (C == D) is fine too
+            go(A, B, buf.view(12 * m * n + 4, 4 * m * n - 4), D, m, n, k, alpha=1.0, beta=0.0)
+            go(A, B, C, C, m, n, k, alpha=1.0, beta=0.0)
+        kern.synchronize()
+    assert np.all(D.download() == np.float32(k))
+
+
 EDGE_SHAPES = [
     # (instance, m, n, k, pad): edge tiles in M and N, K remainders, k < DK, odd leading dims
     ("mt256x256_a32_wg2x2_dk16_s3", 1000, 999, 1001, 0),
