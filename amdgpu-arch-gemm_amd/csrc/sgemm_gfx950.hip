@@ -146,6 +146,9 @@
 #ifndef SG_WS_PD
 #define SG_WS_PD 2
 #endif
+#ifndef SG_KSPLIT
+#define SG_KSPLIT 0
+#endif
 #ifndef SG_KERNEL_NAME
 #define SG_KERNEL_NAME generated_gemm
 #endif
@@ -211,19 +214,25 @@ template <> struct Atom<16> {
 // wave_group / wave_tiling: NT work-items, an MT0 x MT1 tile).  With WS (wave
 // specialisation) the first half of the waves along M computes the whole tile
 // -- WG0 / 2 x WG1 waves of 2 * WT0 x WT1 atoms -- and the other half only
-// moves K tiles from memory to LDS; otherwise every wave does both.
+// moves K tiles from memory to LDS.  With KS (K split inside the work-group)
+// each half is a group of that shape that loads and multiplies half of the K
+// tiles of the whole tile in an LDS ring of its own; the groups' sums meet in
+// LDS.  Otherwise every wave does both jobs for the whole K range.
 template <int AM, int WG0, int WG1, int WT0, int WT1, int DK, int NBUF, int PAD_A, int PAD_B, bool TA, bool TB,
-          bool WS>
+          bool WS, bool KS>
 struct Geometry {
     typedef Atom<AM> atom;
     static constexpr int NT = WG0 * WG1 * 64;
     static constexpr int MT0 = atom::M * WG0 * WT0;
     static constexpr int MT1 = atom::N * WG1 * WT1;
-    static constexpr int CWG0 = WS ? WG0 / 2 : WG0;   // computing waves along M
-    static constexpr int CWT0 = WS ? WT0 * 2 : WT0;   // their atoms along M
-    static constexpr int CWAVES = CWG0 * WG1;         // computing waves
-    static constexpr int CNT = CWAVES * 64;           // their work-items
-    static constexpr int LT = WS ? NT - CNT : NT;     // work-items that load K tiles
+    static constexpr bool HALVES = WS || KS;            // the waves split into two halves along M
+    static constexpr int CWG0 = HALVES ? WG0 / 2 : WG0;  // computing waves along M (of one group)
+    static constexpr int CWT0 = HALVES ? WT0 * 2 : WT0;  // their atoms along M
+    static constexpr int CWAVES = CWG0 * WG1;            // computing waves (of one group)
+    static constexpr int CNT = CWAVES * 64;              // their work-items
+    // work-items that load one LDS ring's K tiles: every one, the loading
+    // half (WS) or one group's (KS)
+    static constexpr int LT = WS ? NT - CNT : (KS ? CNT : NT);
     // k values a lane reads per LDS read of B (and MFMA steps per k block)
     static constexpr int KPL = (DK / atom::K >= 4) ? 4 : ((DK / atom::K >= 2) ? 2 : 1);
     static constexpr int KB = atom::K * KPL;
@@ -247,7 +256,8 @@ struct Geometry {
     static_assert(DK % KB == 0, "DK must be a multiple of the k block");
     static_assert(MT0 % 4 == 0, "MT0 must be a multiple of 4");
     static_assert(CWT0 == 1 || CWT0 == 2 || CWT0 == 4 || CWT0 == 8, "WT0 must be 1, 2, 4 or 8");
-    static_assert(!WS || (WG0 % 2 == 0), "wave specialisation halves an even wave group along M");
+    static_assert(!HALVES || (WG0 % 2 == 0), "wave specialisation / the K split halve an even wave group along M");
+    static_assert(!(WS && KS), "wave specialisation and the in-group K split exclude each other");
     static_assert(WT1 >= 1 && WT1 <= 8, "WT1 must be in [1, 8]");
     static_assert(!TB || WT1 == 1 || WT1 == 2 || WT1 == 4 || WT1 == 8, "B^T reads WT1 consecutive floats");
     static_assert(PAD_A % 4 == 0 && PAD_B % 4 == 0, "LDS pads keep 16-byte rows");
@@ -256,8 +266,10 @@ struct Geometry {
 };
 
 typedef Geometry<SG_ATOM_M, SG_WG0, SG_WG1, SG_WT0, SG_WT1, SG_DK, SG_NBUF, SG_PAD_A, SG_PAD_B, SG_TA != 0, SG_TB != 0,
-                 SG_WS != 0> G;
+                 SG_WS != 0, SG_KSPLIT != 0> G;
 static_assert(!SG_WS || (!SG_SPLITK && !SG_STREAMK), "the wave-specialised K loop has no split-K / stream-K variant");
+static_assert(!SG_KSPLIT || (!SG_SPLITK && !SG_STREAMK && SG_MAPK <= 1),
+              "the in-group K split has no split-K / stream-K variant and no K rotation");
 
 // B-tile chunk swizzle of row n (0: rows stored straight).  The XOR stays
 // inside a row when its chunk count is a multiple of MASK + 1, and a lane's
@@ -456,16 +468,24 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     constexpr int LT = G::LT;
     constexpr bool TA = SG_TA != 0, TB = SG_TB != 0;
 
-    __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
-
     const int lane = tid & 63;
     // wave-uniform (a scalar register): the epilogue's buffer descriptors
     // derived from it then need no per-lane waterfall loop
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave % G::CWG0;
-    const int wn = wave / G::CWG0;
+    // with the in-group K split, group 1's waves repeat group 0's layout
+    const int kgrp = SG_KSPLIT ? wave / G::CWAVES : 0;
+    const int cwave = SG_KSPLIT ? wave % G::CWAVES : wave;
+    const int wm = cwave % G::CWG0;
+    const int wn = cwave / G::CWG0;
     const bool loader_wave = SG_WS && wave >= G::CWAVES;
-    const int ltid = SG_WS ? (tid >= G::CNT ? tid - G::CNT : tid % LT) : tid;
+    const int ltid = SG_WS ? (tid >= G::CNT ? tid - G::CNT : tid % LT) : (SG_KSPLIT ? tid % G::CNT : tid);
+#if SG_KSPLIT
+    // one LDS ring per K group; this wave's group's ring
+    __shared__ __attribute__((aligned(16))) float lds_rings[2 * G::LDS_FLOATS];
+    float* const lds = lds_rings + kgrp * G::LDS_FLOATS;
+#else
+    __shared__ __attribute__((aligned(16))) float lds[G::LDS_FLOATS];
+#endif
     const uint32_t row0 = (uint32_t)tx * MT0;
     const uint32_t col0 = (uint32_t)ty * MT1;
 
@@ -502,7 +522,27 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // per dword), the others are in memory.
     const bool edge = row0 + MT0 > m || col0 + MT1 > n;
     const uint32_t kshift = (k % DK) ? DK - k % DK : 0u;
-    const bool slow = kshift != 0u && (SG_MAPK > 1 || ktiles < 2);
+    // the fast path's head tile needs a second K tile in the wave's range: the
+    // clamped prefetch past the range's end reloads its last tile, which must
+    // not be the head (with the in-group K split: per group)
+    const int kt_half = (ktiles + 1) / 2;
+    const bool slow = kshift != 0u && (SG_MAPK > 1 || (SG_KSPLIT ? kt_half : ktiles) < 2);
+    // The K tiles this wave's K loop runs: all ktiles from tile 0, or with the
+    // in-group K split h = ceil(ktiles / 2) each -- group 0 tiles [0, h),
+    // group 1 tiles [ktiles - h, ktiles), so both run the same number of
+    // iterations (and barriers).  For an odd count group 1's first tile is
+    // group 0's last: group 1 loads it as zeros (a head tile whose shift is
+    // the whole tile: its descriptor starts at that tile's first k and every
+    // lane reads there and discards the value).  kshift_h is the head tile's
+    // shift: values of its first kshift_h k load as zeros.  Without the split
+    // kt_count and kshift_h are ktiles and kshift themselves (references), so
+    // the K loop's code is exactly that of a kernel without the knob.
+    const bool upper = SG_KSPLIT && kgrp == 1;
+    const int& kt_count = SG_KSPLIT ? kt_half : ktiles;
+    const int kt_base = upper ? ktiles - kt_half : 0;
+    const bool zero_head = upper && (ktiles & 1) != 0;
+    const uint32_t kshift_up = zero_head ? (uint32_t)DK : 0u;
+    const uint32_t& kshift_h = upper ? kshift_up : kshift;
 
     // ---- global -> VGPR staging (byte offsets inside a K tile) ----
     // Every thread moves float4 chunks.  A chunk runs along the operand's
@@ -602,7 +642,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     static_assert(PD == 1 || PD == 2, "prefetch depth must be 1 or 2");
     f32x4 ra[PD][G::LA], rb[PD][G::LB];
 
-    int kt_first = 0;
+    int kt_first = kt_base;
     if constexpr (SG_MAPK > 1) kt_first = (tx & (SG_MAPK - 1)) % (ktiles > 0 ? ktiles : 1);
 
     // gload_to(tag, t, da, db, head): global -> VGPR copy of K tile t into
@@ -643,9 +683,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             // element by element.
             auto head_load = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t off, int kk, bool along_k,
                                  uint32_t k_bytes) __attribute__((always_inline)) -> f32x4 {
-                if (!along_k || (kshift & 3u) == 0u) {
-                    const bool live = kk >= (int)kshift;
-                    const uint32_t o = off - (live ? kshift : (uint32_t)kk) * k_bytes;
+                if (!along_k || (kshift_h & 3u) == 0u) {
+                    const bool live = kk >= (int)kshift_h;
+                    const uint32_t o = off - (live ? kshift_h : (uint32_t)kk) * k_bytes;
                     const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, 0));
                     return live ? v : z;
                 }
@@ -656,10 +696,10 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                     // the descriptor's first k; written as one max so that no
                     // constant splits off into the instruction's offset field
                     // (the register part alone could be negative)
-                    const int ke = max(kk + e, (int)kshift);
-                    const uint32_t o = off + (uint32_t)(ke - kk - (int)kshift) * 4u;
+                    const int ke = max(kk + e, (int)kshift_h);
+                    const uint32_t o = off + (uint32_t)(ke - kk - (int)kshift_h) * 4u;
                     const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)o, 0, 0));
-                    v[e] = kk + e >= (int)kshift ? x : 0.0f;
+                    v[e] = kk + e >= (int)kshift_h ? x : 0.0f;
                 }
                 return v;
             };
@@ -695,6 +735,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             }
         } else {
             const uint32_t k0 = (uint32_t)kt * DK;
+            // group 1's zero head tile of the in-group K split loads nothing
+            const bool zt = zero_head && kt == kt_base;
 #pragma unroll
             for (int i = 0; i < G::LA; ++i) {
                 const int ch = ltid + i * LT;
@@ -708,7 +750,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         const uint32_t rc = row < m ? row : m - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TA ? a[(size_t)rc * lda + kc] : a[(size_t)kc * lda + rc];
-                        da[i][e] = (row < m && kk < k) ? x : 0.0f;
+                        da[i][e] = (row < m && kk < k && !zt) ? x : 0.0f;
                     }
                 }
             }
@@ -725,7 +767,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                         const uint32_t cc = col < n ? col : n - 1;
                         const uint32_t kc = kk < k ? kk : k - 1;
                         const float x = TB ? b[(size_t)kc * ldb + cc] : b[(size_t)cc * ldb + kc];
-                        db[i][e] = (col < n && kk < k) ? x : 0.0f;
+                        db[i][e] = (col < n && kk < k && !zt) ? x : 0.0f;
                     }
                 }
             }
@@ -878,8 +920,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         // any point of iteration t may refill it.
     #pragma unroll
         for (int s = 0; s < NBUF - 1; ++s) {
-            if (s < ktiles) {
-                if (s == 0 && kshift != 0u) gload(path, 0, 0, Head{});
+            if (s < kt_count) {
+                if (s == 0 && kshift_h != 0u) gload(path, 0, 0, Head{});
                 else gload(path, s, 0, NoHead{});
                 swrite(s, 0);
             }
@@ -887,7 +929,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         // tiles NBUF - 1 .. NBUF + PD - 2 go to the register sets
     #pragma unroll
         for (int j = 0; j < PD; ++j)
-            if (NBUF - 1 + j < ktiles) gload(path, NBUF - 1 + j, (NBUF - 1 + j) % PD, NoHead{});
+            if (NBUF - 1 + j < kt_count) gload(path, NBUF - 1 + j, (NBUF - 1 + j) % PD, NoHead{});
         __syncthreads();
 
         if constexpr (SG_PLR >= 2) {
@@ -902,14 +944,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
             // so a tile's global loads have PD iterations to arrive.
             constexpr int U = (PD == 2 && NBUF % 2) ? 2 * NBUF : NBUF;  // lcm(NBUF, PD)
             Frag cur, nxt;
-            if (ktiles > 0) load_frag(lds, 0, cur);
-            for (int t0 = 0; t0 < ktiles; t0 += U) {
+            if (kt_count > 0) load_frag(lds, 0, cur);
+            for (int t0 = 0; t0 < kt_count; t0 += U) {
     #pragma unroll
                 for (int uu = 0; uu < U; ++uu) {
                     const int t = t0 + uu;
                     const int u = uu % NBUF;
                     const int set = (uu + NBUF - 1) % PD;
-                    if (t < ktiles) {
+                    if (t < kt_count) {
                         const float* s = lds + u * G::STAGE;
     #pragma unroll
                         for (int kb = 0; kb < NKB; ++kb) {
@@ -923,7 +965,7 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                             mfma_frag(cur);
                             if (kb == 0) {
                                 swrite((u + NBUF - 1) % NBUF, set);
-                                gload(path, min(t + NBUF - 1 + PD, ktiles - 1), set, NoHead{});
+                                gload(path, min(t + NBUF - 1 + PD, kt_count - 1), set, NoHead{});
                             }
                             if constexpr (SG_PLR >= 3) {
                                 constexpr int NMFMA = KPL * WT0 * WT1;
@@ -943,19 +985,19 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
                             if (!last || NBUF >= 3) cur = nxt;
                         }
                         __syncthreads();
-                        if (NBUF == 2 && t + 1 < ktiles) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, cur);
+                        if (NBUF == 2 && t + 1 < kt_count) load_frag(lds + ((u + 1) % NBUF) * G::STAGE, 0, cur);
                     }
                 }
             }
         } else {
-            for (int t0 = 0; t0 < ktiles; t0 += NBUF) {
+            for (int t0 = 0; t0 < kt_count; t0 += NBUF) {
     #pragma unroll
                 for (int u = 0; u < NBUF; ++u) {
                     const int t = t0 + u;
-                    if (t < ktiles) {
+                    if (t < kt_count) {
                         compute(u);
-                        if (t + NBUF - 1 < ktiles) swrite((u + NBUF - 1) % NBUF, 0);
-                        if (t + NBUF < ktiles) gload(path, t + NBUF, 0, NoHead{});
+                        if (t + NBUF - 1 < kt_count) swrite((u + NBUF - 1) % NBUF, 0);
+                        if (t + NBUF < kt_count) gload(path, t + NBUF, 0, NoHead{});
                         __syncthreads();
                     }
                 }
@@ -1107,6 +1149,51 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     if (slow) kloop(SlowPath{});
     else kloop(FastPath{});
 #endif
+    // The epilogue stages the tile through LDS when its chunks fit (SG_GW).
+    constexpr bool STAGED = SG_GW != 0 && G::CWAVES * AT::N * AT::M * WT0 <= G::LDS_FLOATS;
+    if constexpr (SG_KSPLIT != 0) {
+        // ---- the two K halves meet in LDS: group 0 += group 1 ----
+        // Wave w of group 1 holds the same sub-tile as wave w of group 0; its
+        // accumulators go to group 1's ring (the ring after group 0's) as
+        // float4 chunk ch of work-item ctid at float4 (ch * CNT + ctid), read
+        // back by the same work-item of group 0 and added after group 0's own
+        // (a fixed order: the result does not depend on timing).  Group 1
+        // then leaves, after the barrier that opens the staged epilogue.
+        constexpr int HC = AT::ACC / 4;
+        constexpr int CH = WT0 * WT1 * HC;
+        static_assert(!SG_KSPLIT || CH * G::CNT * 4 <= G::LDS_FLOATS, "group 1's sums fit its LDS ring");
+        float* const part = kgrp == 1 ? lds : lds + G::LDS_FLOATS;
+        const int ctid = tid % G::CNT;
+        __syncthreads();  // both groups are past their last K-tile read
+        if (kgrp == 1) {
+#pragma unroll
+            for (int i = 0; i < WT0; ++i)
+#pragma unroll
+                for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                    for (int h = 0; h < HC; ++h) {
+                        f32x4 v;
+                        v.x = acc[i][j][4 * h]; v.y = acc[i][j][4 * h + 1];
+                        v.z = acc[i][j][4 * h + 2]; v.w = acc[i][j][4 * h + 3];
+                        *reinterpret_cast<f32x4*>(part + (((i * WT1 + j) * HC + h) * G::CNT + ctid) * 4) = v;
+                    }
+        }
+        __syncthreads();
+        if (kgrp == 1) {
+            if constexpr (STAGED) __syncthreads();  // pairs with the staged epilogue's barrier
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < WT0; ++i)
+#pragma unroll
+            for (int j = 0; j < WT1; ++j)
+#pragma unroll
+                for (int h = 0; h < HC; ++h) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(part + (((i * WT1 + j) * HC + h) * G::CNT + ctid) * 4);
+                    acc[i][j][4 * h] += v.x; acc[i][j][4 * h + 1] += v.y;
+                    acc[i][j][4 * h + 2] += v.z; acc[i][j][4 * h + 3] += v.w;
+                }
+    }
 
     if (fx.kind != FIX_NONE) {
         // ---- publish the partial; the last arrival combines ----
@@ -1224,7 +1311,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
     // SG_GW (the reference's global-write flavour, generator.py:2290-2508):
     // 1 stages through LDS as above when the chunks fit, 0 always stores
     // straight from the accumulators (no LDS, fewer live registers)
-    if constexpr (SG_GW != 0 && G::CWAVES * E_CHUNK <= G::LDS_FLOATS) {
+    static_assert(STAGED == (SG_GW != 0 && G::CWAVES * E_CHUNK <= G::LDS_FLOATS), "one staging rule");
+    if constexpr (STAGED) {
         {
             // every wave's last K-loop access to LDS is behind this barrier
             // (the wave-specialised loop ends with that barrier itself)

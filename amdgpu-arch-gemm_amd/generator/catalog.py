@@ -31,9 +31,9 @@ def _cfg(mfma, wg, wt, dk, stages=1, ta=False, tb=False):
     return GemmSolutionConfig(F, F, F, F, mfma, wg, wt, dk, ta, tb, vmem_stage=stages)
 
 
-def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1, stk=0, stk_rounds=0, ws=0, ws_pd=2):
+def _opt(wgm=1, plr=1, gw=1, mapk=0, xcd=0, pd=1, occ=0, sk=1, stk=0, stk_rounds=0, ws=0, ws_pd=2, ksplit=0):
     return GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=mapk, xcd=xcd, pd=pd, occ=occ, split_k=sk,
-                             stream_k=stk, stream_k_rounds=stk_rounds, ws=ws, ws_pd=ws_pd)
+                             stream_k=stk, stream_k_rounds=stk_rounds, ws=ws, ws_pd=ws_pd, ksplit=ksplit)
 
 
 # name -> (config, optimizations)
@@ -89,6 +89,13 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
     # 1024^3 and at 1024 x 1024 x 4096, so select() never picks it.
     "mt64x64_a16_wg1x4_dk32_s4_ws": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=3),
                                      _opt(wgm=8, plr=3, xcd=8, ws=1, ws_pd=2)),
+    # in-group K split of the 1024^3 geometry: two groups of four waves each
+    # multiply half of the tile's K tiles in an LDS ring of their own and add
+    # their sums through LDS.  Measured 2.3% behind the one-group instance at
+    # 1024^3 (114.8 against 117.5 TFLOP/s) and 1.5% at 1024 x 1024 x 4096, so
+    # select() never picks it.
+    "mt64x64_a16_wg1x4_dk32_s3_ks": (_cfg(MFMA_16x16x4, (1, 4), (4, 1), 32, stages=2),
+                                     _opt(wgm=8, plr=3, xcd=8, ksplit=1)),
     # prefetch depth 2: global loads issued two K tiles ahead of their LDS writes
     "mt128x64_a16_wg2x2_dk32_s3_pd2": (_cfg(MFMA_16x16x4, (2, 2), (4, 2), 32, stages=2),
                                        _opt(wgm=4, plr=3, xcd=8, pd=2)),

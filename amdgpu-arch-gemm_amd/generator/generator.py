@@ -146,6 +146,14 @@ class GemmOptimizations:
                        compute_wave_tiling.  No split-K or stream-K kernel.
     * ``ws_pd``     -- (with ``ws``) K tiles each loading wave keeps in
                        flight in registers (2..4).
+    * ``ksplit``    -- (gfx950 only) 1 doubles the work-group with a second
+                       group of the configured waves: each group loads and
+                       multiplies half of the tile's K tiles in an LDS ring
+                       of its own (twice the LDS), one barrier per pair of K
+                       tiles, and the groups' sums are added through LDS
+                       before the epilogue.  The .toml describes the launch
+                       as for ``ws``.  No split-K or stream-K kernel, no
+                       ``map_k_idx``.
     * ``stream_k_rounds`` -- (host policy, written to the .toml) the most
                        whole-tile rounds of work-groups for which the host
                        still picks stream-K on its own (0: no limit); tiles
@@ -167,6 +175,7 @@ class GemmOptimizations:
         stream_k_rounds: Optional[int] = None,
         ws: Optional[int] = None,
         ws_pd: Optional[int] = None,
+        ksplit: Optional[int] = None,
     ):
         self.level = level
         self.wgm = 1
@@ -181,6 +190,7 @@ class GemmOptimizations:
         self.stream_k_rounds = 0
         self.ws = 0
         self.ws_pd = 2
+        self.ksplit = 0
         self._setup_optimizations()
         if wgm is not None:
             self.wgm = wgm
@@ -206,6 +216,8 @@ class GemmOptimizations:
             self.ws = ws
         if ws_pd is not None:
             self.ws_pd = ws_pd
+        if ksplit is not None:
+            self.ksplit = ksplit
         if self.wgm < 1:
             raise RuntimeError(f"Invalid wgm: {self.wgm}")
         if self.map_k_idx and not _is_pow2(self.map_k_idx):
@@ -226,6 +238,10 @@ class GemmOptimizations:
             raise RuntimeError(f"Invalid wave specialisation ws={self.ws} ws_pd={self.ws_pd}")
         if self.ws and (self.split_k != 1 or self.stream_k):
             raise RuntimeError("wave specialisation (ws=1) builds no split-K or stream-K kernel")
+        if self.ksplit not in (0, 1):
+            raise RuntimeError(f"Invalid in-group K split ksplit={self.ksplit}")
+        if self.ksplit and (self.ws or self.split_k != 1 or self.stream_k or self.map_k_idx > 1):
+            raise RuntimeError("the in-group K split (ksplit=1) excludes ws, split-K, stream-K and map_k_idx")
 
     def _setup_optimizations(self):
         if self.level != 0:
@@ -247,12 +263,13 @@ class GemmOptimizations:
             "stream_k_rounds": int(self.stream_k_rounds),
             "ws": int(self.ws),
             "ws_pd": int(self.ws_pd),
+            "ksplit": int(self.ksplit),
         }
 
     def __repr__(self) -> str:
         return (f"GemmOptimizations(level={self.level}, wgm={self.wgm}, plr={self.plr}, "
                 f"gw={self.gw}, map_k_idx={self.map_k_idx}, xcd={self.xcd}, pd={self.pd}, occ={self.occ}, "
-                f"split_k={self.split_k}, stream_k={self.stream_k}, ws={self.ws})")
+                f"split_k={self.split_k}, stream_k={self.stream_k}, ws={self.ws}, ksplit={self.ksplit})")
 
 
 def lds_lane_cycle(lane: int, access_bytes: int, write: bool = False) -> int:
@@ -730,7 +747,7 @@ class GemmSolutionConfig:
         self.wavefront_size = int(d["wavefront_size"])
         self.name = d.get("name", "") or None
         self._validate()
-        want = self.lds_usage_bytes + (ws_counter_bytes(self) if d.get("ws") else 0)
+        want = static_lds_bytes(self, GemmOptimizations(1, ws=int(d.get("ws", 0)), ksplit=int(d.get("ksplit", 0))))
         if int(d["lds_usage_bytes"]) != want:
             raise RuntimeError(f"lds_usage_bytes {d['lds_usage_bytes']} does not match the geometry ({want})")
         return self
@@ -738,7 +755,7 @@ class GemmSolutionConfig:
     @classmethod
     def from_toml(cls, path: str) -> "GemmSolutionConfig":
         d = read_toml(path)
-        if d.get("ws"):  # a wave-specialised kernel: the config is its computing geometry
+        if d.get("ws") or d.get("ksplit"):  # the config is the computing geometry
             d = dict(d, wave_group=d["compute_wave_group"], wave_tiling=d["compute_wave_tiling"])
         cfg = cls(d["a_type"], d["b_type"], d["cd_type"], d["scalar_type"], d["mfma"], d["wave_group"],
                   d["wave_tiling"], d["depth_k"], d["trans_a"], d["trans_b"], d.get("vmem_stage", 1))
@@ -819,15 +836,17 @@ class GpuContext:
 
 def launch_geometry(config: GemmSolutionConfig, opt: GemmOptimizations) -> Tuple[Tuple[int, int], Tuple[int, int]]:
     """(wave_group, wave_tiling) the kernel is launched with: the config's,
-    or with wave specialisation twice the waves along M at half the atoms
-    each (same tile; the loading waves make up the second half)."""
+    or with wave specialisation / the in-group K split twice the waves along
+    M at half the atoms each (same tile; the loading waves, or the second K
+    group, make up the second half)."""
     wg, wt = tuple(config.wave_group), tuple(config.wave_tiling)
-    if not opt.ws:
+    if not (opt.ws or opt.ksplit):
         return wg, wt
+    what = "wave specialisation" if opt.ws else "the in-group K split"
     if wt[0] % 2:
-        raise RuntimeError(f"wave specialisation needs an even wave_tiling along M: {wt}")
+        raise RuntimeError(f"{what} needs an even wave_tiling along M: {wt}")
     if 2 * wg[0] * wg[1] * config.wavefront_size > MAX_WORKITEMS:
-        raise RuntimeError(f"wave specialisation doubles the work-group past {MAX_WORKITEMS} work-items")
+        raise RuntimeError(f"{what} doubles the work-group past {MAX_WORKITEMS} work-items")
     return (2 * wg[0], wg[1]), (wt[0] // 2, wt[1])
 
 
@@ -835,6 +854,14 @@ def ws_counter_bytes(config: GemmSolutionConfig) -> int:
     """Static LDS the wave-specialised K loop adds to the operand buffers: a
     ready and a done counter (uint32) per buffer."""
     return 2 * (config.vmem_stage + 1) * 4
+
+
+def static_lds_bytes(config: GemmSolutionConfig, opt: GemmOptimizations) -> int:
+    """The kernel's static LDS: the operand buffers (lds_usage_bytes), two
+    rings of them with the in-group K split, plus the wave-specialised
+    loop's counters."""
+    n = config.lds_usage_bytes * (2 if opt.ksplit else 1)
+    return n + (ws_counter_bytes(config) if opt.ws else 0)
 
 
 def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str = "generated_gemm") -> Dict[str, object]:
@@ -849,6 +876,7 @@ def kernel_defines(config: GemmSolutionConfig, opt: GemmOptimizations, name: str
         "SG_WT1": wt[1],
         "SG_WS": int(opt.ws),
         "SG_WS_PD": int(opt.ws_pd),
+        "SG_KSPLIT": int(opt.ksplit),
         "SG_DK": config.depth_k,
         "SG_NBUF": config.vmem_stage + 1,
         "SG_WGM": opt.wgm,
@@ -983,13 +1011,13 @@ def compile(kern_name: str, kern_str: str, arch: str, output_folder: str, gemm_c
     d = gemm_config.to_dict()
     if not d["name"]:
         d["name"] = kern_name
-    if opt is not None and opt.ws:
+    if opt is not None and (opt.ws or opt.ksplit):
         # the launch geometry for every runner (the reference's included);
         # the computing waves' own geometry beside it
         wg, wt = launch_geometry(gemm_config, opt)
         d["compute_wave_group"], d["compute_wave_tiling"] = d["wave_group"], d["wave_tiling"]
         d["wave_group"], d["wave_tiling"] = list(wg), list(wt)
-        d["lds_usage_bytes"] += ws_counter_bytes(gemm_config)  # the code object's whole static LDS
+        d["lds_usage_bytes"] = static_lds_bytes(gemm_config, opt)  # the code object's whole static LDS
     d["arch"] = arch
     if opt is not None:
         d.update(opt.to_dict())

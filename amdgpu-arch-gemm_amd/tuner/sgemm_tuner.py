@@ -106,21 +106,22 @@ def point_key(cfg: GemmSolutionConfig, opt: GemmOptimizations) -> str:
             f"_dk{cfg.depth_k}_s{cfg.vmem_stage}_wgm{opt.wgm}_plr{opt.plr}_gw{opt.gw}_mk{opt.map_k_idx}_x{opt.xcd}"
             + (f"_pd{opt.pd}" if opt.pd != 1 else "") + (f"_occ{opt.occ}" if opt.occ else "")
             + (f"_sk{opt.split_k}" if opt.split_k != 1 else "")
-            + (f"_ws{opt.ws_pd}" if opt.ws else "")
+            + (f"_ws{opt.ws_pd}" if opt.ws else "") + ("_ks" if opt.ksplit else "")
             + ("_" + ("t" if cfg.trans_a else "n") + ("t" if cfg.trans_b else "n")
                if cfg.trans_a or cfg.trans_b else ""))
 
 
 def make_point(mfma, wg, wt, depth_k, vmem_stage, wgm, plr, gw, map_k_idx, xcd, pd=1, occ=0,
-               split_k=1, trans: Tuple[bool, bool] = (False, False), ws: int = 0) -> Optional[Point]:
+               split_k=1, trans: Tuple[bool, bool] = (False, False), ws: int = 0, ksplit: int = 0) -> Optional[Point]:
     """One candidate; ``trans`` = (trans_a, trans_b) builds it for op(A) = A^T
     and/or op(B) = B^T (the reference's schema fields, generator.py:1007-1009);
-    ``ws`` = 1 adds as many loading waves as the geometry has computing ones."""
+    ``ws`` = 1 adds as many loading waves as the geometry has computing ones,
+    ``ksplit`` = 1 a second group of them for half of the K tiles."""
     try:
         cfg = GemmSolutionConfig(F, F, F, F, mfma, wg, wt, depth_k, trans[0], trans[1], vmem_stage=vmem_stage)
         opt = GemmOptimizations(1, wgm=wgm, plr=plr, gw=gw, map_k_idx=map_k_idx, xcd=xcd, pd=pd, occ=occ,
-                                split_k=split_k, ws=ws)
-        launch_geometry(cfg, opt)  # raises where the geometry cannot take loading waves
+                                split_k=split_k, ws=ws, ksplit=ksplit)
+        launch_geometry(cfg, opt)  # raises where the geometry cannot take the second half of waves
     except RuntimeError as e:
         if VERBOSE:
             print(e)
@@ -163,24 +164,28 @@ def geometry_points(knobs: Dict, wide: bool = False, occs: Sequence[int] = (0,),
 
 
 def knob_points(cfg: GemmSolutionConfig, split_ks: Sequence[int] = (1,), occs: Sequence[int] = (0,),
-                gws: Sequence[int] = (1,), wss: Sequence[int] = (0,)) -> Iterable[Point]:
+                gws: Sequence[int] = (1,), wss: Sequence[int] = (0,), kss: Sequence[int] = (0,)) -> Iterable[Point]:
     """Stage-2 candidates of one geometry; ``split_ks`` and ``occs`` add the
     gfx950-only split-K (0 = chosen per problem) and occupancy knobs, ``gws``
     the epilogue flavour (1: staged through LDS, 0: stores straight from the
     accumulators), ``wss`` wave specialisation (1: loading waves beside the
     computing ones; no split-K, no occupancy cap, one to three extra LDS
-    buffers).  The layout is ``cfg``'s."""
-    for dk, st, wgm, xcd, plr, pd, sk, occ, gw, ws in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES + [3], GFX950_WGM,
-                                                              GFX950_XCD, GFX950_PLR, GFX950_PD, split_ks, occs,
-                                                              gws, wss):
+    buffers), ``kss`` the in-group K split (1: a second group of waves
+    multiplies half of the K tiles in its own LDS ring; no split-K, no
+    occupancy cap, not with ws).  The layout is ``cfg``'s."""
+    for dk, st, wgm, xcd, plr, pd, sk, occ, gw, ws, ks in product(GFX950_DEPTH_K, GFX950_VMEM_STAGES + [3],
+                                                                  GFX950_WGM, GFX950_XCD, GFX950_PLR, GFX950_PD,
+                                                                  split_ks, occs, gws, wss, kss):
         if pd == 2 and plr < 2:
             continue
         if st == 3 and not ws:   # the fourth buffer pays only for the wave-specialised ring
             continue
         if ws and (sk != 1 or occ or pd != 1):
             continue
+        if ks and (ws or sk != 1 or occ):
+            continue
         p = make_point(cfg.mfma, cfg.wave_group, cfg.wave_tiling, dk, st, wgm, plr, gw, 0, xcd, pd, occ, sk,
-                       (cfg.trans_a, cfg.trans_b), ws)
+                       (cfg.trans_a, cfg.trans_b), ws, ks)
         if p:
             yield p
 
@@ -469,6 +474,9 @@ def main(argv=None):
     ap.add_argument("--ws", default="0",
                     help="comma-separated wave-specialisation settings for stage 2 (1 = loading waves beside the "
                          "computing ones, K buffers ordered by LDS counters; default 0)")
+    ap.add_argument("--ksplit", default="0",
+                    help="comma-separated in-group K split settings for stage 2 (1 = a second group of waves "
+                         "multiplies half of the K tiles, the sums meet in LDS; default 0)")
     ap.add_argument("--tiles", default=None,
                     help="comma-separated macro-tiles MT0xMT1 for stage 1 (default: the --space list)")
     ap.add_argument("--stage1-depths", default=",".join(str(d) for d in STAGE1_DEPTHS),
@@ -482,6 +490,7 @@ def main(argv=None):
     occs = [int(x) for x in args.occ.split(",") if x.strip()]
     gws = [int(x) for x in args.gw.split(",") if x.strip()]
     wss = [int(x) for x in args.ws.split(",") if x.strip()]
+    kss = [int(x) for x in args.ksplit.split(",") if x.strip()]
     depths = [int(x) for x in args.stage1_depths.split(",") if x.strip()]
     tiles = None
     if args.tiles:
@@ -502,7 +511,7 @@ def main(argv=None):
         pts = list(stage1)
         if args.all_shapes and args.space != "reference":
             for cfg, _ in stage1:
-                pts += [p for p in knob_points(cfg, split_ks, occs, gws, wss) if fits(p[0], m, n, k)]
+                pts += [p for p in knob_points(cfg, split_ks, occs, gws, wss, kss) if fits(p[0], m, n, k)]
         res = build_points(out, pts, args.jobs)
         bad = sum(1 for v in res.values() if v)
         print(f"compiled {len(res) - bad} of {len(res)} candidates into {point_dir(out)}")
@@ -526,7 +535,7 @@ def main(argv=None):
         seen = set(by_key)
         for r in ranked:
             cfg = by_key[r["point"]][0]
-            for p in knob_points(cfg, split_ks, occs, gws, wss):
+            for p in knob_points(cfg, split_ks, occs, gws, wss, kss):
                 kk = point_key(*p)
                 if kk not in seen and fits(p[0], m, n, k):
                     seen.add(kk)

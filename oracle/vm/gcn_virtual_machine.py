@@ -750,6 +750,9 @@ for _n, _f in (("eq", lambda a, b: a == b), ("lg", lambda a, b: a != b), ("gt", 
     _scmpk(f"s_cmpk_{_n}_i32", _f, signed=True)
 _scmp64("s_cmp_eq_u64", lambda a, b: a == b)
 _scmp64("s_cmp_lg_u64", lambda a, b: a != b)
+# s_bitcmp{0,1}_b32: SCC = (bit S1[4:0] of S0) == 0 / == 1
+_scmp("s_bitcmp0_b32", lambda a, b: (a >> (b & 31)) & 1 == 0)
+_scmp("s_bitcmp1_b32", lambda a, b: (a >> (b & 31)) & 1 == 1)
 
 
 # control flow ------------------------------------------------------------

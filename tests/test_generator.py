@@ -367,6 +367,38 @@ def test_wave_specialised_catalog_toml(kernels):
     assert back.wave_group == (1, 4) and back.wave_tiling == (4, 1) and back.tile_size == (64, 64)
 
 
+def test_k_split_knob():
+    """ksplit = 1 launches a second group of the configured waves (same tile,
+    the .toml gives the launch geometry as for ws), SG_KSPLIT splits the K
+    tiles between the groups, and the static LDS holds two rings; it
+    excludes ws, split-K, stream-K and map_k_idx."""
+    c = cfg((16, 16, 1, 4), (1, 4), (4, 1), 32, stages=2)
+    o = g.GemmOptimizations(1, plr=3, ksplit=1)
+    d = g.kernel_defines(c, o)
+    assert (d["SG_WG0"], d["SG_WG1"], d["SG_WT0"], d["SG_WT1"], d["SG_KSPLIT"], d["SG_WS"]) == (2, 4, 2, 1, 1, 0)
+    assert g.launch_geometry(c, o) == ((2, 4), (2, 1))
+    assert g.kernel_defines(c, g.GemmOptimizations(1))["SG_KSPLIT"] == 0
+    assert g.static_lds_bytes(c, o) == 2 * c.lds_usage_bytes
+    assert g.static_lds_bytes(c, g.GemmOptimizations(1)) == c.lds_usage_bytes
+    for bad in (dict(ksplit=2), dict(ksplit=1, ws=1), dict(ksplit=1, split_k=0), dict(ksplit=1, stream_k=1),
+                dict(ksplit=1, map_k_idx=2)):
+        with pytest.raises(RuntimeError):
+            g.GemmOptimizations(1, **bad)
+    with pytest.raises(RuntimeError, match="in-group K split needs an even wave_tiling"):
+        g.kernel_defines(cfg((16, 16, 1, 4), (1, 4), (1, 1), 32), o)
+    assert o.to_dict()["ksplit"] == 1 and g.GemmOptimizations(1).to_dict()["ksplit"] == 0
+
+
+def test_k_split_catalog_toml(kernels):
+    name = "mt64x64_a16_wg1x4_dk32_s3_ks"
+    d = g.read_toml(catalog.paths(name)[1])
+    assert d["ksplit"] == 1 and d["wave_group"] == [2, 4] and d["wave_tiling"] == [2, 1]
+    assert d["compute_wave_group"] == [1, 4] and d["compute_wave_tiling"] == [4, 1]
+    assert d["lds_bytes_compiled"] == d["lds_usage_bytes"] == 2 * 3 * (64 * 32 + 64 * 32) * 4
+    back = g.GemmSolutionConfig.from_toml(catalog.paths(name)[1])
+    assert back.wave_group == (1, 4) and back.wave_tiling == (4, 1) and back.tile_size == (64, 64)
+
+
 def test_auto_split_known_answers():
     """The per-problem split rule at the shapes it was calibrated on (MI355X,
     256 CUs): the best measured split counts lie where tiles x splits just

@@ -14,6 +14,7 @@ import pytest
 
 import oracle
 from generator import catalog
+from ksplit import k_split_ranges
 from shim import sgemm_shim as S
 
 pytestmark = pytest.mark.gpu
@@ -513,6 +514,49 @@ def test_wave_specialised_instance_equals_its_barrier_twin(kernels, m, n, k):
     assert np.array_equal(D1, D2), "repeated launches differ"
     assert np.array_equal(D1, Dt), "the wave-specialised result differs from its barrier twin"
     _check(D1, oracle.cpu_gemm_blocked(A, B, C, 0.5, -1.5, threads=16), k, ws)
+
+
+# ------------------------------------------------------ in-group K split
+KS_CASES = [
+    # (m, n, k): a shifted head with an odd and an even tile count, one K
+    # tile, two shifted tiles (slow path), edge tiles, deep K
+    (1024, 1024, 1024), (333, 290, 5003), (64, 64, 32), (130, 70, 100), (2048, 64, 31), (1000, 999, 4097),
+    (64, 64, 45), (256, 192, 160),
+]
+
+
+@pytest.mark.parametrize("m,n,k", KS_CASES)
+def test_k_split_instance_is_the_sum_of_its_halves(kernels, m, n, k):
+    """The in-group K split instance: group 0 sums K range [0, k0), group 1
+    [k1, k), group 0 adds the two.  With alpha = 1, beta = 0 its D is exactly
+    the fp32 sum of the one-group instance's results on the two ranges (same
+    tile boundaries and head shift, so the same MFMA sequence per output),
+    stable over repeated launches; with alpha / beta it is within the bar of
+    the oracle."""
+    ks, twin = "mt64x64_a16_wg1x4_dk32_s3_ks", "mt64x64_a16_wg1x4_dk32_s3"
+    _say(f"in-group K split {ks} vs {twin} halves {m}x{n}x{k}")
+    A = S.fill_matrix(m, k, 31, 0)
+    B = S.fill_matrix(k, n, 31, 1)
+    C = S.fill_matrix(m, n, 31, 2)
+    k0, k1 = k_split_ranges(k, catalog.SOLUTIONS[ks][0].depth_k)
+    with _kernel(ks) as kk, _kernel(twin) as kt:
+        kt.set_split_k(1)
+        kt.set_stream_k(0)
+        assert kk.info.workitems == 2 * kt.info.workitems and kk.tile[:2] == kt.tile[:2]
+        assert kk.launch_splits(m, n, k) == 1
+        D1, _ = kk.run(A, B, None, m, n, k, alpha=1.0, beta=0.0, warmup=0, runs=1)
+        D2, _ = kk.run(A, B, None, m, n, k, alpha=1.0, beta=0.0, warmup=2, runs=5)
+        S0, _ = kt.run(np.asfortranarray(A[:, :k0]), np.asfortranarray(B[:k0, :]), None, m, n, k0,
+                       alpha=1.0, beta=0.0, warmup=0, runs=1)
+        S1 = np.zeros((m, n), np.float32)
+        if k1 < k:
+            S1, _ = kt.run(np.asfortranarray(A[:, k1:]), np.asfortranarray(B[k1:, :]), None, m, n, k - k1,
+                           alpha=1.0, beta=0.0, warmup=0, runs=1)
+        Dab, _ = kk.run(A, B, C, m, n, k, alpha=0.5, beta=-1.5, warmup=0, runs=1)
+    assert np.array_equal(D1, D2), "repeated launches differ"
+    assert np.array_equal(D1, (S0 + S1).astype(np.float32)), "D is not the sum of the two K halves"
+    err = _check(Dab, oracle.cpu_gemm_blocked(A, B, C, 0.5, -1.5, threads=16), k, ks)
+    _say(f"  K ranges [0, {k0}) + [{k1}, {k}): bit-identical to the halves; alpha/beta normwise error {err:.3e}")
 
 
 # ----------------------------------------------------------------- split-K

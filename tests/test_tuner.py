@@ -220,3 +220,18 @@ def test_stage2_wave_specialisation_points():
     odd = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (2, 2), (1, 2), 32, False, False, vmem_stage=2)
     assert not [o for _, o in T.knob_points(odd, wss=(1,)) if o.ws]
 
+
+def test_stage2_k_split_points():
+    """--ksplit 0,1 adds in-group K split points: no split-K, no occupancy
+    cap, never with ws, no fourth LDS buffer, and keys of their own."""
+    from generator.generator import GemmSolutionConfig, MFMA_16x16x4
+    base = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (1, 4), (4, 1), 32, False, False, vmem_stage=2)
+    pts = list(T.knob_points(base, split_ks=(1, 0), occs=(0, 2), gws=(1,), wss=(0, 1), kss=(0, 1)))
+    ks = [(c, o) for c, o in pts if o.ksplit]
+    assert ks and all(o.split_k == 1 and o.occ == 0 and not o.ws for _, o in ks)
+    assert {c.vmem_stage for c, _ in ks} == {1, 2}
+    keys = [T.point_key(c, o) for c, o in pts]
+    assert len(keys) == len(set(keys)) and all(T.point_key(c, o).endswith("_ks") for c, o in ks)
+    odd = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (2, 2), (1, 2), 32, False, False, vmem_stage=2)
+    assert not [o for _, o in T.knob_points(odd, kss=(1,)) if o.ksplit]
+

@@ -19,6 +19,7 @@ from generator import catalog
 from generator import generator as g
 from vm import gcn_virtual_machine as V
 from vm.gcn_virtual_machine import GcnVirtualMachine, parse_operand, run_kernel, run_sgemm, pack_kernargs
+from ksplit import k_split_ranges
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 _PROGRAMS = {}
@@ -898,6 +899,48 @@ def test_wave_specialised_kernel_in_vm(seed):
     assert oracle.normwise_error(D, oracle.gemm_f64(A, B, C, 0.5, -1.25)) <= oracle.tolerance(k)
     D0, _ = run_sgemm(prog, cfg.tile_size, _ws_workitems(WS_NAME), A, B, C, 0.5, -1.25)
     assert np.array_equal(D, D0)
+
+
+KS_NAME, KS_TWIN = "mt64x64_a16_wg1x4_dk32_s3_ks", "mt64x64_a16_wg1x4_dk32_s3"
+
+
+def test_k_split_ranges_partition_k():
+    for dk in (16, 32, 64):
+        for k in range(0, 8 * dk + 3):
+            k0, k1 = k_split_ranges(k, dk)
+            assert k0 == k1 and 0 <= k0 <= k
+            assert abs((k - k0) - k0) <= dk   # the halves differ by at most one K tile
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 64, 197), (64, 64, 160), (64, 64, 128), (64, 64, 45), (64, 64, 32),
+                                   (64, 64, 17), (100, 70, 77), (64, 128, 3)])
+def test_k_split_kernel_in_vm(m, n, k):
+    """The in-group K split: group 0 sums K range [0, k0), group 1 [k1, k)
+    (a zero head tile when the tile count is odd), and group 0 adds group 1's
+    sums.  With alpha = 1, beta = 0, D is therefore exactly the fp32 sum of
+    the one-group kernel's results on the two ranges (same tile boundaries and
+    head shift, so the same MFMA sequence); the cases cover a shifted head, an
+    odd and an even tile count, one K tile, the slow path for two shifted
+    tiles, and edge tiles.  With alpha / beta and random preemption the
+    result stays within the bar and bit-stable."""
+    prog, cfg = program(KS_NAME)
+    twin, tcfg = program(KS_TWIN)
+    wi = _ws_workitems(KS_NAME)
+    assert wi == 2 * tcfg.num_workitems and cfg.tile_size == tcfg.tile_size
+    A = oracle.fill_matrix(m, k, 7, 0)
+    B = oracle.fill_matrix(k, n, 7, 1)
+    C = oracle.fill_matrix(m, n, 7, 2)
+    D, _ = run_sgemm(prog, cfg.tile_size, wi, A, B, None, 1.0, 0.0)
+    k0, k1 = k_split_ranges(k, cfg.depth_k)
+    S0, _ = run_sgemm(twin, tcfg.tile_size, tcfg.num_workitems, A[:, :k0], B[:k0, :], None, 1.0, 0.0)
+    S1 = np.zeros((m, n), np.float32)
+    if k1 < k:
+        S1, _ = run_sgemm(twin, tcfg.tile_size, tcfg.num_workitems, A[:, k1:], B[k1:, :], None, 1.0, 0.0)
+    assert np.array_equal(D, (S0 + S1).astype(np.float32))
+    Dab, _ = run_sgemm(prog, cfg.tile_size, wi, A, B, C, 0.5, -1.25, preempt_seed=3)
+    assert oracle.normwise_error(Dab, oracle.gemm_f64(A, B, C, 0.5, -1.25)) <= oracle.tolerance(k)
+    Dab0, _ = run_sgemm(prog, cfg.tile_size, wi, A, B, C, 0.5, -1.25)
+    assert np.array_equal(Dab, Dab0)
 
 
 FLAG_PROTOCOL = """
