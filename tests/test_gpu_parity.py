@@ -1128,17 +1128,28 @@ def test_generator_runner_validates(kernels):
     assert 0 < gpu_err <= tol and 0 < cpu_err <= tol, f64[0]
 
 
-def test_generator_runner_validates_the_headline_shape(kernels):
-    """The runner with validation_flag = 1 at BASELINE config 3 (4096^3, U[-1,1)
-    seed 2, alpha = 1, beta = 0) and the catalog's instance for it: all 16.8M
-    outputs against the CPU reference by the normwise bar and by the
-    reference's elementwise |gpu - cpu| < 1e-3 (generator_runner.cpp:287-316),
-    with the single-thread cpuGemm figure on a column slice and the blocked
-    multithreaded reference on its own line."""
-    m = n = k = 4096
+RUNNER_CONFIGS = [
+    # (BASELINE config, m, n, k, seed, distribution: 0 U[-1,1), 1 N(0,1)); alpha = 1, beta = 0
+    ("cfg2", 1024, 1024, 1024, 1, 0),
+    ("cfg3", 4096, 4096, 4096, 2, 0),
+    ("cfg4", 8192, 8192, 256, 3, 1),
+    ("cfg5", 16384, 128, 4096, 4, 0),
+]
+
+
+@pytest.mark.parametrize("cid,m,n,k,seed,dist", RUNNER_CONFIGS)
+def test_generator_runner_validates_the_baseline_configs(kernels, cid, m, n, k, seed, dist):
+    """The runner with validation_flag = 1 at each GPU config of BASELINE.json
+    and the catalog's instance for it: all m*n outputs against the CPU
+    reference by the normwise bar and by the reference's elementwise
+    |gpu - cpu| < 1e-3 (generator_runner.cpp:287-316), with the single-thread
+    cpuGemm figure (on a column slice where the whole would take long) and the
+    blocked multithreaded reference on its own line."""
     name = catalog.select(m, n, k)
     co, toml = catalog.paths(name)
-    ret = _run([RUNNER, co, toml, str(m), str(n), str(k), "2", "5", "1", "2", "0", "1", "0"], timeout=600)
+    _say(f"runner validation {cid} {m}x{n}x{k} seed {seed} dist {dist} -> {name}")
+    ret = _run([RUNNER, co, toml, str(m), str(n), str(k), "2", "5", "1", str(seed), str(dist), "1", "0"],
+               timeout=600)
     out = ret.stdout.decode()
     _say(out)
     assert ret.returncode == 0, out
