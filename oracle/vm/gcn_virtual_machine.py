@@ -230,7 +230,7 @@ def parse_assembly(asm: str, kernel: str = "generated_gemm") -> "Program":
                 "amdhsa_system_sgpr_workgroup_id_z", "amdhsa_user_sgpr_dispatch_ptr", "amdhsa_user_sgpr_queue_ptr",
                 "amdhsa_user_sgpr_dispatch_id", "amdhsa_user_sgpr_private_segment_size",
                 "amdhsa_system_vgpr_workitem_id", "amdhsa_next_free_sgpr", "amdhsa_next_free_vgpr",
-                "amdhsa_accum_offset"):
+                "amdhsa_accum_offset", "amdhsa_kernarg_size"):
         m = re.search(r"\." + key + r"\s+(\d+)", block)
         if m:
             desc[key] = int(m.group(1))
@@ -1213,6 +1213,70 @@ for _nd, _sfx in ((1, "dword"), (2, "dwordx2"), (3, "dwordx3"), (4, "dwordx4")):
     _DISPATCH[f"global_store_{_sfx}"] = _global_store(_nd)
 
 
+# scratch (private) memory: register spills --------------------------------
+PRIVATE_BYTES = 1 << 16  # per lane; far above any spill area the kernels use
+
+
+def _scratch_offsets(vm, ins, vaddr_op, saddr_op):
+    """Per-lane byte offset into the lane's private memory: the 32-bit vaddr
+    and/or saddr when given (not ``off``) plus the instruction offset."""
+    off = np.full(WAVE, ins.mods.get("offset", 0), dtype=np.int64)
+    if vaddr_op is not None and vaddr_op.kind != "off":
+        off = off + vm.rv32(vaddr_op).astype(np.int64)
+    if saddr_op is not None and saddr_op.kind != "off":
+        off = off + np.int64(vm.rs32(saddr_op))
+    return off
+
+
+def _private(vm):
+    if getattr(vm, "private", None) is None:
+        vm.private = np.zeros((WAVE, PRIVATE_BYTES // 4), dtype=np.uint32)
+    return vm.private
+
+
+def _scratch_check(off, nd, ins):
+    if (off % 4).any() or (off < 0).any() or (off + 4 * nd > PRIVATE_BYTES).any():
+        raise MemoryError(f"{ins}: scratch access outside [0, {PRIVATE_BYTES}) or unaligned")
+
+
+def _scratch_load(nd):
+    def _impl(vm, ins, prog):
+        dst, vaddr, saddr = ins.ops[0], ins.ops[1], ins.ops[2]
+        mask = vm.exec_mask()
+        off = _scratch_offsets(vm, ins, vaddr, saddr)
+        _scratch_check(off[mask], nd, ins)
+        mem = _private(vm)
+        lanes = np.nonzero(mask)[0]
+        data = np.zeros((nd, WAVE), dtype=np.uint32)
+        for i in range(nd):
+            data[i, lanes] = mem[lanes, off[lanes] // 4 + i]
+
+        def land():
+            for i in range(nd):
+                vm.regfile(dst)[dst.index + i][mask] = data[i][mask]
+        vm.pending["vmcnt"].append(land)
+    return _impl
+
+
+def _scratch_store(nd):
+    def _impl(vm, ins, prog):
+        vaddr, src, saddr = ins.ops[0], ins.ops[1], ins.ops[2]
+        mask = vm.exec_mask()
+        off = _scratch_offsets(vm, ins, vaddr, saddr)
+        _scratch_check(off[mask], nd, ins)
+        mem = _private(vm)
+        lanes = np.nonzero(mask)[0]
+        for i in range(nd):
+            mem[lanes, off[lanes] // 4 + i] = vm.regfile(src)[src.index + i][lanes]
+        vm.pending["vmcnt"].append(lambda: None)
+    return _impl
+
+
+for _nd, _sfx in ((1, "dword"), (2, "dwordx2"), (3, "dwordx3"), (4, "dwordx4")):
+    _DISPATCH[f"scratch_load_{_sfx}"] = _scratch_load(_nd)
+    _DISPATCH[f"scratch_store_{_sfx}"] = _scratch_store(_nd)
+
+
 @op("global_atomic_add")
 def _global_atomic_add(vm, ins, prog):
     """32-bit atomic add, lanes in ascending order.  With sc0 (glc) the first
@@ -1439,7 +1503,9 @@ def run_kernel(program, grid: Tuple[int, ...], workgroup_size: int, kernargs: by
     total = 0
     for (wx, wy, wz) in order:
         lds = Memory(max(lds_size, 4), "lds")
-        smem = Memory(max(len(kernargs), 8), "smem")
+        # the kernel's whole declared kernarg segment, as the runtime allocates
+        # it: bytes past the given image read as zeros
+        smem = Memory(max(len(kernargs), desc.get("amdhsa_kernarg_size", 0), 8), "smem")
         smem.write_bytes(0, kernargs)
         waves = []
         for w in range(nwaves):

@@ -999,3 +999,55 @@ def test_vm_preemption_catches_a_flag_raised_before_its_data():
     stale = [s for s in range(200) if _flag_protocol_result(False, s) == 0]
     assert stale, "no interleaving put the reader between the writer's two writes"
 
+
+
+SCRATCH_ROUND_TRIP = """
+generated_gemm:
+    s_mov_b32 s4, 1024
+    s_mov_b32 s5, 0
+    v_lshlrev_b32 v1, 2, v0
+    v_add_u32 v2, 1000, v0
+    v_add_u32 v3, 2000, v0
+    scratch_store_dwordx2 off, v[2:3], off offset:8
+    v_mov_b32 v2, 0
+    v_mov_b32 v3, 0
+    scratch_load_dwordx2 v[4:5], off, off offset:8
+    s_waitcnt vmcnt(0)
+    s_load_dword s2, s[0:1], 0x54
+    s_waitcnt lgkmcnt(0)
+    v_add_u32 v4, s2, v4
+    global_store_dword v1, v4, s[4:5]
+    global_store_dword v1, v5, s[4:5] offset:256
+    s_endpgm
+.Lfunc_end0:
+.amdhsa_kernel generated_gemm
+    .amdhsa_group_segment_fixed_size 0
+    .amdhsa_kernarg_size 88
+    .amdhsa_user_sgpr_count 2
+    .amdhsa_user_sgpr_kernarg_segment_ptr 1
+    .amdhsa_system_sgpr_workgroup_id_x 1
+.end_amdhsa_kernel
+"""
+
+
+def test_vm_scratch_is_private_per_lane_and_kernargs_span_the_declared_segment():
+    """Spilled registers (scratch_store / scratch_load with no address
+    registers) come back per lane after the vmcnt wait, and the kernarg
+    segment is as long as the kernel declares: bytes past the given 8-byte
+    image (offset 0x54 here, inside the declared 88) read as zero, as the
+    runtime's zero-filled segment does."""
+    prog = V.parse_assembly(SCRATCH_ROUND_TRIP)
+    assert prog.desc["amdhsa_kernarg_size"] == 88
+    mem = V.Memory(4096, "vmem")
+    mem.allocate_region(1024, 512, "out")
+    V.run_kernel(prog, (1, 1), 64, b"\0" * 8, mem)
+    out = np.frombuffer(mem.read_bytes(1024, 512), dtype=np.uint32)
+    lanes = np.arange(64, dtype=np.uint32)
+    assert np.array_equal(out[:64], 1000 + lanes) and np.array_equal(out[64:], 2000 + lanes)
+
+
+def test_vm_scratch_bounds_are_checked():
+    vm = GcnVirtualMachine()
+    vm.v[1] = np.full(64, 1 << 20, dtype=np.uint32)
+    with pytest.raises(MemoryError, match="scratch"):
+        vm.run("generated_gemm:\n    scratch_store_dword v1, v2, off\n    s_endpgm\n")
