@@ -7,6 +7,7 @@ layout known-answer tests (:409-445), whole-kernel SGEMMs on arange inputs
 invariance under map_k_idx / extra LDS stages (:743-963) -- but every kernel
 here is the real hipcc output for gfx950, not an emitter's instruction list.
 """
+import copy
 import json
 import os
 import struct
@@ -1051,3 +1052,42 @@ def test_vm_scratch_bounds_are_checked():
     vm.v[1] = np.full(64, 1 << 20, dtype=np.uint32)
     with pytest.raises(MemoryError, match="scratch"):
         vm.run("generated_gemm:\n    scratch_store_dword v1, v2, off\n    s_endpgm\n")
+
+
+def _with_layout(name, ta, tb):
+    cfg, opt = copy.deepcopy(catalog.SOLUTIONS[name])
+    c = g.GemmSolutionConfig(cfg.a_type, cfg.b_type, cfg.cd_type, cfg.scalar_type, cfg.mfma, cfg.wave_group,
+                             cfg.wave_tiling, cfg.depth_k, ta, tb, vmem_stage=cfg.vmem_stage)
+    ctx = g.GpuContext()
+    g.gemm(ctx, "generated_gemm", "gfx950", c, opt, g.default_arguments())
+    wg, _ = g.launch_geometry(c, opt)
+    return V.parse_assembly(ctx.assembly(), "generated_gemm"), c, wg[0] * wg[1] * 64
+
+
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+def test_ws_and_k_split_with_transposed_operands_in_vm(ta, tb):
+    """The wave-specialised and the in-group K split instances rebuilt for
+    TN, NT and TT: the first bit-identical to the barrier twin of its layout,
+    the second to the sum of that twin's results on its two K ranges, on a
+    ragged shape with a K remainder (alpha = 1, beta = 0)."""
+    m, n, k = 100, 70, 77
+    A = oracle.fill_matrix(m, k, 8, 0)
+    B = oracle.fill_matrix(k, n, 8, 1)
+    As = np.asfortranarray(A.T) if ta else A
+    Bs = np.asfortranarray(B.T) if tb else B
+    twin, tcfg, twi = _with_layout(KS_TWIN, ta, tb)
+
+    def run_twin(k0, k1):
+        a = np.asfortranarray(As[k0:k1, :] if ta else As[:, k0:k1])
+        b = np.asfortranarray(Bs[:, k0:k1] if tb else Bs[k0:k1, :])
+        return run_sgemm(twin, tcfg.tile_size, twi, a, b, None, 1.0, 0.0, mnk=(m, n, k1 - k0))[0]
+
+    ws, wcfg, wwi = _with_layout(WS_NAME, ta, tb)
+    Dw, _ = run_sgemm(ws, wcfg.tile_size, wwi, As, Bs, None, 1.0, 0.0, mnk=(m, n, k))
+    assert np.array_equal(Dw, run_twin(0, k))
+    ks, kcfg, kwi = _with_layout(KS_NAME, ta, tb)
+    Dk, _ = run_sgemm(ks, kcfg.tile_size, kwi, As, Bs, None, 1.0, 0.0, mnk=(m, n, k))
+    k0, k1 = k_split_ranges(k, kcfg.depth_k)
+    S1 = run_twin(k1, k) if k1 < k else np.zeros((m, n), np.float32)
+    assert np.array_equal(Dk, (run_twin(0, k0) + S1).astype(np.float32))
+    assert oracle.normwise_error(Dk, oracle.gemm_f64(A, B, None, 1.0, 0.0)) <= oracle.tolerance(k)
