@@ -845,6 +845,12 @@ def launch_geometry(config: GemmSolutionConfig, opt: GemmOptimizations) -> Tuple
     what = "wave specialisation" if opt.ws else "the in-group K split"
     if wt[0] % 2:
         raise RuntimeError(f"{what} needs an even wave_tiling along M: {wt}")
+    if opt.ksplit:
+        tile_bytes = config.tile_size[0] * config.tile_size[1] * 4
+        if tile_bytes > config.lds_usage_bytes:
+            raise RuntimeError(f"the in-group K split passes group 1's sums ({tile_bytes} bytes for the "
+                               f"{config.tile_size[0]} x {config.tile_size[1]} tile) through its LDS ring of "
+                               f"{config.lds_usage_bytes} bytes: use more stages or a deeper K tile")
     if 2 * wg[0] * wg[1] * config.wavefront_size > MAX_WORKITEMS:
         raise RuntimeError(f"{what} doubles the work-group past {MAX_WORKITEMS} work-items")
     return (2 * wg[0], wg[1]), (wt[0] // 2, wt[1])

@@ -387,6 +387,11 @@ def test_k_split_knob():
     with pytest.raises(RuntimeError, match="in-group K split needs an even wave_tiling"):
         g.kernel_defines(cfg((16, 16, 1, 4), (1, 4), (1, 1), 32), o)
     assert o.to_dict()["ksplit"] == 1 and g.GemmOptimizations(1).to_dict()["ksplit"] == 0
+    # group 1's tile of sums (64 x 128 floats, 32 KiB) does not fit a two-buffer ring of 24 KiB
+    small = cfg((32, 32, 1, 2), (1, 2), (2, 2), 16, stages=1)
+    with pytest.raises(RuntimeError, match="LDS ring"):
+        g.kernel_defines(small, g.GemmOptimizations(1, plr=3, ksplit=1))
+    assert g.kernel_defines(cfg((32, 32, 1, 2), (1, 2), (2, 2), 16, stages=2), g.GemmOptimizations(1, plr=3, ksplit=1))
 
 
 def test_k_split_catalog_toml(kernels):
