@@ -23,8 +23,9 @@
 // the epilogue stores only elements inside D.  A K remainder shifts the K
 // origin so that the first K tile is the partial one, its missing values
 // loaded as zeros (element by element for chunks along k that straddle it).
-// Only a K remainder with a single K tile, or with a rotated first K tile
-// (SG_MAPK > 1), takes the element-wise path.  The host side (shim, runner)
+// Only a K remainder with a single K tile (per K group under the in-group K
+// split, SG_KSPLIT), or with a rotated first K tile (SG_MAPK > 1), takes the
+// element-wise path.  The host side (shim, runner)
 // checks that lda >= m, ldb >= k, ldc >= m, ldd >= m before every launch.
 //
 // Data path per K tile of depth DK:
