@@ -155,6 +155,47 @@ def gpu_agent(out_dir):
     raise RuntimeError(f"no GPU agent in {out_dir}")
 
 
+def derive(values, probe_vals, trace_durs, agent, m, n, k):
+    """The summary's figures from the measurements, no I/O: ``values`` maps
+    each counter (and ``duration_s_<pass>``) to its per-dispatch list,
+    ``probe_vals`` copy_probe's FETCH_SIZE / WRITE_SIZE lists (KiB per
+    dispatch of a PROBE_BYTES copy), ``trace_durs`` the kernel-trace durations
+    (s) and ``agent`` what gpu_agent returns.  Medians skip the first
+    dispatch (steady)."""
+    xcc, cus, simds, engines, max_mhz = agent
+    f = {"med": {c: steady(v) for c, v in values.items()}}
+    med = f["med"]
+    probe_kib = PROBE_BYTES / 1024.0
+    f["fetch_scale"] = probe_kib / statistics.median(probe_vals["FETCH_SIZE"])
+    f["write_scale"] = probe_kib / statistics.median(probe_vals["WRITE_SIZE"])
+    f["fetch_bytes"] = med["FETCH_SIZE"] * 1024.0 * f["fetch_scale"]
+    f["write_bytes"] = med["WRITE_SIZE"] * 1024.0 * f["write_scale"]
+    f["traffic"] = f["fetch_bytes"] + f["write_bytes"]
+    f["avg_s"] = steady(trace_durs)
+    f["flops"] = 2.0 * m * n * k
+    f["alg_bytes"] = 4.0 * (m * k + k * n + m * n)
+    f["tflops"] = f["flops"] / f["avg_s"] / 1e12
+    # MFMA cycles per SIMD: measured, and the ideal at 64 FLOP per SIMD-cycle
+    f["ideal_per_simd"] = f["flops"] / 64.0 / simds
+    f["busy_per_simd"] = med["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
+    # per dispatch of the PMC pass: shader-busy cycles per engine, MfmaUtil and
+    # the clock over that dispatch's own duration
+    disp = list(zip(values["SQ_VALU_MFMA_BUSY_CYCLES"], values["SQ_BUSY_CYCLES"], values["GRBM_GUI_ACTIVE"],
+                    values["duration_s_mfma"]))
+    f["sq_per_engine"] = steady([q / engines for _, q, _, _ in disp])
+    f["mfma_util"] = 100.0 * steady([(b / simds) / (q / engines) for b, q, _, _ in disp])
+    f["clock_mhz"] = steady([q / engines / dur / 1e6 for _, q, _, dur in disp])
+    f["pmc_dur"] = steady([dur for _, _, _, dur in disp])
+    f["gui_window_mhz"] = steady([a / xcc / dur / 1e6 for _, _, a, dur in disp])
+    f["clock_ok"] = f["clock_mhz"] <= max_mhz
+    f["tflops_pmc"] = f["flops"] / f["pmc_dur"] / 1e12
+    f["clock_peak"] = cus * 256 * f["clock_mhz"] * 1e6 / 1e12
+    f["busy_us_at_max"] = f["sq_per_engine"] / max_mhz  # the engine-busy cycles at the maximum clock, in us
+    f["lds_rate"] = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
+    f["util_holds"] = f["mfma_util"] >= 100.0 * f["tflops_pmc"] / PEAK_TFLOPS - 1e-9
+    return f
+
+
 def rocprof(args, out_dir, program, timeout):
     cmd = ["rocprofv3", *args, "--output-format", "csv", "-d", out_dir, "-o", "run", "--", *program]
     return run(["timeout", "-s", "KILL", str(timeout), *cmd], timeout + 30)
@@ -222,38 +263,17 @@ def main():
         per = counters_per_dispatch(find(d, "run_counter_collection.csv"), "copy_probe")
         probe_vals[c] = per[c]
 
-    xcc, cus, simds, engines, max_mhz = gpu_agent(os.path.join(args.out, "pmc_mfma"))
-    med = {c: steady(v) for c, v in values.items()}
-    probe_kib = PROBE_BYTES / 1024.0
-    fetch_scale = probe_kib / statistics.median(probe_vals["FETCH_SIZE"])
-    write_scale = probe_kib / statistics.median(probe_vals["WRITE_SIZE"])
-    fetch_bytes = med["FETCH_SIZE"] * 1024.0 * fetch_scale
-    write_bytes = med["WRITE_SIZE"] * 1024.0 * write_scale
-    traffic = fetch_bytes + write_bytes
-    avg_s = steady(trace_durations(os.path.join(args.out, "trace"), "generated_gemm"))
-    flops = 2.0 * m * n * k
-    alg_bytes = 4.0 * (m * k + k * n + m * n)
-    tflops = flops / avg_s / 1e12
-    # MFMA cycles per SIMD: measured, and the ideal at 64 FLOP per SIMD-cycle
-    ideal_per_simd = flops / 64.0 / simds
-    busy_per_simd = med["SQ_VALU_MFMA_BUSY_CYCLES"] / simds
-    # per dispatch of the PMC pass: shader-busy cycles per engine, MfmaUtil and
-    # the clock over that dispatch's own duration
-    disp = list(zip(values["SQ_VALU_MFMA_BUSY_CYCLES"], values["SQ_BUSY_CYCLES"], values["GRBM_GUI_ACTIVE"],
-                    values["duration_s_mfma"]))
-    sq_per_engine = steady([q / engines for _, q, _, _ in disp])
-    mfma_util = 100.0 * steady([(b / simds) / (q / engines) for b, q, _, _ in disp])
-    clock_pmc_mhz = steady([q / engines / dur / 1e6 for _, q, _, dur in disp])
-    pmc_dur = steady([dur for _, _, _, dur in disp])
-    gui_window_mhz = steady([a / xcc / dur / 1e6 for _, _, a, dur in disp])
-    clock_mhz = clock_pmc_mhz
-    clock_ok = clock_mhz <= max_mhz
-    tflops_pmc = flops / pmc_dur / 1e12
-    clock_peak = cus * 256 * clock_mhz * 1e6 / 1e12
-    busy_us_at_max = sq_per_engine / max_mhz            # the engine-busy cycles at the maximum clock, in us
-    lds_rate = med["SQ_LDS_BANK_CONFLICT"] / max(med["SQ_LDS_IDX_ACTIVE"] - med["SQ_LDS_BANK_CONFLICT"], 1.0)
+    agent = gpu_agent(os.path.join(args.out, "pmc_mfma"))
+    xcc, cus, simds, engines, max_mhz = agent
+    fig = derive(values, probe_vals, trace_durations(os.path.join(args.out, "trace"), "generated_gemm"), agent, m, n, k)
+    (med, fetch_scale, write_scale, fetch_bytes, write_bytes, traffic, avg_s, alg_bytes, tflops, ideal_per_simd,
+     busy_per_simd, sq_per_engine, mfma_util, clock_mhz, pmc_dur, gui_window_mhz, clock_ok, tflops_pmc, clock_peak,
+     busy_us_at_max, lds_rate) = (fig[x] for x in (
+        "med", "fetch_scale", "write_scale", "fetch_bytes", "write_bytes", "traffic", "avg_s", "alg_bytes", "tflops",
+        "ideal_per_simd", "busy_per_simd", "sq_per_engine", "mfma_util", "clock_mhz", "pmc_dur", "gui_window_mhz",
+        "clock_ok", "tflops_pmc", "clock_peak", "busy_us_at_max", "lds_rate"))
     valid = "valid" if clock_ok else f"INVALID (above the {max_mhz:.0f} MHz maximum)"
-    util_check = "holds" if mfma_util >= 100.0 * tflops_pmc / PEAK_TFLOPS - 1e-9 else "FAILS"
+    util_check = "holds" if fig["util_holds"] else "FAILS"
 
     summary = args.summary or os.path.join(args.out, "summary.md")
     os.makedirs(os.path.dirname(os.path.abspath(summary)), exist_ok=True)
