@@ -1057,6 +1057,58 @@ def test_random_selected_transposed_launches(kernels, m, n, k, ta, tb, mode, alp
     _check(D, oracle.cpu_gemm_mt(opA, opB, Cf, alpha, beta, threads=16), k, name)
 
 
+def _deep_selected_cases(count, seed):
+    """(m, n, k, trans_a, trans_b, alpha, beta) with a deep K (320..4096) on
+    grids of hundreds to thousands of tiles, in all four layouts: the regime
+    of long K loops, head tiles after many full ones and large split counts
+    that the shallow random sweeps above leave to the BASELINE configs."""
+    rng = np.random.default_rng(seed)
+    layouts = [(False, False), (True, False), (False, True), (True, True)]
+    cases = []
+    for i in range(count):
+        m, n = (int(x) for x in rng.integers(300, 4200, size=2))
+        k = int(rng.integers(320, 4097))
+        ta, tb = layouts[i % 4]
+        cases.append((m, n, k, ta, tb, float(rng.choice([1.0, -0.5])), float(rng.choice([0.0, 0.75]))))
+    cases += [(384, 384, 4096, False, False, 1.0, 0.0), (4096, 200, 3000, True, True, 1.0, 0.5)]
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,alpha,beta",
+                         _deep_selected_cases(int(os.environ.get("SGEMM_DEEP_CASES", "8")),
+                                              int(os.environ.get("SGEMM_RANDOM_SEED", "2024"))))
+def test_random_deep_selected_launches(kernels, m, n, k, ta, tb, alpha, beta):
+    """catalog.select(m, n, k, trans_a, trans_b) with its edge kernels and
+    default split-K / stream-K settings on deep-K random shapes in every
+    layout: whole D against the blocked cpuGemm (the reference's summation
+    order) and against float64."""
+    name = catalog.select(m, n, k, ta, tb)
+    Af = S.fill_matrix(*((k, m) if ta else (m, k)), 23, 0)
+    Bf = S.fill_matrix(*((n, k) if tb else (k, n)), 23, 1)
+    Cf = S.fill_matrix(m, n, 23, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer(m * n * 4)
+    edges = [_kernel(e) for e in catalog.EDGE_KERNEL.get(name, ())]
+    try:
+        with _kernel(name) as kern:
+            if edges:
+                kern.set_edge_kernels(*edges)
+            _say(f"deep {name} {m}x{n}x{k} ta {ta} tb {tb} K ranges {kern.launch_splits(m, n, k)} "
+                 f"interior {kern.edge_interior(m, n, k)} alpha {alpha} beta {beta}")
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=alpha, beta=beta)
+            kern.synchronize()
+    finally:
+        for e in edges:
+            e.close()
+    D = dD.download().reshape(n, m).T
+    opA = np.asfortranarray(Af.T) if ta else Af
+    opB = np.asfortranarray(Bf.T) if tb else Bf
+    err = _check(D, oracle.cpu_gemm_blocked(opA, opB, Cf, alpha, beta, threads=16), k, name)
+    ref64 = alpha * (np.asarray(opA, np.float64) @ np.asarray(opB, np.float64)) + beta * np.asarray(Cf, np.float64)
+    err64 = _check(D, ref64, k, name + " vs float64")
+    _say(f"  normwise error {err:.3e} vs cpuGemm, {err64:.3e} vs float64")
+
+
 # D = alpha * op(A) * op(B) + beta * D in place (C and D one buffer): every
 # kind of launch -- plain, transposed, split-K, stream-K, edge strips and the
 # no-alloc entry point -- against the same launch into a separate D
