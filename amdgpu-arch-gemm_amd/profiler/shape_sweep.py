@@ -9,7 +9,7 @@ over the shapes, each timing at least ~3 ms of back-to-back launches, and the
 median per shape is reported, with its K ranges and stream-K tiles.
 
     python amdgpu-arch-gemm_amd/profiler/shape_sweep.py --shapes 2048x2048x2048,3000x3000x3000 \\
-        --summary gpurun_out/profiles/default_path_shapes.md
+        --summary out/default_path_shapes.md
 """
 import argparse
 import os
