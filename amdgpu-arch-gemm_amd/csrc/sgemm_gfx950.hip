@@ -1094,9 +1094,6 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ a, const flo
         constexpr int NREAD_B = TB ? (WT1 >= 4 ? KPL * (WT1 / 4) : (KPL + 1) / 2) : WT1 * (KPL >= 4 ? KPL / 4 : 1);
         constexpr int NREAD = NREAD_A + NREAD_B;
         Frag cur, nxt;
-#ifdef SG_WS_AGPR_HINT
-        { float z = 0.0f; asm volatile("; accumulators may live in AGPRs" : "+a"(z)); acc[0][0][0] += z; }
-#endif
         if (ktiles > 0) {
             wait_at_least(&ready[0], (uint32_t)NLW);
             load_frag(lds, 0, cur);
