@@ -1119,6 +1119,8 @@ IN_PLACE_CASES = [
     ("mt64x64_a16_wg1x4_dk32_s3", None, 2, 1792, 1792, 256, "launch"),            # stream-K
     ("mt256x128_a32_wg2x2_dk16_s3_occ2", "edges", None, 4097, 4096, 64, "launch"),  # edge strips
     ("mt64x64_a16_wg1x4_dk32_s3_tn", None, None, 256, 256, 4096, "launch_noalloc"),
+    ("mt64x64_a16_wg1x4_dk32_s4_ws", None, None, 333, 290, 517, "launch"),        # wave-specialised
+    ("mt64x64_a16_wg1x4_dk32_s3_ks", None, None, 333, 290, 517, "launch_noalloc"),  # in-group K split
 ]
 
 
