@@ -7,8 +7,11 @@ into itself.  These tests feed them what the reference's config boundary
 (toml++ in /root/reference/runner/generator_runner.cpp:85-124) and CLI
 (:192-223) would see at their worst: malformed and hostile .toml files,
 extreme shapes through the shape check and the launch plan, aliasing
-buffers, edge handles closed in every order, and bad command lines.  Any
-sanitizer report fails the test; so does a wrong return code.
+buffers, edge handles closed in every order, and bad command lines.  The
+runner's multithreaded CPU validation GEMMs (runner/cpu_reference.hpp) run
+under ASan + UBSan and under ThreadSanitizer from
+tests/asan/cpu_reference_check.cpp.  Any sanitizer report fails the test; so
+does a wrong return code.
 """
 import os
 import subprocess
@@ -25,7 +28,8 @@ KERNELS = os.path.join(PKG, "kernels")
 SGEMM_E_IO, SGEMM_E_CONFIG = -2, -3
 
 ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:exitcode=99", UBSAN_OPTIONS="print_stacktrace=1:exitcode=98",
-           HIP_VISIBLE_DEVICES="")
+           TSAN_OPTIONS="halt_on_error=1:exitcode=97", HIP_VISIBLE_DEVICES="")
+CPU_REF_CHECK = os.path.join(ROOT, "tests", "asan", "cpu_reference_check.cpp")
 
 VALID = """a_type = 0
 b_type = 0
@@ -187,3 +191,20 @@ def test_runner_cli_under_sanitizers(asan_build, tmp_path):
         rc, out = _run([RUNNER] + args)
         assert rc == 255, (args, out)
         assert needle in out, (args, out)
+
+
+@pytest.mark.parametrize("sanitizer", ["address,undefined", "thread"])
+def test_runner_cpu_reference_under_sanitizers(tmp_path, sanitizer):
+    """The column-split, blocked and float64 loops share each output among
+    threads; they must agree bitwise at every thread count, including more
+    threads than column blocks and empty dimensions, with no report from
+    either sanitizer (ThreadSanitizer would name two threads writing one
+    column)."""
+    exe = str(tmp_path / "cpu_reference_check")
+    ret = subprocess.run(["g++", "-std=c++17", "-ffp-contract=off", "-pthread", "-g", "-O1",
+                          "-fno-omit-frame-pointer", f"-fsanitize={sanitizer}", "-fno-sanitize-recover=all",
+                          "-I", os.path.join(PKG, "runner"), CPU_REF_CHECK, "-o", exe],
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    assert ret.returncode == 0, ret.stdout.decode()[-3000:]
+    rc, out = _run([exe])
+    assert rc == 0 and out.strip().endswith("ok (0 failed checks)"), out
