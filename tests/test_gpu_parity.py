@@ -1153,6 +1153,93 @@ def test_in_place_update_of_c(kernels, name, edges, mode, m, n, k, entry):
     _check(D_in, oracle.cpu_gemm_mt(opA, opB, C, 0.5, -1.5, threads=16), k, name)
 
 
+# NaN and +-Inf in A and B.  Which outputs end up NaN, +Inf or -Inf does not
+# depend on the order of a sum (no finite value here comes near overflow), so
+# those patterns must equal the oracle's exactly; the finite outputs keep the
+# usual bar.  The cases cover every place where the kernel puts zeros in
+# front of the MFMAs instead of operand values -- the head tile of a K
+# remainder, tiles straddling the M and N edges, the element-wise path, the
+# in-group K split's zero head tile -- since a zero multiplied by a planted Inf
+# there would make a NaN the oracle does not have.
+SPECIAL_CASES = [
+    # (instance, edges, split-K ranges, stream-K mode, m, n, k, beta)
+    ("mt64x64_a32_wg2x2_dk16", None, 1, None, 130, 70, 53, 0.75),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", None, 1, None, 300, 200, 100, 0.0),
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2_tt", None, 1, None, 300, 200, 100, 0.75),
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 3, None, 200, 190, 333, 0.75),          # split-K
+    ("mt64x64_a16_wg1x4_dk32_s3", None, 1, 2, 1792, 1792, 77, 0.75),            # stream-K
+    ("mt256x128_a32_wg2x2_dk16_s3_occ2", "edges", 1, None, 4097, 4096, 40, 0.0),  # edge strips
+    ("mt64x64_a16_wg1x4_dk32_s3_ks", None, 1, None, 130, 70, 333, 0.75),        # in-group K split, 11 K tiles
+    ("mt64x64_a16_wg1x4_dk32_s4_ws", None, 1, None, 130, 70, 333, 0.75),        # wave-specialised
+    ("mt16x16_a16_wg1x1_dk16_mapk4", None, 1, None, 40, 30, 70, 0.75),          # element-wise path
+    ("mt128x64_a16_wg2x4_dk64_tn", None, 2, None, 200, 100, 150, 0.75),         # A^T, split-K
+]
+
+
+def _plant_special(opA, opB, seed):
+    """NaN, +Inf and -Inf at seeded places of op(A) and op(B) (in place), plus
+    the corners a tile edge or the K head reaches: A's last row at the last k,
+    B's last column at k = 0, and a 0 in A meeting an Inf in B."""
+    rng = np.random.default_rng(seed)
+    m, k = opA.shape
+    n = opB.shape[1]
+
+    def at(rows, cols):
+        return int(rng.integers(rows)), int(rng.integers(cols))
+
+    opA[at(m, k)] = np.nan
+    opA[at(m, k)] = np.inf
+    opA[at(m, k)] = -np.inf
+    opA[m - 1, k - 1] = np.inf
+    opB[at(k, n)] = np.inf
+    opB[at(k, n)] = -np.inf
+    opB[0, n - 1] = -np.inf
+    kz, jz = at(k, n)
+    opB[kz, jz] = np.inf
+    opA[int(rng.integers(m)), kz] = 0.0
+
+
+@pytest.mark.parametrize("name,edges,splits,mode,m,n,k,beta", SPECIAL_CASES)
+def test_special_values_propagate_as_in_the_oracle(kernels, name, edges, splits, mode, m, n, k, beta):
+    cfg, _ = catalog.SOLUTIONS[name]
+    _, _, opA, opB = _operands(name, m, n, k, 41, S.SGEMM_DIST_NORMAL)
+    opA, opB = np.array(opA, order="F"), np.array(opB, order="F")
+    _plant_special(opA, opB, 41 + m + n + k)
+    A = np.asfortranarray(opA.T) if cfg.trans_a else opA
+    B = np.asfortranarray(opB.T) if cfg.trans_b else opB
+    C = S.fill_matrix(m, n, 41, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (A, B, C))
+    dD = S.DeviceBuffer(4 * m * n)
+    strips = [_kernel(e) for e in catalog.EDGE_KERNEL[name]] if edges else []
+    try:
+        with _kernel(name) as kern:
+            if strips:
+                kern.set_edge_kernels(*strips)
+            if splits != 1:
+                kern.set_split_k(splits)
+            if mode is not None:
+                kern.set_stream_k(mode)
+            plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0,
+                    kern.edge_interior(m, n, k))
+            _say(f"special values {name} {m}x{n}x{k} beta {beta}: splits, stream-K tiles, interior = {plan}")
+            assert plan[0] == splits and (mode is None) == (plan[1] == 0) and (edges is None) == (plan[2] == (m, n))
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=-0.5, beta=beta)
+            kern.synchronize()
+    finally:
+        for e in strips:
+            e.close()
+    D = dD.download().reshape(n, m).T
+    ref = oracle.cpu_gemm_mt(opA, opB, C, -0.5, beta, threads=16)
+    for kind in (np.isnan, np.isposinf, np.isneginf):
+        want, got = kind(ref), kind(D)
+        assert want.any() or kind is np.isnan
+        assert np.array_equal(got, want), \
+            f"{name}: {kind.__name__} at {np.argwhere(got != want)[:4].tolist()} differs from the oracle"
+    finite = np.isfinite(ref)
+    assert finite.mean() > 0.75
+    _check(D[finite], ref[finite], k, name)
+
+
 # ----------------------------------------------------------------- runner
 def _run(cmd, timeout=300):
     _say("+ " + " ".join(cmd))
