@@ -4,8 +4,10 @@
                            [--extra inst1,inst2] --out sweep.json
 
 Every shape is timed over all candidates (``catalog.CANDIDATES`` plus
-``--extra``) round-robin, ``--rounds`` times, and the median launch time is
-kept, so that the clock state is shared by the instances compared on a shape.
+``--extra``) round-robin, ``--rounds`` times, the order reversed every other
+round, and the median launch time is kept, so that the clock state is shared
+by the instances compared on a shape and none always runs first (the first
+timing after another shape's launches can be off by 1-3% either way).
 Each instance launches with its own split-K / stream-K setting (split-K per
 problem where the code object carries the kernel) and without edge kernels:
 what ``predicted_launch_seconds`` models.  Inputs are U[-1, 1), alpha = 1,
@@ -55,8 +57,8 @@ def main() -> int:
         flops = 2.0 * m * n * k
         runs = max(3, min(40, int(1.2e14 / flops)))   # about 1 ms of launches per timing
         times = {c: [] for c in cands}
-        for _ in range(args.rounds):
-            for c in cands:
+        for r in range(args.rounds):
+            for c in (cands if r % 2 == 0 else cands[::-1]):
                 kerns[c].time(dA, dB, None, dD, m, n, k, warmup=2, runs=1)
                 times[c].append(kerns[c].time(dA, dB, None, dD, m, n, k, warmup=0, runs=runs) / runs)
         tf = {c: round(flops / (float(np.median(times[c])) * 1e-3) / 1e12, 1) for c in cands}
