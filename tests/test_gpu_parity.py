@@ -1002,6 +1002,43 @@ def test_random_selected_launches(kernels, m, n, k, mode, alpha, beta):
     _check(D, oracle.cpu_gemm_mt(Af, Bf, Cf, alpha, beta, threads=16), k, name)
 
 
+# Extreme aspect ratios through the default selection path: a single row or
+# column of D, k = 1, one huge K, and grids of thousands of work-groups along
+# one dimension only (the y dimension of the grid included).
+EXTREME_CASES = [
+    (1, 65536, 64, False, False), (65536, 1, 64, False, False), (1, 1, 100000, False, False),
+    (300000, 16, 8, False, False), (16, 300000, 8, False, False), (4096, 4096, 1, False, False),
+    (2, 3, 1, False, False), (7, 40000, 33, True, True), (40000, 7, 33, True, False), (1, 5000, 3000, False, True),
+]
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb", EXTREME_CASES)
+def test_extreme_aspect_ratios_through_select(kernels, m, n, k, ta, tb):
+    name = catalog.select(m, n, k, ta, tb)
+    Af = S.fill_matrix(*((k, m) if ta else (m, k)), 29, 0)
+    Bf = S.fill_matrix(*((n, k) if tb else (k, n)), 29, 1)
+    Cf = S.fill_matrix(m, n, 29, 2)
+    dA, dB, dC = (S.DeviceBuffer.from_array(x) for x in (Af, Bf, Cf))
+    dD = S.DeviceBuffer(m * n * 4)
+    edges = [_kernel(e) for e in catalog.EDGE_KERNEL.get(name, ())]
+    try:
+        with _kernel(name) as kern:
+            if edges:
+                kern.set_edge_kernels(*edges)
+            plan = (kern.launch_splits(m, n, k), kern.stream_k_tiles(m, n, k) if kern.info.stream_k_groups else 0,
+                    kern.edge_interior(m, n, k))
+            _say(f"extreme {name} {m}x{n}x{k} ta {ta} tb {tb}: splits, stream-K tiles, interior = {plan}")
+            kern.launch(dA, dB, dC, dD, m, n, k, alpha=-0.75, beta=0.5)
+            kern.synchronize()
+    finally:
+        for e in edges:
+            e.close()
+    D = dD.download().reshape(n, m).T
+    opA = np.asfortranarray(Af.T) if ta else Af
+    opB = np.asfortranarray(Bf.T) if tb else Bf
+    _check(D, oracle.cpu_gemm_mt(opA, opB, Cf, -0.75, 0.5, threads=16), k, name)
+
+
 def _selected_transposed_cases(count, seed):
     """(m, n, k, trans_a, trans_b, stream-K mode or None, alpha, beta): random
     grids as above in the three transposed layouts, plus the BASELINE shapes'
