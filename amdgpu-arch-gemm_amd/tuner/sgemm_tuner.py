@@ -31,6 +31,10 @@ stdout line) and print the best.  Additions:
   on the shape clipped to 1024 per dimension) is re-emitted as
   ``<out>/generated_gemm.co`` + ``.toml`` (the reference overwrites one
   artifact per point and keeps none, :67, :107);
+* ``--playoff N`` times the N fastest points again, ``--playoff-rounds``
+  times round-robin with the order reversed every other round, and emits by
+  their medians: one timing per point ranks points within 1-2% of each other
+  by noise and by what ran before them;
 * ``--compile-only`` builds every candidate without a GPU; ``--no-compile``
   benchmarks candidates built earlier; ``--in-process`` times them through the
   ctypes shim instead of one runner process per point.
@@ -42,6 +46,7 @@ import hashlib
 import json
 import os
 import shutil
+import statistics
 import subprocess
 import sys
 import time
@@ -422,12 +427,51 @@ class ShimValidator:
         return bool(err <= tol), f"{m}x{n}x{k}: normwise error vs float64 {err:.3e} (tolerance {tol:.3e})"
 
 
+def playoff(recs: List[Dict], out: str, bench, top: int, rounds: int, timeout: float) -> List[Dict]:
+    """Times the ``top`` fastest points again, ``rounds`` times round-robin
+    with the order reversed every other round, and stores each one's median
+    as ``playoff_gflops`` (its timings in ``playoff``).  A single timing per
+    point ranks points within 1-2% of each other by noise and by what ran
+    before them; the median of interleaved timings does not.  Returns the
+    participants, fastest median first."""
+    cands = sorted((r for r in recs if r["status"] == "ok" and r["gflops"] > 0), key=lambda r: -r["gflops"])[:top]
+    if len(cands) < 2 or rounds < 1:
+        return cands
+    for rec in cands:
+        rec["playoff"] = []
+    for r in range(rounds):
+        for rec in (cands if r % 2 == 0 else cands[::-1]):
+            co = os.path.join(point_dir(out), f"{rec['point']}.co")
+            toml = os.path.join(point_dir(out), f"{rec['point']}.toml")
+            try:
+                rc, gflops = bench(co, toml, timeout)
+            except Exception as e:  # a point that fails now drops out of the ranking
+                print(f"playoff: {rec['point']} failed ({e})", flush=True)
+                continue
+            if rc == 0 and gflops > 0:
+                rec["playoff"].append(gflops)
+    for rec in cands:
+        rec["playoff_gflops"] = statistics.median(rec["playoff"]) if rec["playoff"] else 0.0
+        print(f"playoff: {rec['playoff_gflops']:.1f} Gflops median of {len(rec['playoff'])} "
+              f"(single timing {rec['gflops']:.1f}), {rec['point']}", flush=True)
+    return sorted(cands, key=lambda r: -r["playoff_gflops"])
+
+
 def emit_best(out: str, recs: List[Dict], validate=None) -> Optional[Dict]:
     """Copies the fastest point that passes ``validate(co, toml) -> (ok, detail)``
     to <out>/generated_gemm.co + .toml and returns its record (None if no
-    point passes); a point that fails is marked and the next one tried."""
+    point passes); a point that fails is marked and the next one tried.
+    Points that went through ``playoff`` come first, by their median; the
+    others follow by their single timing."""
     src = point_dir(out)
-    for rec in sorted((r for r in recs if r["status"] == "ok" and r["gflops"] > 0), key=lambda r: -r["gflops"]):
+
+    def rank(r):
+        if "playoff_gflops" in r:
+            return (0, -r["playoff_gflops"])
+        return (1, -r["gflops"])
+
+    ok = [r for r in recs if r["status"] == "ok" and r["gflops"] > 0 and r.get("playoff_gflops", 1.0) > 0]
+    for rec in sorted(ok, key=rank):
         co = os.path.join(src, f"{rec['point']}.co")
         toml = os.path.join(src, f"{rec['point']}.toml")
         if validate is not None:
@@ -482,6 +526,9 @@ def main(argv=None):
     ap.add_argument("--stage1-depths", default=",".join(str(d) for d in STAGE1_DEPTHS),
                     help="comma-separated K depths every stage-1 geometry is tried at")
     ap.add_argument("--summary", default=None, help="write a markdown summary of the sweep to this path")
+    ap.add_argument("--playoff", type=int, default=0, metavar="N",
+                    help="time the N fastest points again, interleaved, and emit by median (0: off)")
+    ap.add_argument("--playoff-rounds", type=int, default=6)
     ap.add_argument("--trans-a", action="store_true", help="op(A) = A^T: A stored k x m (lda >= k)")
     ap.add_argument("--trans-b", action="store_true", help="op(B) = B^T: B stored n x k (ldb >= n)")
     args = ap.parse_args(argv)
@@ -546,6 +593,8 @@ def main(argv=None):
     if not ok:
         print("No valid configurations found.")
         return 1
+    if args.playoff > 1:
+        playoff(recs, out, bench, args.playoff, args.playoff_rounds, args.timeout)
     # the emitted pair is checked first: the runner's own CPU validation when
     # the --bench executable exists, else the shim against a float64 GEMM
     validate = RunnerValidator(args.bench, m, n, k) if os.path.isfile(args.bench) else ShimValidator(m, n, k)
@@ -578,7 +627,14 @@ def write_summary(path: str, recs: List[Dict], best: Dict, m: int, n: int, k: in
     for i, r in enumerate(ok[:top], 1):
         lines.append(f"| {i} | `{r['point']}` | {r['tile'][0]}x{r['tile'][1]} | {r['gflops'] / 1e3:.2f} | "
                      f"{r['gflops'] / 1e3 / 157.3 * 100:.1f} |")
-    lines += ["", f"Emitted `generated_gemm.co` + `.toml`: `{best['point']}`, {best['gflops'] / 1e3:.2f} TFLOP/s; "
+    po = sorted((r for r in recs if "playoff_gflops" in r), key=lambda r: -r["playoff_gflops"])
+    if po:
+        lines += ["", f"Playoff ({len(po[0]['playoff'])} interleaved rounds, order reversed every other round):", "",
+                  "| point | single timing TFLOP/s | median TFLOP/s |", "|---|---|---|"]
+        lines += [f"| `{r['point']}` | {r['gflops'] / 1e3:.2f} | {r['playoff_gflops'] / 1e3:.2f} |" for r in po]
+    speed = (f"{best['playoff_gflops'] / 1e3:.2f} TFLOP/s (playoff median)" if "playoff_gflops" in best
+             else f"{best['gflops'] / 1e3:.2f} TFLOP/s")
+    lines += ["", f"Emitted `generated_gemm.co` + `.toml`: `{best['point']}`, {speed}; "
               f"validation {best.get('validation', 'not run')}.", ""]
     os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
     with open(path, "w") as f:

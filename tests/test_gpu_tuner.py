@@ -85,6 +85,34 @@ def test_small_sweep_emits_a_validated_drop_in_pair(kernels, tmp_path):
     assert len(open(os.path.join(out, "results.jsonl")).read().splitlines()) == len(recs)
 
 
+def test_playoff_emits_the_best_interleaved_median(kernels, tmp_path):
+    """--playoff: the three fastest points are timed again, round-robin in
+    alternating order, and the emitted pair is the best median among them."""
+    out = str(tmp_path / "tune_po")
+    c = graft.TUNER_CHECK
+    summary = str(tmp_path / "summary.md")
+    cmd = [sys.executable, TUNER, "--m", str(c["m"]), "--n", str(c["n"]), "--k", str(c["k"]), "--bench", RUNNER,
+           "--output-folder", out, "--points-dir", graft.TUNER_CHECK_POINTS, "--in-process", "--refine", "0",
+           "--tiles", c["tiles"], "--occ", c["occ"], "--stage1-depths", c["depths"], "--warmup", "3", "--runs", "10",
+           "--jobs", "16", "--timeout", "60", "--playoff", "3", "--playoff-rounds", "4", "--summary", summary]
+    _say("+ " + " ".join(cmd))
+    ret = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=600)
+    log = ret.stdout.decode(errors="replace")
+    _say(log[-3000:])
+    assert ret.returncode == 0, log
+    medians = {}
+    for line in log.splitlines():
+        if line.startswith("playoff: ") and "Gflops median of 4" in line:
+            medians[line.rsplit(", ", 1)[1]] = float(line.split()[1])
+    assert len(medians) == 3 and all(v > 1000.0 for v in medians.values()), medians
+    best = max(medians, key=medians.get)
+    assert f"validation of {best}: PASS" in log
+    co = os.path.join(out, "generated_gemm.co")
+    assert open(co, "rb").read() == open(os.path.join(graft.TUNER_CHECK_POINTS, best + ".co"), "rb").read()
+    text = open(summary).read()
+    assert "Playoff (4 interleaved rounds" in text and f"`{best}`" in text and "(playoff median)" in text
+
+
 def test_transposed_sweep_emits_a_validated_tt_pair(kernels, tmp_path):
     """The same sweep for op(A) = A^T, op(B) = B^T (--trans-a --trans-b): the
     emitted pair is a TT kernel, and it validates in this build's runner and

@@ -235,3 +235,42 @@ def test_stage2_k_split_points():
     odd = GemmSolutionConfig(0, 0, 0, 0, MFMA_16x16x4, (2, 2), (1, 2), 32, False, False, vmem_stage=2)
     assert not [o for _, o in T.knob_points(odd, kss=(1,)) if o.ksplit]
 
+
+
+def test_playoff_reranks_by_interleaved_medians(tmp_path, monkeypatch):
+    """The playoff re-times the leaders round-robin, the order reversed every
+    other round, and emission follows the medians: a point whose single
+    timing was lucky loses to one that is faster every time it is re-timed."""
+    out = str(tmp_path)
+    monkeypatch.setattr(T, "POINTS_DIR", None)
+    pts = [T.make_point((32, 32, 1, 2), (2, 2), wt, 16, 2, 4, 3, 1, 0, 8) for wt in ((1, 1), (2, 2), (4, 4), (2, 1))]
+    keys = [T.point_key(*p) for p in pts]
+    _fake_points(out, pts)
+    compiled = {kk: 0 for kk in keys}
+    single = {keys[0]: 1100.0, keys[1]: 1000.0, keys[2]: 990.0, keys[3]: 500.0}   # keys[0]'s first timing was lucky
+    steady = {keys[0]: 900.0, keys[1]: 980.0, keys[2]: 995.0, keys[3]: 500.0}
+    order = []
+
+    def bench(co, toml, timeout):
+        kk = os.path.basename(co)[:-3]
+        order.append(kk)
+        if len(order) <= len(keys):
+            return 0, single[kk]
+        if kk == keys[2] and len(order) == len(keys) + 3:
+            return 0, 1.0       # its first re-timing is bad: the median ignores it
+        return 0, steady[kk]
+
+    recs = T.sweep(pts, out, 256, 256, 64, bench, 10.0, os.path.join(out, "results.jsonl"), compiled)
+    ranked = T.playoff(recs, out, bench, 3, 4, 10.0)
+    played = order[len(keys):]
+    assert played == [keys[0], keys[1], keys[2], keys[2], keys[1], keys[0]] * 2   # ABC CBA ABC CBA
+    assert [r["point"] for r in ranked] == [keys[2], keys[1], keys[0]]
+    assert ranked[0]["playoff"] == [1.0, 995.0, 995.0, 995.0] and ranked[0]["playoff_gflops"] == 995.0
+    best = T.emit_best(out, recs, lambda co, toml: (True, "ok"))
+    assert best["point"] == keys[2]
+    # a participant that fails validation hands over to the next median, not to a single timing
+    best = T.emit_best(out, recs, lambda co, toml: (os.path.basename(co)[:-3] != keys[2], "x"))
+    assert best["point"] == keys[1]
+    T.write_summary(os.path.join(out, "s.md"), recs, best, 256, 256, 64, ["--playoff", "3"])
+    text = open(os.path.join(out, "s.md")).read()
+    assert "Playoff (4 interleaved rounds" in text and "(playoff median)" in text
