@@ -160,11 +160,14 @@ SOLUTIONS: Dict[str, Tuple[GemmSolutionConfig, GemmOptimizations]] = {
 
 # shape class -> preferred instance (filled from tuner results; see select())
 PREFERRED: List[Tuple[Tuple[int, int, int], str]] = [
-    # two 256 x 128 work-groups per CU: each hides the other's prologue and
-    # epilogue (interleaved runs at 4096^3: 152.0 / 151.9 TFLOP/s against
-    # 150.9 / 151.0 for the 256 x 256 depth-24 instance, which held this row
-    # before)
-    ((4096, 4096, 4096), "mt256x128_a32_wg2x2_dk16_s3_occ2"),
+    # one 256 x 256 work-group of eight waves per CU (two per SIMD hide each
+    # other's waits): as fast as two four-wave 256 x 128 work-groups per CU
+    # (151.47 against 151.55 TFLOP/s over 30 rounds in alternating order;
+    # 139.7 against 138.7 as three fresh processes each under bench.py's
+    # 5-launch warm-up) with 22% less HBM traffic: each A and B panel is read
+    # by half as many tiles (470 MB per launch, 2.33x the algorithmic bytes,
+    # against 605 MB)
+    ((4096, 4096, 4096), "mt256x256_a32_wg4x2_dk16_s3"),
     ((1024, 1024, 1024), "mt64x64_a16_wg1x4_dk32_s3"),
     # eight 64 x 64 waves, two work-groups per CU: 135.9 / 136.0 TFLOP/s in
     # bench.py against 134.3 / 134.4 for the four-wave 256 x 128 plr=2 instance
@@ -272,7 +275,8 @@ STREAM_K_GROUPS_PER_CU: Dict[str, int] = {
     "mt128x64_a16_wg2x4_dk64": 1,
 }
 
-# Transposed twins of the time model's candidates: the same geometry and
+# Transposed twins of the time model's candidates and of the BASELINE
+# shapes' preferred instances: the same geometry and
 # knobs with trans_a / trans_b, named <candidate>_tn / _nt / _tt, for
 # select(..., trans_a, trans_b).  The transposed tiles keep each operand's
 # contiguous dimension and run at the NN speed (4096^3 on 256 x 256: NN, TN,
@@ -297,7 +301,7 @@ def _add_twins() -> None:
         for (ta, tb), suffix in LAYOUT_SUFFIX.items():
             SOLUTIONS[name + suffix] = (_cfg(cfg.mfma, cfg.wave_group, cfg.wave_tiling, cfg.depth_k,
                                              stages=cfg.vmem_stage, ta=ta, tb=tb), copy.copy(opt))
-    for name in CANDIDATES:
+    for name in list(CANDIDATES) + [nm for _, nm in PREFERRED if nm not in CANDIDATES]:
         cfg, opt = SOLUTIONS[name]
         resident = min(MAX_LDS_NUM_BYTES // cfg.lds_usage_bytes, RESIDENT_PER_CU.get(name, MAX_LDS_NUM_BYTES))
         for (ta, tb), suffix in LAYOUT_SUFFIX.items():

@@ -1084,12 +1084,13 @@ def build_kernel(output_folder: str, config: GemmSolutionConfig, opt: GemmOptimi
     return os.path.join(output_folder, f"{kern_name}.co"), os.path.join(output_folder, f"{kern_name}.toml")
 
 
-# Default instance of the CLI: the configuration the gfx950 tuner selected for
-# the 4096^3 headline problem (in the layout trans_a / trans_b ask for).
+# Default instance of the CLI: the catalog's instance for the 4096^3 headline
+# problem, one 256 x 256 work-group of eight waves per CU (in the layout
+# trans_a / trans_b ask for).
 def default_config(trans_a: bool = False, trans_b: bool = False) -> Tuple[GemmSolutionConfig, GemmOptimizations]:
     cfg = GemmSolutionConfig(DataType.FP32, DataType.FP32, DataType.FP32, DataType.FP32,
-                             MFMA_32x32x2, (2, 2), (4, 2), 16, trans_a, trans_b, vmem_stage=2)
-    opt = GemmOptimizations(1, wgm=4, plr=3, gw=1, map_k_idx=0, xcd=8, occ=2)
+                             MFMA_32x32x2, (4, 2), (2, 4), 16, trans_a, trans_b, vmem_stage=2)
+    opt = GemmOptimizations(1, wgm=8, plr=3, gw=1, map_k_idx=0, xcd=8)
     return cfg, opt
 
 

@@ -469,8 +469,10 @@ def test_cli_writes_a_transposed_pair(tmp_path):
 # 16384 x 128 x 4096: the model books the 64 x 64 instance's two work-groups
 # per CU at its full rate and picks it; measured, it runs 131.6 TFLOP/s there
 # against 137.9 for the eight-wave 128 x 64 instance the table holds (same
-# sweep, tests/golden/select_measured.json)
-MODEL_OVERRIDDEN = {(16384, 128, 4096)}
+# sweep, tests/golden/select_measured.json).  4096^3: the table holds the
+# eight-wave 256 x 256 instance, which is no candidate of the model; it ties the
+# model's 256 x 128 pick in speed and moves 22% fewer HBM bytes
+MODEL_OVERRIDDEN = {(16384, 128, 4096), (4096, 4096, 4096)}
 
 
 def test_select_prefers_tuned_and_divisible():
@@ -534,7 +536,9 @@ def test_transposed_twins_and_select():
     occ2 = catalog.SOLUTIONS["mt256x128_a32_wg2x2_dk16_s3_occ2_tn"][0]
     assert occ2.lds_a_row_swizzle[1] > 0 and occ2.lds_pad_bytes[0] == 0
     assert occ2.lds_usage_bytes == catalog.SOLUTIONS["mt256x128_a32_wg2x2_dk16_s3_occ2"][0].lds_usage_bytes
-    assert catalog.select(4096, 4096, 4096, False, False) == "mt256x128_a32_wg2x2_dk16_s3_occ2"
+    assert catalog.select(4096, 4096, 4096, False, False) == "mt256x256_a32_wg4x2_dk16_s3"
+    # one element either way leaves the exact BASELINE shape: the time model picks
+    assert catalog.select(4097, 4097, 4097) == catalog.select(4095, 4095, 4095) == "mt256x128_a32_wg2x2_dk16_s3_occ2"
     with pytest.raises(RuntimeError):
         catalog.select(16, 0, 16, True, False)
 
